@@ -1,0 +1,99 @@
+// Internal helpers shared by the libparoquant_hip.so translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/paroquant_hip.h"
+
+namespace pq {
+
+// Records the message returned by pq_last_error() (thread-local).
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
+inline bool aligned_to(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+inline int dtype_size(int dt) {
+  switch (dt) {
+    case PQ_F32: return 4;
+    case PQ_F16: return 2;
+    case PQ_BF16: return 2;
+    default: return 0;
+  }
+}
+
+// Checks hipGetLastError() after a launch.
+int launch_status(const char* what);
+
+}  // namespace pq
+
+#define PQ_REQUIRE(cond, code, ...)       \
+  do {                                    \
+    if (!(cond)) {                        \
+      ::pq::set_error(__VA_ARGS__);       \
+      return (code);                      \
+    }                                     \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Device-side scalar conversions (gfx950 has native f16 and bf16 converts).
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float pq_bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even float -> bfloat16 bits (NaN stays NaN).
+__device__ __forceinline__ uint16_t pq_f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float pq_f16_to_f32(uint16_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, h);
+  return static_cast<float>(v);
+}
+
+// Round-to-nearest-even float -> fp16 bits.
+__device__ __forceinline__ uint16_t pq_f32_to_f16(float f) {
+  _Float16 v = static_cast<_Float16>(f);
+  return __builtin_bit_cast(uint16_t, v);
+}
+
+__device__ __forceinline__ float pq_round_f16(float f) { return pq_f16_to_f32(pq_f32_to_f16(f)); }
+
+template <int DT>
+__device__ __forceinline__ float pq_load_as_f32(const void* p, int64_t i) {
+  if constexpr (DT == PQ_F32) return static_cast<const float*>(p)[i];
+  else if constexpr (DT == PQ_F16) return pq_f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  else return pq_bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+template <int DT>
+__device__ __forceinline__ void pq_store_from_f32(void* p, int64_t i, float v) {
+  if constexpr (DT == PQ_F32) static_cast<float*>(p)[i] = v;
+  else if constexpr (DT == PQ_F16) static_cast<uint16_t*>(p)[i] = pq_f32_to_f16(v);
+  else static_cast<uint16_t*>(p)[i] = pq_f32_to_bf16(v);
+}
+
+__device__ __forceinline__ float pq_load_dyn(const void* p, int dt, int64_t i) {
+  if (dt == PQ_F32) return static_cast<const float*>(p)[i];
+  if (dt == PQ_F16) return pq_f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  return pq_bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+__device__ __forceinline__ void pq_store_dyn(void* p, int dt, int64_t i, float v) {
+  if (dt == PQ_F32) static_cast<float*>(p)[i] = v;
+  else if (dt == PQ_F16) static_cast<uint16_t*>(p)[i] = pq_f32_to_f16(v);
+  else static_cast<uint16_t*>(p)[i] = pq_f32_to_bf16(v);
+}
+
+// Wave64 max-reduction through cross-lane swizzles (result in every lane).
+__device__ __forceinline__ float pq_wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}

@@ -1,0 +1,484 @@
+// Stage 3 of the W4A8 linear on gfx950: int4-weight x int8-activation GEMM
+// with per-(128-group, column) fp16 scales and uint4 zero points, int32
+// accumulation per group on the int8 MFMA units and an fp32 epilogue:
+//
+//   P[m, g, n] = sum_{k in g} (q[k, n] - z[g, n]) * xq[m, k]        (int32)
+//   y[m, n]    = xscale[m] * sum_g s[g, n] * P[m, g, n] (+ bias[n])
+//
+// Reference: the Marlin W4A8 GEMM reached through apply_awq_marlin_linear
+// (src/alpamayo_r1/utils/quantization/paroquant_marlin_w4a8.py:314-333) with
+// AWQ weight semantics (dequant_awq, 227-235).
+//
+// Weights use the layout written by pq_w4a8_prepack (pq_prepack.hip):
+//   wpack [N/16][G][64 slots][16 B]: slot 16j + c = column 16*tile + c,
+//     codes k = 128g + 32j + [0, 32); each dword holds 8 consecutive k,
+//     low nibbles the first four, high nibbles the next four;
+//   wmeta [N/16][G][16] uint32: fp16 scale bits | zero << 16.
+//
+// Unpacking: a dword of 8 codes becomes two dwords of 4 signed bytes
+// (q - z) by  ((w & 0x0f0f0f0f) + (0x80808080 - z*0x01010101)) ^ 0x80808080
+// -- every byte stays in [113, 143] before the xor, so no carry crosses a
+// byte, and the xor maps 128 + d to the two's complement of d.
+//
+// Two kernels:
+//   gemm_skinny  M <= 16: each wave streams 1 KB weight blocks (one 16-column
+//                tile x one 128-group) with 16-byte loads, two
+//                v_mfma_i32_16x16x64_i8 per block (activation rows padded to
+//                16), waves of a workgroup split K, workgroups optionally
+//                split K further with a deterministic last-arriving-block
+//                reduction through the workspace.
+//   gemm_tiled   M > 16: 128x128 output tiles, A (int8) and B (int4) staged
+//                through LDS one group at a time with the next group
+//                prefetched into registers, 2x2 waves of 64x64, each
+//                2x2 v_mfma_i32_32x32x32_i8 tiles per 32-deep K step.
+#include "pq_common.h"
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+namespace {
+
+__device__ __forceinline__ uint32_t zero_bias(uint32_t z) { return 0x80808080u - z * 0x01010101u; }
+
+__device__ __forceinline__ int unpack_lo(uint32_t w, uint32_t zb) {
+  return static_cast<int>(((w & 0x0f0f0f0fu) + zb) ^ 0x80808080u);
+}
+__device__ __forceinline__ int unpack_hi(uint32_t w, uint32_t zb) {
+  return static_cast<int>((((w >> 4) & 0x0f0f0f0fu) + zb) ^ 0x80808080u);
+}
+
+// 8 bytes of codes (16 k) -> 16 signed bytes in k order.
+__device__ __forceinline__ v4i unpack16(uint32_t w0, uint32_t w1, uint32_t zb) {
+  v4i r;
+  r.x = unpack_lo(w0, zb);
+  r.y = unpack_hi(w0, zb);
+  r.z = unpack_lo(w1, zb);
+  r.w = unpack_hi(w1, zb);
+  return r;
+}
+
+__device__ __forceinline__ float epilogue(float acc, float xscale, const void* bias, int bias_dtype, int n) {
+  float v = acc * xscale;
+  if (bias != nullptr) v = v + pq_load_dyn(bias, bias_dtype, n);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Decode-size GEMM (M <= 16)
+// ---------------------------------------------------------------------------
+template <int NT, int U, bool PARTIALS>
+__global__ __launch_bounds__(256) void gemm_skinny(
+    const int8_t* __restrict__ xq, const float* __restrict__ xs, const uint8_t* __restrict__ wpack,
+    const uint32_t* __restrict__ wmeta, const void* __restrict__ bias, int bias_dtype, void* __restrict__ y,
+    int y_dtype, uint32_t* __restrict__ counters, float* __restrict__ wsp, int32_t* __restrict__ partials, int M,
+    int N, int K, int splits, int gps) {
+  __shared__ float red[4][NT][4][64];
+  __shared__ int is_last;
+  const int G = K >> 7;
+  const int ntg = (N >> 4) / NT;
+  const int tg = blockIdx.x % ntg;
+  const int split = blockIdx.x / ntg;
+  const int g_begin = split * gps;
+  const int g_end = min(G, g_begin + gps);
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15;
+  const int j = lane >> 4;
+  const bool arow = c < M;
+  const int8_t* ap = xq + static_cast<int64_t>(c) * K + j * 32;
+  const int tile0 = tg * NT;
+
+  float acc[NT][4];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[nt][v] = 0.0f;
+
+  for (int g0 = g_begin + wave; g0 < g_end; g0 += 4 * U) {
+    v4i wb[U][NT];
+    uint32_t wm[U][NT];
+    v4i a0[U], a1[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int g = g0 + 4 * u;
+      if (g < g_end) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const int64_t blk = static_cast<int64_t>(tile0 + nt) * G + g;
+          wb[u][nt] = *reinterpret_cast<const v4i*>(wpack + blk * 1024 + lane * 16);
+          wm[u][nt] = wmeta[blk * 16 + c];
+        }
+        if (arow) {
+          a0[u] = *reinterpret_cast<const v4i*>(ap + static_cast<int64_t>(g) * 128);
+          a1[u] = *reinterpret_cast<const v4i*>(ap + static_cast<int64_t>(g) * 128 + 16);
+        } else {
+          a0[u] = v4i{0, 0, 0, 0};
+          a1[u] = v4i{0, 0, 0, 0};
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int g = g0 + 4 * u;
+      if (g < g_end) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const uint32_t meta = wm[u][nt];
+          const uint32_t zb = zero_bias((meta >> 16) & 0xfu);
+          const v4i w = wb[u][nt];
+          const v4i b0 = unpack16(static_cast<uint32_t>(w.x), static_cast<uint32_t>(w.y), zb);
+          const v4i b1 = unpack16(static_cast<uint32_t>(w.z), static_cast<uint32_t>(w.w), zb);
+          v4i p = {0, 0, 0, 0};
+          p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[u], b0, p, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[u], b1, p, 0, 0, 0);
+          if constexpr (PARTIALS) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const int m = 4 * j + v;
+              if (m < M) partials[(static_cast<int64_t>(m) * G + g) * N + (tile0 + nt) * 16 + c] = p[v];
+            }
+          } else {
+            const float sc = pq_f16_to_f32(static_cast<uint16_t>(meta & 0xffffu));
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[nt][v] = fmaf(static_cast<float>(p[v]), sc, acc[nt][v]);
+          }
+        }
+      }
+    }
+  }
+  if constexpr (PARTIALS) return;
+
+  // Sum the four waves' K slices (fixed order).
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[wave][nt][v][lane] = acc[nt][v];
+  __syncthreads();
+  const int rl = threadIdx.x & 63;
+  const int rv = threadIdx.x >> 6;
+  const int m = 4 * (rl >> 4) + rv;
+  const int cc = rl & 15;
+  float sum[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+    sum[nt] = ((red[0][nt][rv][rl] + red[1][nt][rv][rl]) + red[2][nt][rv][rl]) + red[3][nt][rv][rl];
+
+  if (splits == 1) {
+    if (m < M) {
+      const float xsm = xs[m];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int n = (tile0 + nt) * 16 + cc;
+        pq_store_dyn(y, y_dtype, static_cast<int64_t>(m) * N + n, epilogue(sum[nt], xsm, bias, bias_dtype, n));
+      }
+    }
+    return;
+  }
+
+  // Split-K: publish this block's partial, the last block of the tile group
+  // reduces all of them in split order and re-arms the counter.
+  if (m < M) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int n = (tile0 + nt) * 16 + cc;
+      wsp[(static_cast<int64_t>(split) * M + m) * N + n] = sum[nt];
+    }
+  }
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = atomicAdd(&counters[tg], 1u);
+    is_last = (prev == static_cast<uint32_t>(splits - 1));
+  }
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+  if (m < M) {
+    const float xsm = xs[m];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int n = (tile0 + nt) * 16 + cc;
+      float tot = 0.0f;
+      for (int s = 0; s < splits; ++s) tot += wsp[(static_cast<int64_t>(s) * M + m) * N + n];
+      pq_store_dyn(y, y_dtype, static_cast<int64_t>(m) * N + n, epilogue(tot, xsm, bias, bias_dtype, n));
+    }
+  }
+  if (threadIdx.x == 0) counters[tg] = 0u;
+}
+
+// ---------------------------------------------------------------------------
+// Prefill-size GEMM (M > 16)
+// ---------------------------------------------------------------------------
+constexpr int kBM = 128;
+constexpr int kBN = 128;
+constexpr int kAPad = 144;  // LDS row stride of the A tile (bytes)
+
+template <bool PARTIALS>
+__global__ __launch_bounds__(256) void gemm_tiled(const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                                  const uint8_t* __restrict__ wpack,
+                                                  const uint32_t* __restrict__ wmeta, const void* __restrict__ bias,
+                                                  int bias_dtype, void* __restrict__ y, int y_dtype,
+                                                  int32_t* __restrict__ partials, int M, int N, int K) {
+  __shared__ __attribute__((aligned(16))) int8_t As[kBM * kAPad];
+  __shared__ __attribute__((aligned(16))) uint8_t Bs[8 * 1024];
+  __shared__ uint32_t Ms[8 * 16];
+
+  const int G = K >> 7;
+  const int ntiles16 = N >> 4;
+  const int nbn = (N + kBN - 1) / kBN;
+  const int bm = blockIdx.x / nbn;
+  const int bn = blockIdx.x % nbn;
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  const int r32 = lane & 31;
+  const int hj = lane >> 5;
+
+  // Global -> register mapping of one group's tiles.
+  const int a_row = t >> 1;
+  const int a_half = t & 1;
+  const int64_t a_grow = static_cast<int64_t>(bm) * kBM + a_row;
+  const bool a_ok = a_grow < M;
+  const int8_t* a_src = xq + (a_ok ? a_grow : 0) * K + a_half * 64;
+  const int b_tile = t >> 5;
+  const int b_off = (t & 31) * 32;
+  const int b_gtile = bn * 8 + b_tile;
+  const bool b_ok = b_gtile < ntiles16;
+  const uint8_t* b_src = wpack + static_cast<int64_t>(b_ok ? b_gtile : 0) * G * 1024 + b_off;
+  const int m_gtile = bn * 8 + (t >> 4);
+  const bool m_ok = t < 128 && m_gtile < ntiles16;
+  const uint32_t* m_src = wmeta + static_cast<int64_t>(m_ok ? m_gtile : 0) * G * 16 + (t & 15);
+
+  v4i ra[4];
+  v4i rb[2];
+  uint32_t rm = 0;
+  auto gload = [&](int g) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      ra[q] = a_ok ? *reinterpret_cast<const v4i*>(a_src + static_cast<int64_t>(g) * 128 + q * 16) : v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      rb[q] = b_ok ? *reinterpret_cast<const v4i*>(b_src + static_cast<int64_t>(g) * 1024 + q * 16) : v4i{0, 0, 0, 0};
+    rm = m_ok ? m_src[static_cast<int64_t>(g) * 16] : 0u;
+  };
+
+  float acc[2][2][16];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.0f;
+
+  int bt[2], bc[2];
+#pragma unroll
+  for (int ni = 0; ni < 2; ++ni) {
+    const int nl = wn * 64 + ni * 32 + r32;
+    bt[ni] = nl >> 4;
+    bc[ni] = nl & 15;
+  }
+
+  gload(0);
+  for (int g = 0; g < G; ++g) {
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) *reinterpret_cast<v4i*>(As + a_row * kAPad + a_half * 64 + q * 16) = ra[q];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) *reinterpret_cast<v4i*>(Bs + b_tile * 1024 + b_off + q * 16) = rb[q];
+    if (t < 128) Ms[t] = rm;
+    __syncthreads();
+    if (g + 1 < G) gload(g + 1);
+
+    uint32_t zb[2];
+    float sc[2];
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      const uint32_t meta = Ms[bt[ni] * 16 + bc[ni]];
+      zb[ni] = zero_bias((meta >> 16) & 0xfu);
+      sc[ni] = pq_f16_to_f32(static_cast<uint16_t>(meta & 0xffffu));
+    }
+    v16i T[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) T[mi][ni] = v16i{};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v4i a[2], b[2];
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+        a[mi] = *reinterpret_cast<const v4i*>(As + (wm * 64 + mi * 32 + r32) * kAPad + hj * 64 + i * 16);
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) {
+        const uint2 w =
+            *reinterpret_cast<const uint2*>(Bs + bt[ni] * 1024 + ((2 * hj + (i >> 1)) * 16 + bc[ni]) * 16 + (i & 1) * 8);
+        b[ni] = unpack16(w.x, w.y, zb[ni]);
+      }
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+          T[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[mi], b[ni], T[mi][ni], 0, 0, 0);
+    }
+    if constexpr (PARTIALS) {
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int64_t m = static_cast<int64_t>(bm) * kBM + wm * 64 + mi * 32 + 8 * (v >> 2) + 4 * hj + (v & 3);
+            const int n = bn * kBN + wn * 64 + ni * 32 + r32;
+            if (m < M && n < N) partials[(m * G + g) * N + n] = T[mi][ni][v];
+          }
+    } else {
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            acc[mi][ni][v] = fmaf(static_cast<float>(T[mi][ni][v]), sc[ni], acc[mi][ni][v]);
+    }
+  }
+  if constexpr (PARTIALS) return;
+
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t m = static_cast<int64_t>(bm) * kBM + wm * 64 + mi * 32 + 8 * (v >> 2) + 4 * hj + (v & 3);
+      if (m >= M) continue;
+      const float xsm = xs[m];
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) {
+        const int n = bn * kBN + wn * 64 + ni * 32 + r32;
+        if (n < N) pq_store_dyn(y, y_dtype, m * N + n, epilogue(acc[mi][ni][v], xsm, bias, bias_dtype, n));
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side configuration
+// ---------------------------------------------------------------------------
+constexpr int kSkinnyMaxM = 16;
+constexpr int kSkinnyU = 4;
+constexpr size_t kCounterBytes = 4096;  // counters live in the first 4 KB of the workspace
+
+struct SkinnyCfg {
+  int nt;
+  int splits;
+  int gps;
+};
+
+SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k) {
+  const int G = static_cast<int>(k / 128);
+  const int tiles = static_cast<int>(n / 16);
+  const int nt = (m > 4 && tiles % 2 == 0) ? 2 : 1;
+  const int wg0 = tiles / nt;
+  int splits = 1;
+  while (static_cast<int64_t>(wg0) * splits < 512 && G / (splits * 2) >= 4) splits *= 2;
+  const int gps = (G + splits - 1) / splits;
+  splits = (G + gps - 1) / gps;
+  return {nt, splits, gps};
+}
+
+size_t skinny_ws_bytes(int64_t m, int64_t n, int64_t k) {
+  const SkinnyCfg cfg = choose_skinny(m, n, k);
+  if (cfg.splits <= 1) return 0;
+  return kCounterBytes + static_cast<size_t>(cfg.splits) * m * n * sizeof(float);
+}
+
+int check_gemm_args(const char* who, int64_t m, int64_t n, int64_t k, int group_size) {
+  PQ_REQUIRE(group_size == 128, PQ_ERR_UNSUPPORTED, "%s: group_size=%d (only 128 is supported)", who, group_size);
+  PQ_REQUIRE(m >= 0 && m <= 0x7fffffffLL, PQ_ERR_ARG, "%s: m=%lld", who, (long long)m);
+  PQ_REQUIRE(n > 0 && n % 16 == 0 && n <= (1 << 20), PQ_ERR_ARG, "%s: n=%lld must be a positive multiple of 16", who,
+             (long long)n);
+  PQ_REQUIRE(k > 0 && k % 128 == 0 && k <= (1 << 20), PQ_ERR_ARG, "%s: k=%lld must be a positive multiple of 128",
+             who, (long long)k);
+  return PQ_OK;
+}
+
+template <int NT, bool PARTIALS>
+void launch_skinny(const SkinnyCfg& cfg, const int8_t* xq, const float* xs, const uint8_t* wpack,
+                   const uint32_t* wmeta, const void* bias, int bias_dtype, void* y, int y_dtype, void* ws,
+                   int32_t* partials, int M, int N, int K, hipStream_t stream) {
+  const int ntg = (N / 16) / NT;
+  const unsigned grid = static_cast<unsigned>(ntg * cfg.splits);
+  uint32_t* counters = static_cast<uint32_t*>(ws);
+  float* wsp = ws ? reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes) : nullptr;
+  gemm_skinny<NT, kSkinnyU, PARTIALS><<<grid, 256, 0, stream>>>(xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype,
+                                                                 counters, wsp, partials, M, N, K, cfg.splits,
+                                                                 cfg.gps);
+}
+
+}  // namespace
+
+extern "C" size_t pq_w4a8_workspace_size(int64_t m, int64_t n, int64_t k, int group_size) {
+  if (group_size != 128 || m <= 0 || n <= 0 || k <= 0 || n % 16 || k % 128) return 0;
+  if (m > kSkinnyMaxM) return 0;
+  return skinny_ws_bytes(m, n, k);
+}
+
+extern "C" int pq_w4a8_gemm(const int8_t* xq, const float* xscale, const uint8_t* wpack, const uint32_t* wmeta,
+                            const void* bias, int bias_dtype, void* y, int y_dtype, int64_t m, int64_t n,
+                            int64_t k, int group_size, void* workspace, size_t workspace_bytes, void* stream) {
+  int st = check_gemm_args("pq_w4a8_gemm", m, n, k, group_size);
+  if (st != PQ_OK) return st;
+  PQ_REQUIRE(y_dtype == PQ_F32 || y_dtype == PQ_F16 || y_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED,
+             "pq_w4a8_gemm: y dtype code %d", y_dtype);
+  PQ_REQUIRE(bias == nullptr || bias_dtype == PQ_F32 || bias_dtype == PQ_F16 || bias_dtype == PQ_BF16,
+             PQ_ERR_UNSUPPORTED, "pq_w4a8_gemm: bias dtype code %d", bias_dtype);
+  if (m == 0) return PQ_OK;
+  PQ_REQUIRE(xq && xscale && wpack && wmeta && y, PQ_ERR_ARG, "pq_w4a8_gemm: null pointer");
+  PQ_REQUIRE(pq::aligned_to(xq, 16) && pq::aligned_to(wpack, 16) && pq::aligned_to(wmeta, 4) &&
+                 pq::aligned_to(y, pq::dtype_size(y_dtype)),
+             PQ_ERR_ARG, "pq_w4a8_gemm: xq and wpack must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int M = static_cast<int>(m), N = static_cast<int>(n), K = static_cast<int>(k);
+  if (m <= kSkinnyMaxM) {
+    const SkinnyCfg cfg = choose_skinny(m, n, k);
+    if (cfg.splits > 1) {
+      const size_t need = skinny_ws_bytes(m, n, k);
+      PQ_REQUIRE(workspace != nullptr && workspace_bytes >= need, PQ_ERR_WORKSPACE,
+                 "pq_w4a8_gemm: workspace of %zu bytes needed for m=%lld n=%lld k=%lld, got %zu", need, (long long)m,
+                 (long long)n, (long long)k, workspace ? workspace_bytes : (size_t)0);
+      PQ_REQUIRE(pq::aligned_to(workspace, 16), PQ_ERR_ARG, "pq_w4a8_gemm: workspace must be 16-byte aligned");
+    }
+    if (cfg.nt == 2)
+      launch_skinny<2, false>(cfg, xq, xscale, wpack, wmeta, bias, bias_dtype, y, y_dtype, workspace, nullptr, M, N, K, s);
+    else
+      launch_skinny<1, false>(cfg, xq, xscale, wpack, wmeta, bias, bias_dtype, y, y_dtype, workspace, nullptr, M, N, K, s);
+  } else {
+    const unsigned grid = static_cast<unsigned>(((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN));
+    gemm_tiled<false><<<grid, 256, 0, s>>>(xq, xscale, wpack, wmeta, bias, bias_dtype, y, y_dtype, nullptr, M, N, K);
+  }
+  return pq::launch_status("pq_w4a8_gemm launch");
+}
+
+extern "C" int pq_w4a8_gemm_partials(const int8_t* xq, const uint8_t* wpack, const uint32_t* wmeta,
+                                     int32_t* partials, int64_t m, int64_t n, int64_t k, int group_size,
+                                     void* stream) {
+  int st = check_gemm_args("pq_w4a8_gemm_partials", m, n, k, group_size);
+  if (st != PQ_OK) return st;
+  if (m == 0) return PQ_OK;
+  PQ_REQUIRE(xq && wpack && wmeta && partials, PQ_ERR_ARG, "pq_w4a8_gemm_partials: null pointer");
+  PQ_REQUIRE(pq::aligned_to(xq, 16) && pq::aligned_to(wpack, 16) && pq::aligned_to(wmeta, 4) &&
+                 pq::aligned_to(partials, 4),
+             PQ_ERR_ARG, "pq_w4a8_gemm_partials: misaligned pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int M = static_cast<int>(m), N = static_cast<int>(n), K = static_cast<int>(k);
+  if (m <= kSkinnyMaxM) {
+    SkinnyCfg cfg = choose_skinny(m, n, k);
+    if (cfg.nt == 2)
+      launch_skinny<2, true>(cfg, xq, nullptr, wpack, wmeta, nullptr, 0, nullptr, 0, nullptr, partials, M, N, K, s);
+    else
+      launch_skinny<1, true>(cfg, xq, nullptr, wpack, wmeta, nullptr, 0, nullptr, 0, nullptr, partials, M, N, K, s);
+  } else {
+    const unsigned grid = static_cast<unsigned>(((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN));
+    gemm_tiled<true><<<grid, 256, 0, s>>>(xq, nullptr, wpack, wmeta, nullptr, 0, nullptr, 0, partials, M, N, K);
+  }
+  return pq::launch_status("pq_w4a8_gemm_partials launch");
+}

@@ -1,0 +1,366 @@
+// Stage 1 and 2 of the W4A8 linear on gfx950:
+//   pq_rotate           -- the rotation::rotate op (pairwise Givens + channel scale)
+//   pq_rotate_quant_i8  -- rotation + per-token absmax + int8 quant, one pass
+//   pq_quant_i8         -- per-token int8 quant of an existing tensor
+//
+// Reference semantics: kernels/paroquant_kernels/src/rotation.cuh:247-337
+// (scale-multiply, KROT Givens layers xi' = c xi + s xj, xj' = -s xi + c xj
+// on group-local pair indices, fp32 math, result rounded to the storage
+// dtype) and vLLM's dynamic per-token int8 quant (scale = absmax/127,
+// q = rne(x * 127/absmax)) as called at
+// src/alpamayo_r1/utils/quantization/paroquant_marlin_w4a8.py:319-333.
+//
+// All updates are written with explicit fmaf and the file is compiled with
+// -ffp-contract=off, so the float32 sequence is fixed:
+//   xi' = fma(xi, c, xj*s),  xj' = fma(xj, c, -(xi*s)).
+#include "pq_common.h"
+
+namespace {
+
+constexpr int kRotRows = 4;  // rows per workgroup of the plain rotation kernel
+
+// ---------------------------------------------------------------------------
+// rotation::rotate.  One wave per (4 rows x 128 channels); lane t owns pair t
+// of the chunk (for group 64 the chunk holds two groups).  The 4 x 128 fp32
+// tile lives in LDS; pairs are read per layer and masked to the group so a
+// bad index can never address outside the tile.
+// ---------------------------------------------------------------------------
+template <int DT, int G, bool SCALE>
+__global__ __launch_bounds__(64) void rotate_kernel(const void* __restrict__ x, void* __restrict__ y,
+                                                    const int16_t* __restrict__ idx,
+                                                    const void* __restrict__ theta,
+                                                    const void* __restrict__ scales, int64_t rows,
+                                                    int h, int krot) {
+  __shared__ float tile[kRotRows][128];
+  const int t = threadIdx.x;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kRotRows;
+  const int ch0 = blockIdx.y * 128;
+
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    const int local = t + 64 * half;
+    const int ch = ch0 + local;
+    float s = 1.0f;
+    if (SCALE && ch < h) s = pq_load_as_f32<DT>(scales, ch);
+#pragma unroll
+    for (int r = 0; r < kRotRows; ++r) {
+      const int64_t row = row0 + r;
+      float v = 0.0f;
+      if (row < rows && ch < h) v = pq_load_as_f32<DT>(x, row * h + ch) * s;
+      tile[r][local] = v;
+    }
+  }
+
+  const int P = blockIdx.y * 64 + t;  // pair index within the row; theta column
+  const bool active = P < (h >> 1);
+  const int gi = P / (G / 2);
+  const int pp = P % (G / 2);
+  const int base = gi * G - ch0;  // group start inside the 128-channel tile
+  __syncthreads();
+
+  for (int r = 0; r < krot; ++r) {
+    if (active) {
+      const int64_t o = static_cast<int64_t>(r) * h + gi * G + 2 * pp;
+      const int i = base + (idx[o] & (G - 1));
+      const int j = base + (idx[o + 1] & (G - 1));
+      const float th = pq_load_as_f32<DT>(theta, static_cast<int64_t>(r) * (h >> 1) + P);
+      float sn, cs;
+      sincosf(th, &sn, &cs);
+#pragma unroll
+      for (int rr = 0; rr < kRotRows; ++rr) {
+        const float xi = tile[rr][i];
+        const float xj = tile[rr][j];
+        tile[rr][i] = fmaf(xi, cs, xj * sn);
+        tile[rr][j] = fmaf(xj, cs, -(xi * sn));
+      }
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    const int local = t + 64 * half;
+    const int ch = ch0 + local;
+#pragma unroll
+    for (int r = 0; r < kRotRows; ++r) {
+      const int64_t row = row0 + r;
+      if (row < rows && ch < h) pq_store_from_f32<DT>(y, row * h + ch, tile[r][local]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fused rotate + quant.  One workgroup per row (grid-stride over rows).  The
+// scaled row is staged in LDS as fp32 (h*4 bytes); wave w rotates groups
+// w, w+NW, ...: lane t owns pair t of the group in every layer, and since a
+// group is touched by one wave only, layers need no workgroup barrier (LDS
+// operations of one wave execute in order).  The last layer's outputs are
+// already in registers, so the fp16 rounding and the absmax happen there.
+// ---------------------------------------------------------------------------
+template <int NT>
+__device__ __forceinline__ float block_max(float v, float* red) {
+  constexpr int NW = NT / 64;
+  v = pq_wave_max(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float m = red[0];
+#pragma unroll
+  for (int k = 1; k < NW; ++k) m = fmaxf(m, red[k]);
+  return m;
+}
+
+__device__ __forceinline__ uint32_t quant4(float a, float b, float c, float d, float inv) {
+  auto q = [inv](float v) -> uint32_t {
+    float r = __builtin_rintf(v * inv);
+    r = fminf(fmaxf(r, -128.0f), 127.0f);
+    return static_cast<uint32_t>(static_cast<int>(r)) & 0xffu;
+  };
+  return q(a) | (q(b) << 8) | (q(c) << 16) | (q(d) << 24);
+}
+
+template <int DT>
+__device__ __forceinline__ void load8(const void* base, int64_t elem, float f[8]) {
+  if constexpr (DT == PQ_F32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + elem);
+    const float4 a = p[0], b = p[1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  } else {
+    const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + elem);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t lo = static_cast<uint16_t>(w[e] & 0xffffu), hi = static_cast<uint16_t>(w[e] >> 16);
+      if constexpr (DT == PQ_F16) {
+        f[2 * e] = pq_f16_to_f32(lo);
+        f[2 * e + 1] = pq_f16_to_f32(hi);
+      } else {
+        f[2 * e] = pq_bf16_to_f32(lo);
+        f[2 * e + 1] = pq_bf16_to_f32(hi);
+      }
+    }
+  }
+}
+
+template <int DT, int NT>
+__global__ __launch_bounds__(NT) void rotate_quant_kernel(
+    const void* __restrict__ x, const uint8_t* __restrict__ pairs, const float2* __restrict__ cs,
+    const float* __restrict__ scales, int8_t* __restrict__ xq, float* __restrict__ xscale,
+    uint16_t* __restrict__ xrot, int64_t rows, int h, int krot, unsigned flags) {
+  extern __shared__ float buf[];
+  __shared__ float red[NT / 64];
+  constexpr int NW = NT / 64;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int w = t >> 6;
+  const bool in16 = (flags & PQ_RQ_INPUT_FP16) != 0;
+  const bool mat16 = (flags & PQ_RQ_MATERIALIZE_FP16) != 0;
+  const int ngroups = h >> 7;
+  const int half_h = h >> 1;
+
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const int64_t rbase = row * h;
+    for (int v = t; v < (h >> 3); v += NT) {
+      float f[8];
+      load8<DT>(x, rbase + 8 * v, f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float val = in16 ? pq_round_f16(f[e]) : f[e];
+        if (scales != nullptr) val = val * scales[8 * v + e];
+        buf[8 * v + e] = val;
+      }
+    }
+    __syncthreads();
+
+    float amax = 0.0f;
+    for (int g = w; g < ngroups; g += NW) {
+      float* gb = buf + g * 128;
+      float ni = 0.0f, nj = 0.0f;
+      int i = 0, j = 0;
+      for (int r = 0; r < krot; ++r) {
+        const uint16_t pr =
+            *reinterpret_cast<const uint16_t*>(pairs + static_cast<int64_t>(r) * h + g * 128 + 2 * lane);
+        const float2 c = cs[static_cast<int64_t>(r) * half_h + g * 64 + lane];
+        i = pr & 127;
+        j = (pr >> 8) & 127;
+        const float xi = gb[i];
+        const float xj = gb[j];
+        ni = fmaf(xi, c.x, xj * c.y);
+        nj = fmaf(xj, c.x, -(xi * c.y));
+        gb[i] = ni;
+        gb[j] = nj;
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      }
+      if (mat16) {
+        ni = pq_round_f16(ni);
+        nj = pq_round_f16(nj);
+        gb[i] = ni;
+        gb[j] = nj;
+      }
+      amax = fmaxf(amax, fmaxf(fabsf(ni), fabsf(nj)));
+    }
+    __syncthreads();  // every group's final values are in LDS
+
+    const float am = block_max<NT>(amax, red);
+    const float inv = am > 0.0f ? 127.0f / am : 0.0f;
+    if (t == 0) xscale[row] = am / 127.0f;
+
+    for (int v = t; v < (h >> 2); v += NT) {
+      const float4 f = *reinterpret_cast<const float4*>(buf + 4 * v);
+      *reinterpret_cast<uint32_t*>(xq + rbase + 4 * v) = quant4(f.x, f.y, f.z, f.w, inv);
+      if (xrot != nullptr) {
+        uint2 o;
+        o.x = pq_f32_to_f16(f.x) | (static_cast<uint32_t>(pq_f32_to_f16(f.y)) << 16);
+        o.y = pq_f32_to_f16(f.z) | (static_cast<uint32_t>(pq_f32_to_f16(f.w)) << 16);
+        *reinterpret_cast<uint2*>(xrot + rbase + 4 * v) = o;
+      }
+    }
+    __syncthreads();  // buf and red are reused by the next row
+  }
+}
+
+// Per-token quant of an existing activation: absmax pass, then quant pass.
+template <int DT, int NT>
+__global__ __launch_bounds__(NT) void quant_kernel(const void* __restrict__ x, int8_t* __restrict__ xq,
+                                                   float* __restrict__ xscale, int64_t rows, int h) {
+  __shared__ float red[NT / 64];
+  const int t = threadIdx.x;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const int64_t rbase = row * h;
+    float amax = 0.0f;
+    for (int v = t; v < (h >> 3); v += NT) {
+      float f[8];
+      load8<DT>(x, rbase + 8 * v, f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
+    }
+    const float am = block_max<NT>(amax, red);
+    const float inv = am > 0.0f ? 127.0f / am : 0.0f;
+    if (t == 0) xscale[row] = am / 127.0f;
+    for (int v = t; v < (h >> 3); v += NT) {
+      float f[8];
+      load8<DT>(x, rbase + 8 * v, f);
+      uint2 o;
+      o.x = quant4(f[0], f[1], f[2], f[3], inv);
+      o.y = quant4(f[4], f[5], f[6], f[7], inv);
+      *reinterpret_cast<uint2*>(xq + rbase + 8 * v) = o;
+    }
+    __syncthreads();
+  }
+}
+
+template <int DT, int G, bool SCALE>
+void launch_rotate(const void* x, void* y, const int16_t* idx, const void* theta, const void* scales,
+                   int64_t rows, int h, int krot, hipStream_t stream) {
+  dim3 grid(static_cast<unsigned>((rows + kRotRows - 1) / kRotRows), static_cast<unsigned>((h + 127) / 128));
+  rotate_kernel<DT, G, SCALE><<<grid, 64, 0, stream>>>(x, y, idx, theta, scales, rows, h, krot);
+}
+
+template <int DT>
+void launch_rotate_dt(const void* x, void* y, const int16_t* idx, const void* theta, const void* scales,
+                      int64_t rows, int h, int krot, int group, hipStream_t stream) {
+  if (group == 128) {
+    if (scales) launch_rotate<DT, 128, true>(x, y, idx, theta, scales, rows, h, krot, stream);
+    else launch_rotate<DT, 128, false>(x, y, idx, theta, scales, rows, h, krot, stream);
+  } else {
+    if (scales) launch_rotate<DT, 64, true>(x, y, idx, theta, scales, rows, h, krot, stream);
+    else launch_rotate<DT, 64, false>(x, y, idx, theta, scales, rows, h, krot, stream);
+  }
+}
+
+constexpr int64_t kMaxGrid = 1 << 20;
+
+template <int DT>
+void launch_rotate_quant(const void* x, const uint8_t* pairs, const float* cs, const float* scales, int8_t* xq,
+                         float* xscale, void* xrot, int64_t rows, int h, int krot, unsigned flags,
+                         hipStream_t stream) {
+  const size_t lds = static_cast<size_t>(h) * sizeof(float);
+  const unsigned grid = static_cast<unsigned>(rows < kMaxGrid ? rows : kMaxGrid);
+  const float2* cs2 = reinterpret_cast<const float2*>(cs);
+  uint16_t* xr = static_cast<uint16_t*>(xrot);
+  if (rows <= 64) {
+    rotate_quant_kernel<DT, 1024><<<grid, 1024, lds, stream>>>(x, pairs, cs2, scales, xq, xscale, xr, rows, h, krot,
+                                                               flags);
+  } else {
+    rotate_quant_kernel<DT, 256><<<grid, 256, lds, stream>>>(x, pairs, cs2, scales, xq, xscale, xr, rows, h, krot,
+                                                             flags);
+  }
+}
+
+template <int DT>
+void launch_quant(const void* x, int8_t* xq, float* xscale, int64_t rows, int h, hipStream_t stream) {
+  const unsigned grid = static_cast<unsigned>(rows < kMaxGrid ? rows : kMaxGrid);
+  quant_kernel<DT, 256><<<grid, 256, 0, stream>>>(x, xq, xscale, rows, h);
+}
+
+}  // namespace
+
+extern "C" int pq_rotate(const void* x, void* y, const int16_t* idx_ij, const void* theta, const void* scales,
+                         int64_t rows, int64_t h, int krot, int group_size, int dtype, void* stream) {
+  PQ_REQUIRE(rows >= 0 && h > 0, PQ_ERR_ARG, "pq_rotate: rows=%lld h=%lld", (long long)rows, (long long)h);
+  PQ_REQUIRE(group_size == 64 || group_size == 128, PQ_ERR_UNSUPPORTED,
+             "pq_rotate: Unexpected group_size: %d (supported: 64, 128)", group_size);
+  PQ_REQUIRE(krot == 1 || krot == 2 || krot == 4 || krot == 8 || krot == 16, PQ_ERR_UNSUPPORTED,
+             "pq_rotate: Unsupported KROT = %d; compiled variants: 1/2/4/8/16", krot);
+  PQ_REQUIRE(h % group_size == 0, PQ_ERR_ARG, "pq_rotate: h must be divisible by GROUP_SIZE (h=%lld, G=%d)",
+             (long long)h, group_size);
+  PQ_REQUIRE(h <= (1 << 24), PQ_ERR_ARG, "pq_rotate: h=%lld too large", (long long)h);
+  PQ_REQUIRE(dtype == PQ_F32 || dtype == PQ_F16 || dtype == PQ_BF16, PQ_ERR_UNSUPPORTED,
+             "pq_rotate: rotate only supports Float, Half, and BFloat16 (dtype code %d)", dtype);
+  if (rows == 0) return PQ_OK;
+  PQ_REQUIRE(x && y && idx_ij && theta, PQ_ERR_ARG, "pq_rotate: null pointer");
+  PQ_REQUIRE((rows + kRotRows - 1) / kRotRows <= 0x7fffffffLL, PQ_ERR_ARG, "pq_rotate: too many rows");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int hh = static_cast<int>(h);
+  switch (dtype) {
+    case PQ_F32: launch_rotate_dt<PQ_F32>(x, y, idx_ij, theta, scales, rows, hh, krot, group_size, s); break;
+    case PQ_F16: launch_rotate_dt<PQ_F16>(x, y, idx_ij, theta, scales, rows, hh, krot, group_size, s); break;
+    default: launch_rotate_dt<PQ_BF16>(x, y, idx_ij, theta, scales, rows, hh, krot, group_size, s); break;
+  }
+  return pq::launch_status("pq_rotate launch");
+}
+
+extern "C" int pq_rotate_quant_i8(const void* x, int x_dtype, const uint8_t* pairs, const float* cos_sin,
+                                  const float* scales, int8_t* xq, float* xscale, void* xrot, int64_t rows,
+                                  int64_t h, int krot, unsigned flags, void* stream) {
+  PQ_REQUIRE(rows >= 0 && h > 0 && h % 128 == 0 && h <= 16384, PQ_ERR_ARG,
+             "pq_rotate_quant_i8: need h %% 128 == 0 and 0 < h <= 16384 (h=%lld)", (long long)h);
+  PQ_REQUIRE(krot >= 1 && krot <= 16, PQ_ERR_UNSUPPORTED, "pq_rotate_quant_i8: krot=%d not in 1..16", krot);
+  PQ_REQUIRE(x_dtype == PQ_F32 || x_dtype == PQ_F16 || x_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED,
+             "pq_rotate_quant_i8: dtype code %d", x_dtype);
+  PQ_REQUIRE((flags & ~(PQ_RQ_INPUT_FP16 | PQ_RQ_MATERIALIZE_FP16)) == 0, PQ_ERR_ARG,
+             "pq_rotate_quant_i8: unknown flags 0x%x", flags);
+  if (rows == 0) return PQ_OK;
+  PQ_REQUIRE(x && pairs && cos_sin && xq && xscale, PQ_ERR_ARG, "pq_rotate_quant_i8: null pointer");
+  PQ_REQUIRE(pq::aligned_to(x, 16) && pq::aligned_to(xq, 4) && pq::aligned_to(cos_sin, 8) &&
+                 (xrot == nullptr || pq::aligned_to(xrot, 8)),
+             PQ_ERR_ARG, "pq_rotate_quant_i8: x must be 16-byte, cos_sin 8-byte, xq 4-byte, xrot 8-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int hh = static_cast<int>(h);
+  switch (x_dtype) {
+    case PQ_F32: launch_rotate_quant<PQ_F32>(x, pairs, cos_sin, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
+    case PQ_F16: launch_rotate_quant<PQ_F16>(x, pairs, cos_sin, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
+    default: launch_rotate_quant<PQ_BF16>(x, pairs, cos_sin, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
+  }
+  return pq::launch_status("pq_rotate_quant_i8 launch");
+}
+
+extern "C" int pq_quant_i8(const void* x, int x_dtype, int8_t* xq, float* xscale, int64_t rows, int64_t h,
+                           void* stream) {
+  PQ_REQUIRE(rows >= 0 && h > 0 && h % 8 == 0 && h <= (1 << 24), PQ_ERR_ARG,
+             "pq_quant_i8: need h %% 8 == 0 (h=%lld)", (long long)h);
+  PQ_REQUIRE(x_dtype == PQ_F32 || x_dtype == PQ_F16 || x_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED,
+             "pq_quant_i8: dtype code %d", x_dtype);
+  if (rows == 0) return PQ_OK;
+  PQ_REQUIRE(x && xq && xscale, PQ_ERR_ARG, "pq_quant_i8: null pointer");
+  PQ_REQUIRE(pq::aligned_to(x, 16) && pq::aligned_to(xq, 8), PQ_ERR_ARG,
+             "pq_quant_i8: x must be 16-byte and xq 8-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int hh = static_cast<int>(h);
+  switch (x_dtype) {
+    case PQ_F32: launch_quant<PQ_F32>(x, xq, xscale, rows, hh, s); break;
+    case PQ_F16: launch_quant<PQ_F16>(x, xq, xscale, rows, hh, s); break;
+    default: launch_quant<PQ_BF16>(x, xq, xscale, rows, hh, s); break;
+  }
+  return pq::launch_status("pq_quant_i8 launch");
+}

@@ -1,0 +1,371 @@
+"""torch custom ops over libparoquant_hip.so.
+
+``torch.ops.rotation.rotate`` has the reference's exact schema
+(kernels/paroquant_kernels/src/rotation.cu:576-579); the other ops live in
+the ``paroquant`` namespace:
+
+  rotation::rotate(x, idx_ij, theta, scales?, group_size) -> y
+  paroquant::rotate_quant_i8(x, pairs, cos_sin, scales?, input_fp16, materialize_fp16) -> (xq, xscale)
+  paroquant::rotate_quant_i8_rot(...)                 -> (xq, xscale, xrot fp16)
+  paroquant::quant_i8(x) -> (xq, xscale)
+  paroquant::w4a8_gemm(xq, xscale, wpack, wmeta, bias?, workspace?, out_dtype) -> y
+  paroquant::w4a8_gemm_partials(xq, wpack, wmeta) -> int32 [m, k/128, n]
+  paroquant::w4a8_prepack(awq_qweight, awq_scales, awq_qzeros) -> (wpack, wmeta)
+  paroquant::w4a8_linear(x, pairs, cos_sin, scales?, wpack, wmeta, bias?, workspace?,
+                         input_fp16, materialize_fp16, out_dtype) -> y
+
+Implementations are registered for the CUDA (HIP) dispatch key only, like the
+reference (rotation.cu:581-584); CPU tensors raise from the dispatcher.  Each
+op has a fake (meta) kernel so torch.compile and graph capture can trace it.
+Every op allocates its outputs with torch on the input's device and enqueues
+its kernels on the current stream; none synchronises.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_DT = {torch.float32: _lib.PQ_F32, torch.float16: _lib.PQ_F16, torch.bfloat16: _lib.PQ_BF16}
+
+_rotation_lib = torch.library.Library("rotation", "DEF")
+_rotation_lib.define("rotate(Tensor x, Tensor idx_ij, Tensor theta, Tensor? scales, int group_size) -> Tensor")
+
+_pq_lib = torch.library.Library("paroquant", "DEF")
+_pq_lib.define("rotate_quant_i8(Tensor x, Tensor pairs, Tensor cos_sin, Tensor? scales, bool input_fp16, "
+               "bool materialize_fp16) -> (Tensor, Tensor)")
+_pq_lib.define("rotate_quant_i8_rot(Tensor x, Tensor pairs, Tensor cos_sin, Tensor? scales, bool input_fp16, "
+               "bool materialize_fp16) -> (Tensor, Tensor, Tensor)")
+_pq_lib.define("quant_i8(Tensor x) -> (Tensor, Tensor)")
+_pq_lib.define("w4a8_gemm(Tensor xq, Tensor xscale, Tensor wpack, Tensor wmeta, Tensor? bias, Tensor? workspace, "
+               "ScalarType out_dtype) -> Tensor")
+_pq_lib.define("w4a8_gemm_partials(Tensor xq, Tensor wpack, Tensor wmeta) -> Tensor")
+_pq_lib.define("w4a8_prepack(Tensor awq_qweight, Tensor awq_scales, Tensor awq_qzeros) -> (Tensor, Tensor)")
+_pq_lib.define("w4a8_linear(Tensor x, Tensor pairs, Tensor cos_sin, Tensor? scales, Tensor wpack, Tensor wmeta, "
+               "Tensor? bias, Tensor? workspace, bool input_fp16, bool materialize_fp16, ScalarType out_dtype) "
+               "-> Tensor")
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+class _DeviceGuard:
+    """Makes `dev` current for the duration of a call when it is not already."""
+
+    __slots__ = ("dev", "prev")
+
+    def __init__(self, dev: torch.device):
+        self.dev = dev
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if self.dev.index is not None and self.dev.index != cur:
+            self.prev = cur
+            torch.cuda.set_device(self.dev)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _same_device(name: str, t: torch.Tensor, dev: torch.device) -> None:
+    _require(t.device == dev, f"{name}: expected a tensor on {dev}, got {t.device}")
+
+
+def gemm_dims(wpack: torch.Tensor) -> tuple[int, int]:
+    """(out_features, in_features) of a prepacked weight [N/16, K/128, 64, 16]."""
+    _require(wpack.dim() == 4 and wpack.size(2) == 64 and wpack.size(3) == 16 and wpack.dtype == torch.uint8,
+             "wpack must be uint8 [N/16, K/128, 64, 16]")
+    return wpack.size(0) * 16, wpack.size(1) * 128
+
+
+def workspace_bytes(m: int, n: int, k: int) -> int:
+    return int(_lib.load().pq_w4a8_workspace_size(m, n, k, 128))
+
+
+# ---------------------------------------------------------------------------
+# rotation::rotate
+# ---------------------------------------------------------------------------
+
+def _rotate_impl(x, idx_ij, theta, scales, group_size):
+    _require(x.dtype in _DT, f"rotate only supports Float, Half, and BFloat16, but got {x.dtype}")
+    _require(idx_ij.dtype == torch.int16, f"idx_ij must be int16, got {idx_ij.dtype}")
+    _require(theta.dtype == x.dtype, f"theta must have x's dtype {x.dtype}, got {theta.dtype}")
+    _require(x.dim() >= 1 and x.size(-1) > 0, "x must have a non-empty last dimension")
+    h = x.size(-1)
+    _require(idx_ij.dim() == 2 and theta.dim() == 2, "idx_ij and theta must be 2-D [KROT, H] / [KROT, H/2]")
+    krot = theta.size(0)
+    _require(krot == idx_ij.size(0), "theta.size(0) must equal idx_ij.size(0)")
+    _require(idx_ij.size(1) == h and theta.size(1) * 2 == h,
+             f"idx_ij must be [KROT, {h}] and theta [KROT, {h // 2}], got {tuple(idx_ij.shape)} / {tuple(theta.shape)}")
+    has_scale = scales is not None and scales.numel() > 0
+    if has_scale:
+        _require(scales.dtype == x.dtype, f"scales must have x's dtype {x.dtype}, got {scales.dtype}")
+        _require(scales.numel() == h, f"scales must hold {h} values, got {scales.numel()}")
+    dev = x.device
+    for nm, t in (("idx_ij", idx_ij), ("theta", theta)) + ((("scales", scales),) if has_scale else ()):
+        _same_device(nm, t, dev)
+    xc = x.contiguous()
+    out = torch.empty_like(xc)
+    rows = xc.numel() // h
+    idc, thc = idx_ij.contiguous(), theta.contiguous()
+    scc = scales.contiguous() if has_scale else None
+    lib = _lib.load()
+    with _DeviceGuard(dev):
+        st = lib.pq_rotate(xc.data_ptr(), out.data_ptr(), idc.data_ptr(), thc.data_ptr(),
+                           scc.data_ptr() if has_scale else None, rows, h, krot, int(group_size), _DT[x.dtype],
+                           _stream(dev))
+    _lib.check(st, "rotation::rotate")
+    return out
+
+
+_rotation_lib.impl("rotate", _rotate_impl, "CUDA")
+
+
+@torch.library.register_fake("rotation::rotate")
+def _rotate_fake(x, idx_ij, theta, scales, group_size):
+    return torch.empty_like(x)
+
+
+# ---------------------------------------------------------------------------
+# paroquant::rotate_quant_i8 / rotate_quant_i8_rot / quant_i8
+# ---------------------------------------------------------------------------
+
+def _check_rot_params(x, pairs, cos_sin, scales):
+    h = x.size(-1)
+    _require(x.dtype in _DT, f"x must be float32/float16/bfloat16, got {x.dtype}")
+    _require(h % 128 == 0 and 0 < h <= 16384, f"in_features={h} must be a multiple of 128 and <= 16384")
+    _require(pairs.dtype == torch.uint8 and pairs.dim() == 2 and pairs.size(1) == h,
+             f"pairs must be uint8 [KROT, {h}], got {pairs.dtype} {tuple(pairs.shape)}")
+    krot = pairs.size(0)
+    _require(1 <= krot <= 16, f"KROT={krot} must be in 1..16")
+    _require(cos_sin.dtype == torch.float32 and tuple(cos_sin.shape) == (krot, h // 2, 2),
+             f"cos_sin must be float32 [{krot}, {h // 2}, 2], got {cos_sin.dtype} {tuple(cos_sin.shape)}")
+    if scales is not None:
+        _require(scales.dtype == torch.float32 and scales.numel() == h,
+                 f"scales must be float32 with {h} values, got {scales.dtype} {scales.numel()}")
+    dev = x.device
+    _same_device("pairs", pairs, dev)
+    _same_device("cos_sin", cos_sin, dev)
+    if scales is not None:
+        _same_device("scales", scales, dev)
+    return h, krot
+
+
+def _rotate_quant(x, pairs, cos_sin, scales, input_fp16, materialize_fp16, want_rot):
+    h, krot = _check_rot_params(x, pairs, cos_sin, scales)
+    dev = x.device
+    xc = x.contiguous()
+    rows = xc.numel() // h
+    xq = torch.empty((rows, h), dtype=torch.int8, device=dev)
+    xs = torch.empty((rows,), dtype=torch.float32, device=dev)
+    xr = torch.empty((rows, h), dtype=torch.float16, device=dev) if want_rot else None
+    flags = (_lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0) | (_lib.PQ_RQ_MATERIALIZE_FP16 if materialize_fp16 else 0)
+    pc, cc = pairs.contiguous(), cos_sin.contiguous()
+    sc = scales.contiguous() if scales is not None else None
+    lib = _lib.load()
+    with _DeviceGuard(dev):
+        st = lib.pq_rotate_quant_i8(xc.data_ptr(), _DT[x.dtype], pc.data_ptr(), cc.data_ptr(),
+                                    sc.data_ptr() if sc is not None else None, xq.data_ptr(), xs.data_ptr(),
+                                    xr.data_ptr() if xr is not None else None, rows, h, krot, flags, _stream(dev))
+    _lib.check(st, "paroquant::rotate_quant_i8")
+    return xq, xs, xr
+
+
+def _rotate_quant_impl(x, pairs, cos_sin, scales, input_fp16, materialize_fp16):
+    xq, xs, _ = _rotate_quant(x, pairs, cos_sin, scales, input_fp16, materialize_fp16, False)
+    return xq, xs
+
+
+def _rotate_quant_rot_impl(x, pairs, cos_sin, scales, input_fp16, materialize_fp16):
+    return _rotate_quant(x, pairs, cos_sin, scales, input_fp16, materialize_fp16, True)
+
+
+_pq_lib.impl("rotate_quant_i8", _rotate_quant_impl, "CUDA")
+_pq_lib.impl("rotate_quant_i8_rot", _rotate_quant_rot_impl, "CUDA")
+
+
+@torch.library.register_fake("paroquant::rotate_quant_i8")
+def _rotate_quant_fake(x, pairs, cos_sin, scales, input_fp16, materialize_fp16):
+    h = x.size(-1)
+    rows = x.numel() // h
+    return (x.new_empty((rows, h), dtype=torch.int8), x.new_empty((rows,), dtype=torch.float32))
+
+
+@torch.library.register_fake("paroquant::rotate_quant_i8_rot")
+def _rotate_quant_rot_fake(x, pairs, cos_sin, scales, input_fp16, materialize_fp16):
+    h = x.size(-1)
+    rows = x.numel() // h
+    return (x.new_empty((rows, h), dtype=torch.int8), x.new_empty((rows,), dtype=torch.float32),
+            x.new_empty((rows, h), dtype=torch.float16))
+
+
+def _quant_impl(x):
+    _require(x.dtype in _DT, f"x must be float32/float16/bfloat16, got {x.dtype}")
+    h = x.size(-1)
+    _require(h % 8 == 0 and h > 0, f"last dimension {h} must be a positive multiple of 8")
+    dev = x.device
+    xc = x.contiguous()
+    rows = xc.numel() // h
+    xq = torch.empty((rows, h), dtype=torch.int8, device=dev)
+    xs = torch.empty((rows,), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    with _DeviceGuard(dev):
+        st = lib.pq_quant_i8(xc.data_ptr(), _DT[x.dtype], xq.data_ptr(), xs.data_ptr(), rows, h, _stream(dev))
+    _lib.check(st, "paroquant::quant_i8")
+    return xq, xs
+
+
+_pq_lib.impl("quant_i8", _quant_impl, "CUDA")
+
+
+@torch.library.register_fake("paroquant::quant_i8")
+def _quant_fake(x):
+    h = x.size(-1)
+    rows = x.numel() // h
+    return x.new_empty((rows, h), dtype=torch.int8), x.new_empty((rows,), dtype=torch.float32)
+
+
+# ---------------------------------------------------------------------------
+# paroquant::w4a8_gemm / w4a8_gemm_partials / w4a8_prepack / w4a8_linear
+# ---------------------------------------------------------------------------
+
+def _check_weights(wpack, wmeta, dev):
+    n, k = gemm_dims(wpack)
+    _require(wmeta.dtype in (torch.int32, torch.uint32) and tuple(wmeta.shape) == (n // 16, k // 128, 16),
+             f"wmeta must be int32 [{n // 16}, {k // 128}, 16], got {wmeta.dtype} {tuple(wmeta.shape)}")
+    _require(wpack.is_contiguous() and wmeta.is_contiguous(), "wpack/wmeta must be contiguous")
+    _same_device("wpack", wpack, dev)
+    _same_device("wmeta", wmeta, dev)
+    return n, k
+
+
+def _gemm_launch(xq, xs, wpack, wmeta, bias, workspace, out_dtype, m, n, k, dev):
+    _require(out_dtype in _DT, f"out_dtype must be float32/float16/bfloat16, got {out_dtype}")
+    y = torch.empty((m, n), dtype=out_dtype, device=dev)
+    if bias is not None:
+        _require(bias.dtype in _DT and bias.numel() == n, f"bias must hold {n} float values")
+        _same_device("bias", bias, dev)
+        bias = bias.contiguous()
+    need = workspace_bytes(m, n, k)
+    ws_ptr, ws_bytes = None, 0
+    if need > 0:
+        if workspace is None:
+            workspace = torch.zeros(need, dtype=torch.uint8, device=dev)
+        _same_device("workspace", workspace, dev)
+        _require(workspace.is_contiguous(), "workspace must be contiguous")
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    lib = _lib.load()
+    with _DeviceGuard(dev):
+        st = lib.pq_w4a8_gemm(xq.data_ptr(), xs.data_ptr(), wpack.data_ptr(), wmeta.data_ptr(),
+                              bias.data_ptr() if bias is not None else None,
+                              _DT[bias.dtype] if bias is not None else 0, y.data_ptr(), _DT[out_dtype], m, n, k, 128,
+                              ws_ptr, ws_bytes, _stream(dev))
+    _lib.check(st, "paroquant::w4a8_gemm")
+    return y
+
+
+def _gemm_impl(xq, xscale, wpack, wmeta, bias, workspace, out_dtype):
+    dev = xq.device
+    n, k = _check_weights(wpack, wmeta, dev)
+    _require(xq.dtype == torch.int8 and xq.dim() == 2 and xq.size(1) == k,
+             f"xq must be int8 [M, {k}], got {xq.dtype} {tuple(xq.shape)}")
+    m = xq.size(0)
+    _require(xscale.dtype == torch.float32 and xscale.numel() == m, f"xscale must be float32 [{m}]")
+    _same_device("xscale", xscale, dev)
+    return _gemm_launch(xq.contiguous(), xscale.contiguous(), wpack, wmeta, bias, workspace, out_dtype, m, n, k, dev)
+
+
+_pq_lib.impl("w4a8_gemm", _gemm_impl, "CUDA")
+
+
+@torch.library.register_fake("paroquant::w4a8_gemm")
+def _gemm_fake(xq, xscale, wpack, wmeta, bias, workspace, out_dtype):
+    return xq.new_empty((xq.size(0), wpack.size(0) * 16), dtype=out_dtype)
+
+
+def _partials_impl(xq, wpack, wmeta):
+    dev = xq.device
+    n, k = _check_weights(wpack, wmeta, dev)
+    _require(xq.dtype == torch.int8 and xq.dim() == 2 and xq.size(1) == k, f"xq must be int8 [M, {k}]")
+    m = xq.size(0)
+    out = torch.empty((m, k // 128, n), dtype=torch.int32, device=dev)
+    xc = xq.contiguous()
+    lib = _lib.load()
+    with _DeviceGuard(dev):
+        st = lib.pq_w4a8_gemm_partials(xc.data_ptr(), wpack.data_ptr(), wmeta.data_ptr(), out.data_ptr(), m, n, k,
+                                       128, _stream(dev))
+    _lib.check(st, "paroquant::w4a8_gemm_partials")
+    return out
+
+
+_pq_lib.impl("w4a8_gemm_partials", _partials_impl, "CUDA")
+
+
+@torch.library.register_fake("paroquant::w4a8_gemm_partials")
+def _partials_fake(xq, wpack, wmeta):
+    return xq.new_empty((xq.size(0), wpack.size(1), wpack.size(0) * 16), dtype=torch.int32)
+
+
+def _prepack_impl(awq_qweight, awq_scales, awq_qzeros):
+    dev = awq_qweight.device
+    _require(awq_qweight.dtype == torch.int32 and awq_qweight.dim() == 2, "awq_qweight must be int32 [K, N/8]")
+    k, n = awq_qweight.size(0), awq_qweight.size(1) * 8
+    _require(k % 128 == 0 and n % 16 == 0, f"K={k} must be a multiple of 128 and N={n} of 16")
+    g = k // 128
+    _require(awq_scales.dtype == torch.float16 and tuple(awq_scales.shape) == (g, n),
+             f"awq_scales must be float16 [{g}, {n}], got {awq_scales.dtype} {tuple(awq_scales.shape)}")
+    _require(awq_qzeros.dtype == torch.int32 and tuple(awq_qzeros.shape) == (g, n // 8),
+             f"awq_qzeros must be int32 [{g}, {n // 8}], got {awq_qzeros.dtype} {tuple(awq_qzeros.shape)}")
+    _same_device("awq_scales", awq_scales, dev)
+    _same_device("awq_qzeros", awq_qzeros, dev)
+    qw, sc, qz = awq_qweight.contiguous(), awq_scales.contiguous(), awq_qzeros.contiguous()
+    wpack = torch.empty((n // 16, g, 64, 16), dtype=torch.uint8, device=dev)
+    wmeta = torch.empty((n // 16, g, 16), dtype=torch.int32, device=dev)
+    lib = _lib.load()
+    with _DeviceGuard(dev):
+        st = lib.pq_w4a8_prepack(qw.data_ptr(), sc.data_ptr(), qz.data_ptr(), wpack.data_ptr(), wmeta.data_ptr(), k,
+                                 n, 128, _stream(dev))
+    _lib.check(st, "paroquant::w4a8_prepack")
+    return wpack, wmeta
+
+
+_pq_lib.impl("w4a8_prepack", _prepack_impl, "CUDA")
+
+
+@torch.library.register_fake("paroquant::w4a8_prepack")
+def _prepack_fake(awq_qweight, awq_scales, awq_qzeros):
+    k, n = awq_qweight.size(0), awq_qweight.size(1) * 8
+    return (awq_qweight.new_empty((n // 16, k // 128, 64, 16), dtype=torch.uint8),
+            awq_qweight.new_empty((n // 16, k // 128, 16), dtype=torch.int32))
+
+
+def _linear_impl(x, pairs, cos_sin, scales, wpack, wmeta, bias, workspace, input_fp16, materialize_fp16, out_dtype):
+    dev = x.device
+    n, k = _check_weights(wpack, wmeta, dev)
+    _require(x.size(-1) == k, f"x has {x.size(-1)} features, the weights expect {k}")
+    xq, xs, _ = _rotate_quant(x, pairs, cos_sin, scales, input_fp16, materialize_fp16, False)
+    y = _gemm_launch(xq, xs, wpack, wmeta, bias, workspace, out_dtype, xq.size(0), n, k, dev)
+    return y.view(*x.shape[:-1], n)
+
+
+_pq_lib.impl("w4a8_linear", _linear_impl, "CUDA")
+
+
+@torch.library.register_fake("paroquant::w4a8_linear")
+def _linear_fake(x, pairs, cos_sin, scales, wpack, wmeta, bias, workspace, input_fp16, materialize_fp16, out_dtype):
+    return x.new_empty((*x.shape[:-1], wpack.size(0) * 16), dtype=out_dtype)

@@ -1,0 +1,296 @@
+"""Benchmark of the W4A8 linear path (rotation + per-token int8 quant + int4 x int8 GEMM).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload of ``value`` (one "step"): one Qwen3-8B decoder layer's seven
+quantized linears (q/o 4096->4096, k/v 4096->1024, gate/up 4096->12288,
+down 12288->4096) at M = 1 decode token, bf16 in and out, each linear =
+fused rotate+quant kernel + W4A8 GEMM kernel, replayed as one HIP graph per
+layer.  Steps cycle through a pool of distinct layers (> 512 MB of weights)
+so the 256 MB Infinity Cache cannot serve them.  value = algorithmic bytes
+of the layer / time per step, in GB/s, where per linear
+  B = N*K/2 + 2*N*K/128 + N*K/256 + 3*8*K + 2*K + 2*M*K + 2*M*N.
+Also reported: M = 4 and 16 decode, M = 3072 prefill in int8 TOPS and % of
+the 5.0 POPS dense int8 peak, the roofline of the dominant kernel (the
+decode GEMM at M = 1) and the CPU oracle timed on the host.
+
+Data are synthetic (seeded), weights random-init; one process, one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+KROT = 8
+
+
+def linear_bytes(M: int, N: int, K: int) -> int:
+    return N * K // 2 + 2 * N * K // 128 + N * K // 256 + 3 * KROT * K + 2 * K + 2 * M * K + 2 * M * N
+
+
+def gemm_kernel_bytes(M: int, N: int, K: int) -> int:
+    """Algorithmic bytes of the GEMM kernel alone: int4 codes, fp16 scales, int4 zeros,
+    int8 activations + fp32 token scales in, bf16 out."""
+    return N * K // 2 + 2 * N * K // 128 + N * K // 256 + M * K + 4 * M + 2 * M * N
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--pool-layers", type=int, default=6)
+    ap.add_argument("--prefill-steps", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    import alpamayo_amd  # noqa: F401
+    from alpamayo_amd import _lib, workloads
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    _lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    names = list(workloads.QWEN3_8B_LINEARS)
+    shapes = [workloads.QWEN3_8B_LINEARS[n] for n in names]
+
+    # ---- weight pool -------------------------------------------------------
+    t0 = time.time()
+    pool = []
+    for li in range(args.pool_layers):
+        g = workloads.generator(1001 + li, device=dev)
+        layer = [workloads.build_module(workloads.linear_spec(n, N, K, g, device=dev), dev)
+                 for n, (N, K) in zip(names, shapes)]
+        pool.append(layer)
+    torch.cuda.synchronize()
+    pool_mb = sum(m.rotate_linear.qlinear.qweight.numel() for L in pool for m in L) / 1e6
+    log(f"pool: {args.pool_layers} layers, {pool_mb:.0f} MB of packed int4 weights ({time.time() - t0:.1f}s)")
+
+    def make_inputs(M, seed):
+        g = workloads.generator(seed, device=dev)
+        return [[workloads.activations(M, K, g, device=dev) for (_, K) in shapes] for _ in pool]
+
+    def capture_layers(M, seed):
+        xs = make_inputs(M, seed)
+        graphs, outs = [], []
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for L, X in zip(pool, xs):
+                for m, x in zip(L, X):
+                    m(x)
+        torch.cuda.current_stream().wait_stream(s)
+        for L, X in zip(pool, xs):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                o = [m(x) for m, x in zip(L, X)]
+            graphs.append(gr)
+            outs.append(o)
+        return graphs, outs, xs
+
+    def time_graphs(graphs, steps, warmup):
+        for i in range(warmup):
+            graphs[i % len(graphs)].replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            graphs[i % len(graphs)].replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps          # ms per step
+
+    result = {}
+
+    # ---- decode: M = 1 (value), 4, 16 -------------------------------------
+    decode = {}
+    for M in (1, 4, 16):
+        graphs, _, _ = capture_layers(M, 5000 + M)
+        ms = time_graphs(graphs, args.steps, args.warmup)
+        b = sum(linear_bytes(M, N, K) for N, K in shapes)
+        decode[M] = (ms, b / (ms * 1e-3) / 1e9)
+        log(f"decode M={M}: {ms * 1e3:.1f} us/layer, {decode[M][1]:.0f} GB/s")
+        del graphs
+    ms_per_step, value = decode[1]
+
+    # ---- roofline of the dominant kernel: the decode GEMM at M = 1 --------
+    xq_all = []
+    for L, X in zip(pool, make_inputs(1, 7001)):
+        row = []
+        for m, x in zip(L, X):
+            r = m.rotate_linear.rotation
+            row.append(torch.ops.paroquant.rotate_quant_i8(x, r.pairs_u8, r.cos_sin, r.scales_f32, True, True))
+        xq_all.append(row)
+    gemm_launches = [(m.rotate_linear.qlinear, xq, xs) for L, row in zip(pool, xq_all) for m, (xq, xs) in zip(L, row)]
+    gg = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for q, xq, xs in gemm_launches:
+            torch.ops.paroquant.w4a8_gemm(xq, xs, q.qweight, q.scales, None, q.workspace, torch.bfloat16)
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(gg):
+        for q, xq, xs in gemm_launches:
+            torch.ops.paroquant.w4a8_gemm(xq, xs, q.qweight, q.scales, None, q.workspace, torch.bfloat16)
+    gemm_ms = time_graphs([gg], max(10, args.steps // 10), 3)
+    gemm_bytes = sum(gemm_kernel_bytes(1, q.out_features, q.in_features) for q, _, _ in gemm_launches)
+    achieved = gemm_bytes / (gemm_ms * 1e-3) / 1e9
+    per_launch_us = gemm_ms * 1e3 / len(gemm_launches)
+    log(f"decode GEMM M=1: {per_launch_us:.2f} us/launch avg, {achieved:.0f} GB/s")
+    del gg
+
+    # ---- prefill M = 3072 ---------------------------------------------------
+    prefill = None
+    if not args.no_prefill:
+        M = 3072
+        L = pool[0]
+        g = workloads.generator(6000, device=dev)
+        X = [workloads.activations(M, K, g, device=dev) for (_, K) in shapes]
+        for m, x in zip(L, X):
+            m(x)
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            outs = [m(x) for m, x in zip(L, X)]
+        ms = time_graphs([gr], args.prefill_steps, 3)
+        ops = sum(2 * M * N * K for N, K in shapes)
+        tops = ops / (ms * 1e-3) / 1e12
+        # GEMM kernels alone
+        xq = [torch.ops.paroquant.rotate_quant_i8(x, m.rotate_linear.rotation.pairs_u8,
+                                                  m.rotate_linear.rotation.cos_sin,
+                                                  m.rotate_linear.rotation.scales_f32, True, True)
+              for m, x in zip(L, X)]
+        gg = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gg):
+            for m, (q8, s8) in zip(L, xq):
+                q = m.rotate_linear.qlinear
+                torch.ops.paroquant.w4a8_gemm(q8, s8, q.qweight, q.scales, None, q.workspace, torch.bfloat16)
+        gms = time_graphs([gg], args.prefill_steps, 3)
+        gtops = ops / (gms * 1e-3) / 1e12
+        prefill = {"ms_per_layer": round(ms, 4), "tops": round(tops, 1),
+                   "pct_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2),
+                   "gemm_only_tops": round(gtops, 1), "gemm_only_pct_int8_peak": round(100 * gtops / INT8_PEAK_TOPS, 2)}
+        log(f"prefill M=3072: {ms:.3f} ms/layer, {tops:.0f} TOPS ({prefill['pct_int8_peak']}%), "
+            f"GEMM only {gtops:.0f} TOPS")
+        del gr, gg, outs, xq, X
+
+    # ---- CPU baseline: the oracle on the host ------------------------------
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(args.cpu_seconds)
+
+    result = {
+        "metric": "W4A8 rot+quant+GEMM: M=1 HBM GB/s; M=3072 int8 TOPS (% of peak)",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded activations with 1% x20 outlier channels; random int4 weights, fp16 group scales)",
+        "config": {
+            "workload": "qwen3-8b decoder layer, 7 W4A8 linears (q,k,v,o 4096->4096/1024; gate,up 4096->12288; "
+                        "down 12288->4096), decode M=1, bf16 in/out, KROT=8, group 128",
+            "tokens_per_step": 1,
+            "weight_pool_layers": args.pool_layers,
+            "weight_pool_mb": round(pool_mb, 1),
+            "graph_replay": True,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gemm_skinny (decode W4A8 GEMM), M=1, bytes-weighted over the 7 layer shapes",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(per_launch_us, 3),
+        },
+        "decode": {f"M{M}": {"us_per_layer": round(v[0] * 1e3, 2), "GBps": round(v[1], 1),
+                             "frac_hbm": round(v[1] / HBM_PEAK_GBS, 4)} for M, v in decode.items()},
+        "prefill_M3072": prefill,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def cpu_baseline(seconds: float):
+    """Time the oracle's reference-path linear (AWQ unpack + dequant + fp32 matmul) on the host
+    over one decoder layer's seven linears at M = 1 (a bounded sample)."""
+    import numpy as np
+
+    from alpamayo_amd import workloads
+    from oracle import linear as olin
+    from oracle import rotation as orot
+
+    try:
+        from threadpoolctl import threadpool_info, threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    cores = min(16, len(os.sched_getaffinity(0)))
+    ctx = threadpool_limits(limits=cores) if threadpool_limits else None
+    try:
+        specs = []
+        g = workloads.generator(1001)
+        for n, (N, K) in workloads.QWEN3_8B_LINEARS.items():
+            sp = workloads.linear_spec(n, N, K, g)
+            c, s = orot.cos_sin_table(sp.theta.numpy())
+            x = workloads.activations(1, K, g).float().numpy()
+            specs.append((sp, c, s, x))
+        layer_bytes = sum(linear_bytes(1, sp.N, sp.K) for sp, _, _, _ in specs)
+        layers, t0 = 0, time.perf_counter()
+        times = []
+        while True:
+            t1 = time.perf_counter()
+            for sp, c, s, x in specs:
+                olin.reference_path_dequant(x, sp.pairs.numpy(), c, s, sp.channel_scales.float().reshape(-1).numpy(),
+                                            sp.w.awq_qweight.numpy(), sp.w.awq_scales.numpy(), sp.w.awq_qzeros.numpy())
+            times.append(time.perf_counter() - t1)
+            layers += 1
+            if time.perf_counter() - t0 > seconds or layers >= 50:
+                break
+        if threadpool_limits:
+            used = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+        else:
+            used = cores
+        per_layer = float(np.median(times))
+    finally:
+        if ctx is not None:
+            ctx.__exit__(None, None, None)
+    gbps = layer_bytes / per_layer / 1e9
+    log(f"cpu oracle: {per_layer * 1e3:.1f} ms/layer over {layers} layers, {gbps:.3f} GB/s, {used} threads")
+    return {"value": round(gbps, 4), "unit": "GB/s", "cores": int(used), "kind": "port",
+            "sample": f"{layers} passes of one decoder layer's 7 linears at M=1 (median {per_layer * 1e3:.0f} ms/layer): "
+                      "numpy oracle reference path (AWQ unpack, dequant_awq, fp32 matmul)",
+            "ms_per_step": round(per_layer * 1e3, 2)}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,120 @@
+/*
+ * paroquant_hip.h -- C ABI of libparoquant_hip.so, the MI355X (gfx950)
+ * implementation of the ParoQuant W4A8 linear path.
+ *
+ * Conventions (shared by every entry point):
+ *   - plain pointers and sizes; every device buffer is allocated by the
+ *     caller; no entry point allocates device memory or synchronises;
+ *   - work is enqueued on the `stream` argument (a hipStream_t, passed as
+ *     void* so the header needs no HIP include; NULL = default stream);
+ *   - the return value is a pq_status; on failure pq_last_error() returns a
+ *     thread-local message describing the first failing check.  Arguments
+ *     are validated on the host before anything is launched;
+ *   - inputs are never written.
+ *
+ * Reference interfaces replaced (paths relative to the reference tree):
+ *   pq_rotate            torch.ops.rotation.rotate
+ *                        kernels/paroquant_kernels/src/rotation.cu:456-493, 576-584
+ *   pq_rotate_quant_i8   rotation.rotate (fp16) followed by vLLM's per-token
+ *                        int8 quant inside apply_awq_marlin_linear
+ *                        src/alpamayo_r1/utils/quantization/paroquant_marlin_w4a8.py:59-65, 319-333
+ *   pq_quant_i8          the per-token int8 quant alone (same call site)
+ *   pq_w4a8_gemm         the Marlin int4 x int8 GEMM (same call site, launch #4)
+ *   pq_w4a8_prepack      MarlinW4A8Linear.load_from_awq's repack of AWQ
+ *                        buffers (paroquant_marlin_w4a8.py:274-312)
+ */
+#ifndef PAROQUANT_HIP_H
+#define PAROQUANT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PQ_ABI_VERSION 1
+
+enum pq_status {
+  PQ_OK = 0,
+  PQ_ERR_ARG = 1,          /* bad pointer, size, alignment or shape */
+  PQ_ERR_UNSUPPORTED = 2,  /* valid but not implemented (dtype, krot, group) */
+  PQ_ERR_HIP = 3,          /* a HIP runtime call failed */
+  PQ_ERR_WORKSPACE = 4     /* workspace missing or too small */
+};
+
+enum pq_dtype { PQ_F32 = 0, PQ_F16 = 1, PQ_BF16 = 2 };
+
+/* flags of pq_rotate_quant_i8 */
+#define PQ_RQ_INPUT_FP16 1u        /* round the input to fp16 first (the bf16->fp16 wrapper cast) */
+#define PQ_RQ_MATERIALIZE_FP16 2u  /* round rotated values to fp16 before quantizing */
+
+int pq_abi_version(void);
+const char* pq_last_error(void);
+
+/* y = R_{krot-1} ... R_0 (scales * x) per group, the rotation::rotate op.
+ * x, y: [rows, h] of `dtype`; idx_ij: int16 [krot, h] group-local pair
+ * indices (pair t of group g = idx[r, g*G+2t], idx[r, g*G+2t+1]); theta:
+ * [krot, h/2] of `dtype`; scales: [h] of `dtype` or NULL.
+ * krot in {1, 2, 4, 8, 16}; group_size in {64, 128}; h % group_size == 0.
+ * Each layer must pair every channel of a group exactly once.
+ * Reference: rotation.cu:116-225 (launcher), 456-493 (dispatch). */
+int pq_rotate(const void* x, void* y, const int16_t* idx_ij, const void* theta,
+              const void* scales, int64_t rows, int64_t h, int krot, int group_size,
+              int dtype, void* stream);
+
+/* Fused rotation + channel scale + per-token absmax + int8 quantization.
+ * x: [rows, h] of x_dtype; pairs: uint8 [krot, h] group-local indices
+ * (group 128); cos_sin: float32 [krot, h/2, 2] (cos, sin) of each pair's
+ * angle; scales: float32 [h] or NULL.
+ * Outputs xq int8 [rows, h], xscale float32 [rows] (absmax/127), and, when
+ * xrot is not NULL, the rotated activations as fp16 [rows, h].
+ * flags: PQ_RQ_* bits.  krot in 1..16, h % 128 == 0, h <= 16384.
+ * Reference: rotation.cu:15-60 + paroquant_marlin_w4a8.py:319-333. */
+int pq_rotate_quant_i8(const void* x, int x_dtype, const uint8_t* pairs, const float* cos_sin,
+                       const float* scales, int8_t* xq, float* xscale, void* xrot,
+                       int64_t rows, int64_t h, int krot, unsigned flags, void* stream);
+
+/* Per-token int8 quantization of x [rows, h] (x_dtype) -> xq, xscale.
+ * Reference: vLLM scaled_int8_quant as called at paroquant_marlin_w4a8.py:319-333. */
+int pq_quant_i8(const void* x, int x_dtype, int8_t* xq, float* xscale, int64_t rows, int64_t h,
+                void* stream);
+
+/* Bytes of workspace pq_w4a8_gemm needs for this shape (0 if none).
+ * The workspace must be zero-filled once before its first use; every call
+ * leaves it zero-filled again, so it can be reused by later calls on the
+ * same stream.  Calls that overlap in time must not share a workspace. */
+size_t pq_w4a8_workspace_size(int64_t m, int64_t n, int64_t k, int group_size);
+
+/* y[m, n] = xscale[m] * sum_g s[g, n] * sum_{k in g} (q[k, n] - z[g, n]) * xq[m, k]
+ *           (+ bias[n]),  written as y_dtype.
+ * xq: int8 [m, k]; xscale: float32 [m]; wpack/wmeta: the prepacked weights
+ * (pq_w4a8_prepack); bias: [n] of bias_dtype or NULL.
+ * group_size == 128, k % 128 == 0, n % 16 == 0.
+ * Reference: apply_awq_marlin_linear, paroquant_marlin_w4a8.py:314-333. */
+int pq_w4a8_gemm(const int8_t* xq, const float* xscale, const uint8_t* wpack, const uint32_t* wmeta,
+                 const void* bias, int bias_dtype, void* y, int y_dtype, int64_t m, int64_t n,
+                 int64_t k, int group_size, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Debug/parity variant: the exact per-group int32 partials
+ * partials[m, g, n] = sum_{k in g} (q[k, n] - z[g, n]) * xq[m, k].
+ * Same kernels as pq_w4a8_gemm up to the epilogue.  Reference: the int32
+ * accumulators of the Marlin W4A8 GEMM (paroquant_marlin_w4a8.py:319-333). */
+int pq_w4a8_gemm_partials(const int8_t* xq, const uint8_t* wpack, const uint32_t* wmeta,
+                          int32_t* partials, int64_t m, int64_t n, int64_t k, int group_size,
+                          void* stream);
+
+/* Repack AWQ buffers into the kernel layout.
+ * awq_qweight: int32 [k, n/8]; awq_scales: fp16 bits [k/128, n];
+ * awq_qzeros: int32 [k/128, n/8] (nibble order 0,2,4,6,1,3,5,7).
+ * wpack: uint8 [n/16, k/128, 64, 16] (n*k/2 bytes); wmeta: uint32 [n/16, k/128, 16].
+ * Reference: MarlinW4A8Linear.load_from_awq, paroquant_marlin_w4a8.py:274-312. */
+int pq_w4a8_prepack(const int32_t* awq_qweight, const uint16_t* awq_scales,
+                    const int32_t* awq_qzeros, uint8_t* wpack, uint32_t* wmeta, int64_t k,
+                    int64_t n, int group_size, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAROQUANT_HIP_H */

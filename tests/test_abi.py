@@ -1,0 +1,87 @@
+"""The C-ABI library loads on the CPU, exports every symbol the header declares,
+and rejects bad arguments on the host before any launch (no GPU needed)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from alpamayo_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "paroquant_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(pq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = _declared()
+    assert len(names) >= 9
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures must cover the header exactly"
+
+
+def test_abi_version():
+    assert _lib.load().pq_abi_version() == _lib.ABI_VERSION == 1
+
+
+def _err(lib):
+    return lib.pq_last_error().decode()
+
+
+def test_rotate_argument_checks():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation first
+    assert lib.pq_rotate(p, p, p, p, None, 4, 256, 8, 32, 1, None) == 2
+    assert "group_size" in _err(lib)
+    assert lib.pq_rotate(p, p, p, p, None, 4, 256, 3, 128, 1, None) == 2
+    assert "KROT" in _err(lib)
+    assert lib.pq_rotate(p, p, p, p, None, 4, 200, 8, 128, 1, None) == 1
+    assert "divisible" in _err(lib)
+    assert lib.pq_rotate(p, p, p, p, None, 4, 256, 8, 128, 7, None) == 2
+    assert lib.pq_rotate(None, None, None, None, None, 4, 256, 8, 128, 1, None) == 1
+    assert lib.pq_rotate(None, None, None, None, None, 0, 256, 8, 128, 1, None) == 0  # empty input: no-op
+
+
+def test_rotate_quant_and_gemm_argument_checks():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)
+    assert lib.pq_rotate_quant_i8(p, 2, p, p, None, p, p, None, 4, 200, 8, 3, None) == 1
+    assert lib.pq_rotate_quant_i8(p, 2, p, p, None, p, p, None, 4, 256, 0, 3, None) == 2
+    assert lib.pq_rotate_quant_i8(p, 2, p, p, None, p, p, None, 4, 256, 8, 8, None) == 1
+    assert "flags" in _err(lib)
+    assert lib.pq_rotate_quant_i8(ctypes.c_void_p(18), 2, p, p, None, p, p, None, 4, 256, 8, 3, None) == 1
+    assert "aligned" in _err(lib)
+    assert lib.pq_w4a8_gemm(p, p, p, p, None, 0, p, 2, 4, 64, 256, 64, None, 0, None) == 2
+    assert lib.pq_w4a8_gemm(p, p, p, p, None, 0, p, 2, 4, 60, 256, 128, None, 0, None) == 1
+    assert lib.pq_w4a8_gemm(p, p, p, p, None, 0, p, 2, 4, 64, 200, 128, None, 0, None) == 1
+    assert lib.pq_w4a8_gemm(p, p, p, p, None, 0, p, 9, 4, 64, 256, 128, None, 0, None) == 2
+    need = lib.pq_w4a8_workspace_size(1, 1024, 4096, 128)
+    assert need > 0
+    assert lib.pq_w4a8_gemm(p, p, p, p, None, 0, p, 2, 1, 1024, 4096, 128, None, 0, None) == 4
+    assert "workspace" in _err(lib)
+    assert lib.pq_w4a8_gemm(p, p, p, p, None, 0, p, 2, 1, 1024, 4096, 128, p, need - 1, None) == 4
+    assert lib.pq_w4a8_prepack(p, p, p, p, p, 100, 64, 128, None) == 1
+    assert lib.pq_w4a8_gemm_partials(p, p, p, p, 0, 64, 256, 128, None) == 0
+
+
+def test_workspace_size_rules():
+    lib = _lib.load()
+    assert lib.pq_w4a8_workspace_size(64, 4096, 4096, 128) == 0        # tiled path needs none
+    assert lib.pq_w4a8_workspace_size(1, 64, 100, 128) == 0            # invalid shape -> 0
+    for m in (1, 4, 16):
+        for n, k in ((1024, 4096), (4096, 4096), (12288, 4096), (4096, 12288)):
+            ws = lib.pq_w4a8_workspace_size(m, n, k, 128)
+            assert ws == 0 or ws >= 4096 + m * n * 4
+
+
+def test_status_names_and_error_type():
+    with pytest.raises(_lib.PQError, match="PQ_ERR_ARG"):
+        _lib.check(1, "x")
+    _lib.check(0, "x")
