@@ -23,7 +23,7 @@ from . import _lib
 if _os.path.exists(_lib.LIB_PATH):
     _lib.load()
 elif _torch.cuda.is_available():
-    raise ImportError(f"{_lib.LIB_PATH} is missing: build it with `python -m alpamayo_amd.build`")
+    raise ImportError(f"{_lib.LIB_PATH} is missing: build it with `python alpamayo_amd/build.py`")
 
 from . import ops  # noqa: E402,F401
 

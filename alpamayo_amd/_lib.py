@@ -40,6 +40,9 @@ SIGNATURES = {
     "pq_w4a8_gemm": (_INT, [_P, _P, _P, _P, _P, _INT, _P, _INT, _I64, _I64, _I64, _INT, _P, _SZ, _P]),
     "pq_w4a8_gemm_partials": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
     "pq_w4a8_prepack": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _INT, _P]),
+    "pq_w4a8_linear_workspace_size": (_SZ, [_I64, _I64, _I64, _INT]),
+    "pq_w4a8_linear": (_INT, [_P, _INT, _P, _P, _P, _P, _P, _P, _INT, _P, _INT, _I64, _I64, _I64, _INT, _UINT, _P, _SZ,
+                              _P]),
 }
 
 _lock = threading.Lock()
@@ -61,7 +64,7 @@ def load() -> ctypes.CDLL:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(
                 f"libparoquant_hip.so not found at {LIB_PATH}; build it with "
-                "`python -m alpamayo_amd.build` (there is no non-HIP implementation)")
+                "`python alpamayo_amd/build.py` (there is no non-HIP implementation)")
         lib = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)

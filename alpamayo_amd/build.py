@@ -1,6 +1,6 @@
 """Build libparoquant_hip.so (gfx950) in-tree with hipcc.
 
-    python -m alpamayo_amd.build          # or __graft_entry__.build()
+    python alpamayo_amd/build.py          # or __graft_entry__.build()
 
 Every ``csrc/*.hip`` file is compiled to an object under ``_build/`` and the
 objects are linked into ``alpamayo_amd/libparoquant_hip.so``.  Device code

@@ -24,69 +24,41 @@
 //   gemm_skinny  M <= 16: each wave streams 1 KB weight blocks (one 16-column
 //                tile x one 128-group) with 16-byte loads, two
 //                v_mfma_i32_16x16x64_i8 per block (activation rows padded to
-//                16), waves of a workgroup split K, workgroups optionally
-//                split K further with a deterministic last-arriving-block
-//                reduction through the workspace.
+//                16); the waves of a workgroup split K and add their partial
+//                sums in LDS in a fixed order.
 //   gemm_tiled   M > 16: 128x128 output tiles, A (int8) and B (int4) staged
 //                through LDS one group at a time with the next group
 //                prefetched into registers, 2x2 waves of 64x64, each
 //                2x2 v_mfma_i32_32x32x32_i8 tiles per 32-deep K step.
-#include "pq_common.h"
+#include "pq_device.h"
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
+using namespace pqd;
 
 namespace {
 
-__device__ __forceinline__ uint32_t zero_bias(uint32_t z) { return 0x80808080u - z * 0x01010101u; }
-
-__device__ __forceinline__ int unpack_lo(uint32_t w, uint32_t zb) {
-  return static_cast<int>(((w & 0x0f0f0f0fu) + zb) ^ 0x80808080u);
-}
-__device__ __forceinline__ int unpack_hi(uint32_t w, uint32_t zb) {
-  return static_cast<int>((((w >> 4) & 0x0f0f0f0fu) + zb) ^ 0x80808080u);
-}
-
-// 8 bytes of codes (16 k) -> 16 signed bytes in k order.
-__device__ __forceinline__ v4i unpack16(uint32_t w0, uint32_t w1, uint32_t zb) {
-  v4i r;
-  r.x = unpack_lo(w0, zb);
-  r.y = unpack_hi(w0, zb);
-  r.z = unpack_lo(w1, zb);
-  r.w = unpack_hi(w1, zb);
-  return r;
-}
-
-__device__ __forceinline__ float epilogue(float acc, float xscale, const void* bias, int bias_dtype, int n) {
-  float v = acc * xscale;
-  if (bias != nullptr) v = v + pq_load_dyn(bias, bias_dtype, n);
-  return v;
-}
-
 // ---------------------------------------------------------------------------
 // Decode-size GEMM (M <= 16)
+//
+// Workgroup = W waves over NT 16-column tiles; wave w takes the groups
+// w, w+W, w+2W, ... of K and issues the 16-byte loads of U groups at once.
+// The W partial sums meet in LDS and are added in a fixed order, so no
+// workgroup ever communicates with another (no split-K workspace, no
+// device-scope fence).
 // ---------------------------------------------------------------------------
-template <int NT, int U, bool PARTIALS>
-__global__ __launch_bounds__(256) void gemm_skinny(
+template <int NT, int W, int U, bool PARTIALS>
+__global__ __launch_bounds__(W * 64) void gemm_skinny(
     const int8_t* __restrict__ xq, const float* __restrict__ xs, const uint8_t* __restrict__ wpack,
     const uint32_t* __restrict__ wmeta, const void* __restrict__ bias, int bias_dtype, void* __restrict__ y,
-    int y_dtype, uint32_t* __restrict__ counters, float* __restrict__ wsp, int32_t* __restrict__ partials, int M,
-    int N, int K, int splits, int gps) {
-  __shared__ float red[4][NT][4][64];
-  __shared__ int is_last;
+    int y_dtype, int32_t* __restrict__ partials, int M, int N, int K) {
+  __shared__ float red[W][NT][4][64];
   const int G = K >> 7;
-  const int ntg = (N >> 4) / NT;
-  const int tg = blockIdx.x % ntg;
-  const int split = blockIdx.x / ntg;
-  const int g_begin = split * gps;
-  const int g_end = min(G, g_begin + gps);
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int c = lane & 15;
   const int j = lane >> 4;
   const bool arow = c < M;
-  const int8_t* ap = xq + static_cast<int64_t>(c) * K + j * 32;
-  const int tile0 = tg * NT;
+  const int8_t* ap = xq + static_cast<int64_t>(arow ? c : 0) * K + j * 32;
+  const int tile0 = blockIdx.x * NT;
 
   float acc[NT][4];
 #pragma unroll
@@ -94,14 +66,14 @@ __global__ __launch_bounds__(256) void gemm_skinny(
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc[nt][v] = 0.0f;
 
-  for (int g0 = g_begin + wave; g0 < g_end; g0 += 4 * U) {
+  for (int g0 = wave; g0 < G; g0 += W * U) {
     v4i wb[U][NT];
     uint32_t wm[U][NT];
     v4i a0[U], a1[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int g = g0 + 4 * u;
-      if (g < g_end) {
+      const int g = g0 + W * u;
+      if (g < G) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const int64_t blk = static_cast<int64_t>(tile0 + nt) * G + g;
@@ -119,12 +91,12 @@ __global__ __launch_bounds__(256) void gemm_skinny(
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int g = g0 + 4 * u;
-      if (g < g_end) {
+      const int g = g0 + W * u;
+      if (g < G) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const uint32_t meta = wm[u][nt];
-          const uint32_t zb = zero_bias((meta >> 16) & 0xfu);
+          const uint32_t zb = meta_zero_bias(meta);
           const v4i w = wb[u][nt];
           const v4i b0 = unpack16(static_cast<uint32_t>(w.x), static_cast<uint32_t>(w.y), zb);
           const v4i b1 = unpack16(static_cast<uint32_t>(w.z), static_cast<uint32_t>(w.w), zb);
@@ -138,7 +110,7 @@ __global__ __launch_bounds__(256) void gemm_skinny(
               if (m < M) partials[(static_cast<int64_t>(m) * G + g) * N + (tile0 + nt) * 16 + c] = p[v];
             }
           } else {
-            const float sc = pq_f16_to_f32(static_cast<uint16_t>(meta & 0xffffu));
+            const float sc = meta_scale(meta);
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[nt][v] = fmaf(static_cast<float>(p[v]), sc, acc[nt][v]);
           }
@@ -148,62 +120,23 @@ __global__ __launch_bounds__(256) void gemm_skinny(
   }
   if constexpr (PARTIALS) return;
 
-  // Sum the four waves' K slices (fixed order).
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
     for (int v = 0; v < 4; ++v) red[wave][nt][v][lane] = acc[nt][v];
   __syncthreads();
-  const int rl = threadIdx.x & 63;
-  const int rv = threadIdx.x >> 6;
-  const int m = 4 * (rl >> 4) + rv;
-  const int cc = rl & 15;
-  float sum[NT];
+  for (int t = threadIdx.x; t < NT * 256; t += W * 64) {
+    const int nt = t >> 8;
+    const int rv = (t >> 6) & 3;
+    const int rl = t & 63;
+    const int m = 4 * (rl >> 4) + rv;
+    if (m >= M) continue;
+    float sum = 0.0f;
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt)
-    sum[nt] = ((red[0][nt][rv][rl] + red[1][nt][rv][rl]) + red[2][nt][rv][rl]) + red[3][nt][rv][rl];
-
-  if (splits == 1) {
-    if (m < M) {
-      const float xsm = xs[m];
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const int n = (tile0 + nt) * 16 + cc;
-        pq_store_dyn(y, y_dtype, static_cast<int64_t>(m) * N + n, epilogue(sum[nt], xsm, bias, bias_dtype, n));
-      }
-    }
-    return;
+    for (int w = 0; w < W; ++w) sum += red[w][nt][rv][rl];
+    const int n = (tile0 + nt) * 16 + (rl & 15);
+    pq_store_dyn(y, y_dtype, static_cast<int64_t>(m) * N + n, epilogue(sum, xs[m], bias, bias_dtype, n));
   }
-
-  // Split-K: publish this block's partial, the last block of the tile group
-  // reduces all of them in split order and re-arms the counter.
-  if (m < M) {
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int n = (tile0 + nt) * 16 + cc;
-      wsp[(static_cast<int64_t>(split) * M + m) * N + n] = sum[nt];
-    }
-  }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev = atomicAdd(&counters[tg], 1u);
-    is_last = (prev == static_cast<uint32_t>(splits - 1));
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  if (m < M) {
-    const float xsm = xs[m];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int n = (tile0 + nt) * 16 + cc;
-      float tot = 0.0f;
-      for (int s = 0; s < splits; ++s) tot += wsp[(static_cast<int64_t>(s) * M + m) * N + n];
-      pq_store_dyn(y, y_dtype, static_cast<int64_t>(m) * N + n, epilogue(tot, xsm, bias, bias_dtype, n));
-    }
-  }
-  if (threadIdx.x == 0) counters[tg] = 0u;
 }
 
 // ---------------------------------------------------------------------------
@@ -364,31 +297,48 @@ __global__ __launch_bounds__(256) void gemm_tiled(const int8_t* __restrict__ xq,
 // Host-side configuration
 // ---------------------------------------------------------------------------
 constexpr int kSkinnyMaxM = 16;
-constexpr int kSkinnyU = 4;
-constexpr size_t kCounterBytes = 4096;  // counters live in the first 4 KB of the workspace
 
 struct SkinnyCfg {
-  int nt;
-  int splits;
-  int gps;
+  int nt;  // 16-column tiles per workgroup
+  int w;   // waves per workgroup (split K)
 };
 
+// Enough workgroups to cover the chip with every weight byte of a wave
+// requested up front (<= 8 groups per wave), and more waves per workgroup
+// when the column tiles are few.
 SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k) {
   const int G = static_cast<int>(k / 128);
   const int tiles = static_cast<int>(n / 16);
-  const int nt = (m > 4 && tiles % 2 == 0) ? 2 : 1;
-  const int wg0 = tiles / nt;
-  int splits = 1;
-  while (static_cast<int64_t>(wg0) * splits < 512 && G / (splits * 2) >= 4) splits *= 2;
-  const int gps = (G + splits - 1) / splits;
-  splits = (G + gps - 1) / gps;
-  return {nt, splits, gps};
+  const int nt = (m > 4 && tiles % 2 == 0 && tiles / 2 >= 128) ? 2 : 1;
+  const int wgs = tiles / nt;
+  int w = 4;
+  if (wgs < 256 || G > 32) w = 8;
+  if (wgs < 128 || G > 64) w = 16;
+  return {nt, w};
 }
 
-size_t skinny_ws_bytes(int64_t m, int64_t n, int64_t k) {
-  const SkinnyCfg cfg = choose_skinny(m, n, k);
-  if (cfg.splits <= 1) return 0;
-  return kCounterBytes + static_cast<size_t>(cfg.splits) * m * n * sizeof(float);
+template <int NT, int W, bool PARTIALS>
+void launch_skinny_nw(const int8_t* xq, const float* xs, const uint8_t* wpack, const uint32_t* wmeta,
+                      const void* bias, int bias_dtype, void* y, int y_dtype, int32_t* partials, int M, int N, int K,
+                      hipStream_t stream) {
+  constexpr int U = W >= 16 ? 4 : 8;
+  const unsigned grid = static_cast<unsigned>((N / 16) / NT);
+  gemm_skinny<NT, W, U, PARTIALS><<<grid, W * 64, 0, stream>>>(xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype,
+                                                                partials, M, N, K);
+}
+
+template <bool PARTIALS>
+void launch_skinny(const SkinnyCfg& cfg, const int8_t* xq, const float* xs, const uint8_t* wpack,
+                   const uint32_t* wmeta, const void* bias, int bias_dtype, void* y, int y_dtype, int32_t* partials,
+                   int M, int N, int K, hipStream_t stream) {
+#define PQ_SKINNY(NT_, W_)                                                                                      \
+  if (cfg.nt == NT_ && cfg.w == W_) {                                                                           \
+    launch_skinny_nw<NT_, W_, PARTIALS>(xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype, partials, M, N, K, \
+                                        stream);                                                               \
+    return;                                                                                                     \
+  }
+  PQ_SKINNY(1, 4) PQ_SKINNY(1, 8) PQ_SKINNY(1, 16) PQ_SKINNY(2, 4) PQ_SKINNY(2, 8) PQ_SKINNY(2, 16)
+#undef PQ_SKINNY
 }
 
 int check_gemm_args(const char* who, int64_t m, int64_t n, int64_t k, int group_size) {
@@ -401,25 +351,12 @@ int check_gemm_args(const char* who, int64_t m, int64_t n, int64_t k, int group_
   return PQ_OK;
 }
 
-template <int NT, bool PARTIALS>
-void launch_skinny(const SkinnyCfg& cfg, const int8_t* xq, const float* xs, const uint8_t* wpack,
-                   const uint32_t* wmeta, const void* bias, int bias_dtype, void* y, int y_dtype, void* ws,
-                   int32_t* partials, int M, int N, int K, hipStream_t stream) {
-  const int ntg = (N / 16) / NT;
-  const unsigned grid = static_cast<unsigned>(ntg * cfg.splits);
-  uint32_t* counters = static_cast<uint32_t*>(ws);
-  float* wsp = ws ? reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes) : nullptr;
-  gemm_skinny<NT, kSkinnyU, PARTIALS><<<grid, 256, 0, stream>>>(xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype,
-                                                                 counters, wsp, partials, M, N, K, cfg.splits,
-                                                                 cfg.gps);
-}
-
 }  // namespace
 
 extern "C" size_t pq_w4a8_workspace_size(int64_t m, int64_t n, int64_t k, int group_size) {
-  if (group_size != 128 || m <= 0 || n <= 0 || k <= 0 || n % 16 || k % 128) return 0;
-  if (m > kSkinnyMaxM) return 0;
-  return skinny_ws_bytes(m, n, k);
+  // No kernel of this version exchanges data between workgroups.
+  (void)m, (void)n, (void)k, (void)group_size;
+  return 0;
 }
 
 extern "C" int pq_w4a8_gemm(const int8_t* xq, const float* xscale, const uint8_t* wpack, const uint32_t* wmeta,
@@ -439,18 +376,9 @@ extern "C" int pq_w4a8_gemm(const int8_t* xq, const float* xscale, const uint8_t
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int M = static_cast<int>(m), N = static_cast<int>(n), K = static_cast<int>(k);
   if (m <= kSkinnyMaxM) {
-    const SkinnyCfg cfg = choose_skinny(m, n, k);
-    if (cfg.splits > 1) {
-      const size_t need = skinny_ws_bytes(m, n, k);
-      PQ_REQUIRE(workspace != nullptr && workspace_bytes >= need, PQ_ERR_WORKSPACE,
-                 "pq_w4a8_gemm: workspace of %zu bytes needed for m=%lld n=%lld k=%lld, got %zu", need, (long long)m,
-                 (long long)n, (long long)k, workspace ? workspace_bytes : (size_t)0);
-      PQ_REQUIRE(pq::aligned_to(workspace, 16), PQ_ERR_ARG, "pq_w4a8_gemm: workspace must be 16-byte aligned");
-    }
-    if (cfg.nt == 2)
-      launch_skinny<2, false>(cfg, xq, xscale, wpack, wmeta, bias, bias_dtype, y, y_dtype, workspace, nullptr, M, N, K, s);
-    else
-      launch_skinny<1, false>(cfg, xq, xscale, wpack, wmeta, bias, bias_dtype, y, y_dtype, workspace, nullptr, M, N, K, s);
+    (void)workspace, (void)workspace_bytes;
+    launch_skinny<false>(choose_skinny(m, n, k), xq, xscale, wpack, wmeta, bias, bias_dtype, y, y_dtype, nullptr, M,
+                         N, K, s);
   } else {
     const unsigned grid = static_cast<unsigned>(((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN));
     gemm_tiled<false><<<grid, 256, 0, s>>>(xq, xscale, wpack, wmeta, bias, bias_dtype, y, y_dtype, nullptr, M, N, K);
@@ -471,11 +399,8 @@ extern "C" int pq_w4a8_gemm_partials(const int8_t* xq, const uint8_t* wpack, con
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int M = static_cast<int>(m), N = static_cast<int>(n), K = static_cast<int>(k);
   if (m <= kSkinnyMaxM) {
-    SkinnyCfg cfg = choose_skinny(m, n, k);
-    if (cfg.nt == 2)
-      launch_skinny<2, true>(cfg, xq, nullptr, wpack, wmeta, nullptr, 0, nullptr, 0, nullptr, partials, M, N, K, s);
-    else
-      launch_skinny<1, true>(cfg, xq, nullptr, wpack, wmeta, nullptr, 0, nullptr, 0, nullptr, partials, M, N, K, s);
+    launch_skinny<true>(choose_skinny(m, n, k), xq, nullptr, wpack, wmeta, nullptr, 0, nullptr, 0, partials, M, N,
+                        K, s);
   } else {
     const unsigned grid = static_cast<unsigned>(((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN));
     gemm_tiled<true><<<grid, 256, 0, s>>>(xq, nullptr, wpack, wmeta, nullptr, 0, nullptr, 0, partials, M, N, K);

@@ -13,11 +13,16 @@
 // All updates are written with explicit fmaf and the file is compiled with
 // -ffp-contract=off, so the float32 sequence is fixed:
 //   xi' = fma(xi, c, xj*s),  xj' = fma(xj, c, -(xi*s)).
-#include "pq_common.h"
+#include <type_traits>
+
+#include "pq_device.h"
+
+using pqd::quant4;
 
 namespace {
 
-constexpr int kRotRows = 4;  // rows per workgroup of the plain rotation kernel
+constexpr int kRotRows = 4;   // rows per workgroup of the plain rotation kernel
+constexpr int kMaxKrot = 16;  // rotation layers the fused kernel holds in registers
 
 // ---------------------------------------------------------------------------
 // rotation::rotate.  One wave per (4 rows x 128 channels); lane t owns pair t
@@ -89,14 +94,6 @@ __global__ __launch_bounds__(64) void rotate_kernel(const void* __restrict__ x, 
   }
 }
 
-// ---------------------------------------------------------------------------
-// Fused rotate + quant.  One workgroup per row (grid-stride over rows).  The
-// scaled row is staged in LDS as fp32 (h*4 bytes); wave w rotates groups
-// w, w+NW, ...: lane t owns pair t of the group in every layer, and since a
-// group is touched by one wave only, layers need no workgroup barrier (LDS
-// operations of one wave execute in order).  The last layer's outputs are
-// already in registers, so the fp16 rounding and the absmax happen there.
-// ---------------------------------------------------------------------------
 template <int NT>
 __device__ __forceinline__ float block_max(float v, float* red) {
   constexpr int NW = NT / 64;
@@ -107,15 +104,6 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 #pragma unroll
   for (int k = 1; k < NW; ++k) m = fmaxf(m, red[k]);
   return m;
-}
-
-__device__ __forceinline__ uint32_t quant4(float a, float b, float c, float d, float inv) {
-  auto q = [inv](float v) -> uint32_t {
-    float r = __builtin_rintf(v * inv);
-    r = fminf(fmaxf(r, -128.0f), 127.0f);
-    return static_cast<uint32_t>(static_cast<int>(r)) & 0xffu;
-  };
-  return q(a) | (q(b) << 8) | (q(c) << 16) | (q(d) << 24);
 }
 
 template <int DT>
@@ -142,80 +130,193 @@ __device__ __forceinline__ void load8(const void* base, int64_t elem, float f[8]
   }
 }
 
-template <int DT, int NT>
-__global__ __launch_bounds__(NT) void rotate_quant_kernel(
+// Orders this wave's LDS accesses across a Givens layer.  The wave's LDS
+// instructions already execute in order; this only stops the compiler from
+// moving them (it emits no wait on global loads).
+#define PQ_LDS_WAVE_FENCE() __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront", "local")
+
+// All KMAX layers' pair indices and (cos, sin) of one group, for lane = pair.
+// Layers past krot re-read layer krot-1 so every load is unconditional (the
+// loads then issue back to back instead of one round trip per layer).
+template <int KMAX>
+__device__ __forceinline__ void load_group_params(const uint8_t* __restrict__ pairs, const float2* __restrict__ cs,
+                                                  int h, int krot, int g, int lane, uint32_t (&pr)[KMAX],
+                                                  float2 (&cc)[KMAX]) {
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) {
+    const int rr = r < krot ? r : krot - 1;
+    pr[r] = *reinterpret_cast<const uint16_t*>(pairs + static_cast<int64_t>(rr) * h + g * 128 + 2 * lane);
+    cc[r] = cs[static_cast<int64_t>(rr) * (h >> 1) + g * 64 + lane];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fused rotate + quant over blocks of R rows.  512 threads; wave w rotates
+// groups w, w+8, ... for all R rows of the block in a private fp32 scratch
+// [R][128] (lane t owns pair t; the R rows give R independent LDS chains per
+// layer), and stores the finished values in a row buffer [R][h] (fp16 when
+// the result is materialized in fp16, fp32 otherwise).  The next group's
+// parameters and inputs are requested before the current group's layers
+// run.  After a block-wide absmax per row, the row buffer is quantized with
+// coalesced stores.  Parameters are read once per group per R rows.
+// ---------------------------------------------------------------------------
+constexpr int kRQWaves = 8;
+constexpr int kRQMaxRows = 8;
+
+template <int DT, int KMAX, bool MAT16>
+__global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(
     const void* __restrict__ x, const uint8_t* __restrict__ pairs, const float2* __restrict__ cs,
     const float* __restrict__ scales, int8_t* __restrict__ xq, float* __restrict__ xscale,
-    uint16_t* __restrict__ xrot, int64_t rows, int h, int krot, unsigned flags) {
-  extern __shared__ float buf[];
-  __shared__ float red[NT / 64];
-  constexpr int NW = NT / 64;
+    uint16_t* __restrict__ xrot, int64_t rows, int h, int krot, unsigned flags, int R) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
+  __shared__ float red[kRQWaves][kRQMaxRows];
+  using RowT = typename std::conditional<MAT16, uint16_t, float>::type;
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int w = t >> 6;
   const bool in16 = (flags & PQ_RQ_INPUT_FP16) != 0;
-  const bool mat16 = (flags & PQ_RQ_MATERIALIZE_FP16) != 0;
-  const int ngroups = h >> 7;
-  const int half_h = h >> 1;
+  const int G = h >> 7;
+  float* scratch = reinterpret_cast<float*>(lds_raw) + w * (kRQMaxRows * 128);
+  RowT* rowbuf = reinterpret_cast<RowT*>(lds_raw + kRQWaves * kRQMaxRows * 128 * sizeof(float));
 
-  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
-    const int64_t rbase = row * h;
-    for (int v = t; v < (h >> 3); v += NT) {
-      float f[8];
-      load8<DT>(x, rbase + 8 * v, f);
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
+  const int nr = static_cast<int>(rows - row0 < R ? rows - row0 : R);
+  float rmax[kRQMaxRows];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float val = in16 ? pq_round_f16(f[e]) : f[e];
-        if (scales != nullptr) val = val * scales[8 * v + e];
-        buf[8 * v + e] = val;
+  for (int r = 0; r < kRQMaxRows; ++r) rmax[r] = 0.0f;
+
+  uint32_t pr[KMAX], prn[KMAX];
+  float2 cc[KMAX], ccn[KMAX];
+  float xa[kRQMaxRows], xb[kRQMaxRows], xan[kRQMaxRows], xbn[kRQMaxRows];
+  float sa = 1.0f, sb = 1.0f, san = 1.0f, sbn = 1.0f;
+
+  // Inputs of group g for the block's rows (row indices clamped to valid rows).
+  auto load_inputs = [&](int g, float (&va)[kRQMaxRows], float (&vb)[kRQMaxRows], float& s0, float& s1) {
+#pragma unroll
+    for (int r = 0; r < kRQMaxRows; ++r) {
+      const int64_t row = row0 + (r < nr ? r : nr - 1);
+      va[r] = pq_load_as_f32<DT>(x, row * h + g * 128 + lane);
+      vb[r] = pq_load_as_f32<DT>(x, row * h + g * 128 + 64 + lane);
+    }
+    if (scales != nullptr) {
+      s0 = scales[g * 128 + lane];
+      s1 = scales[g * 128 + 64 + lane];
+    }
+  };
+
+  if (w < G) {
+    load_group_params<KMAX>(pairs, cs, h, krot, w, lane, pr, cc);
+    load_inputs(w, xa, xb, sa, sb);
+  }
+  for (int g = w; g < G; g += kRQWaves) {
+    const int gn = (g + kRQWaves < G) ? g + kRQWaves : g;   // clamped: the loads stay unconditional
+    load_group_params<KMAX>(pairs, cs, h, krot, gn, lane, prn, ccn);
+    load_inputs(gn, xan, xbn, san, sbn);
+
+#pragma unroll
+    for (int r = 0; r < kRQMaxRows; ++r) {
+      if (r < nr) {
+        const float a = in16 ? pq_round_f16(xa[r]) : xa[r];
+        const float b = in16 ? pq_round_f16(xb[r]) : xb[r];
+        scratch[r * 128 + lane] = a * sa;
+        scratch[r * 128 + 64 + lane] = b * sb;
       }
     }
-    __syncthreads();
-
-    float amax = 0.0f;
-    for (int g = w; g < ngroups; g += NW) {
-      float* gb = buf + g * 128;
-      float ni = 0.0f, nj = 0.0f;
-      int i = 0, j = 0;
-      for (int r = 0; r < krot; ++r) {
-        const uint16_t pr =
-            *reinterpret_cast<const uint16_t*>(pairs + static_cast<int64_t>(r) * h + g * 128 + 2 * lane);
-        const float2 c = cs[static_cast<int64_t>(r) * half_h + g * 64 + lane];
-        i = pr & 127;
-        j = (pr >> 8) & 127;
-        const float xi = gb[i];
-        const float xj = gb[j];
-        ni = fmaf(xi, c.x, xj * c.y);
-        nj = fmaf(xj, c.x, -(xi * c.y));
-        gb[i] = ni;
-        gb[j] = nj;
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    PQ_LDS_WAVE_FENCE();
+    float ni[kRQMaxRows], nj[kRQMaxRows];
+    int i = 0, j = 0;
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      if (k < krot) {
+        i = pr[k] & 127;
+        j = (pr[k] >> 8) & 127;
+#pragma unroll
+        for (int r = 0; r < kRQMaxRows; ++r) {
+          if (r < nr) {
+            pqd::givens(scratch[r * 128 + i], scratch[r * 128 + j], cc[k].x, cc[k].y, ni[r], nj[r]);
+            scratch[r * 128 + i] = ni[r];
+            scratch[r * 128 + j] = nj[r];
+          }
+        }
+        PQ_LDS_WAVE_FENCE();
       }
-      if (mat16) {
-        ni = pq_round_f16(ni);
-        nj = pq_round_f16(nj);
-        gb[i] = ni;
-        gb[j] = nj;
-      }
-      amax = fmaxf(amax, fmaxf(fabsf(ni), fabsf(nj)));
     }
-    __syncthreads();  // every group's final values are in LDS
+#pragma unroll
+    for (int r = 0; r < kRQMaxRows; ++r) {
+      if (r < nr) {
+        float vi = ni[r], vj = nj[r];
+        if constexpr (MAT16) {
+          const uint16_t hi = pq_f32_to_f16(vi), hj = pq_f32_to_f16(vj);
+          rowbuf[r * h + g * 128 + i] = hi;
+          rowbuf[r * h + g * 128 + j] = hj;
+          vi = pq_f16_to_f32(hi);
+          vj = pq_f16_to_f32(hj);
+        } else {
+          rowbuf[r * h + g * 128 + i] = vi;
+          rowbuf[r * h + g * 128 + j] = vj;
+        }
+        rmax[r] = fmaxf(rmax[r], fmaxf(fabsf(vi), fabsf(vj)));
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      pr[k] = prn[k];
+      cc[k] = ccn[k];
+    }
+#pragma unroll
+    for (int r = 0; r < kRQMaxRows; ++r) {
+      xa[r] = xan[r];
+      xb[r] = xbn[r];
+    }
+    sa = san;
+    sb = sbn;
+  }
 
-    const float am = block_max<NT>(amax, red);
-    const float inv = am > 0.0f ? 127.0f / am : 0.0f;
-    if (t == 0) xscale[row] = am / 127.0f;
+#pragma unroll
+  for (int r = 0; r < kRQMaxRows; ++r) {
+    const float v = pq_wave_max(rmax[r]);
+    if (lane == 0) red[w][r] = v;
+  }
+  __syncthreads();
 
-    for (int v = t; v < (h >> 2); v += NT) {
-      const float4 f = *reinterpret_cast<const float4*>(buf + 4 * v);
-      *reinterpret_cast<uint32_t*>(xq + rbase + 4 * v) = quant4(f.x, f.y, f.z, f.w, inv);
+  // Quantize the row buffer: 8 elements per thread per step (16-byte reads of fp16 rows).
+  const int per_row = h >> 3;
+  for (int e = t; e < nr * per_row; e += kRQWaves * 64) {
+    const int r = e / per_row;
+    const int c8 = (e - r * per_row) * 8;
+    float am = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < kRQWaves; ++ww) am = fmaxf(am, red[ww][r]);
+    const float inv = pqd::inv_scale(am);
+    float f[8];
+    if constexpr (MAT16) {
+      const uint4 u = *reinterpret_cast<const uint4*>(rowbuf + r * h + c8);
+      const uint32_t wds[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f[2 * q] = pq_f16_to_f32(static_cast<uint16_t>(wds[q] & 0xffffu));
+        f[2 * q + 1] = pq_f16_to_f32(static_cast<uint16_t>(wds[q] >> 16));
+      }
+      if (xrot != nullptr) *reinterpret_cast<uint4*>(xrot + (row0 + r) * h + c8) = u;
+    } else {
+      const float4 a = *reinterpret_cast<const float4*>(rowbuf + r * h + c8);
+      const float4 b = *reinterpret_cast<const float4*>(rowbuf + r * h + c8 + 4);
+      f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+      f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
       if (xrot != nullptr) {
-        uint2 o;
-        o.x = pq_f32_to_f16(f.x) | (static_cast<uint32_t>(pq_f32_to_f16(f.y)) << 16);
-        o.y = pq_f32_to_f16(f.z) | (static_cast<uint32_t>(pq_f32_to_f16(f.w)) << 16);
-        *reinterpret_cast<uint2*>(xrot + rbase + 4 * v) = o;
+        uint4 o;
+        o.x = pq_f32_to_f16(f[0]) | (static_cast<uint32_t>(pq_f32_to_f16(f[1])) << 16);
+        o.y = pq_f32_to_f16(f[2]) | (static_cast<uint32_t>(pq_f32_to_f16(f[3])) << 16);
+        o.z = pq_f32_to_f16(f[4]) | (static_cast<uint32_t>(pq_f32_to_f16(f[5])) << 16);
+        o.w = pq_f32_to_f16(f[6]) | (static_cast<uint32_t>(pq_f32_to_f16(f[7])) << 16);
+        *reinterpret_cast<uint4*>(xrot + (row0 + r) * h + c8) = o;
       }
     }
-    __syncthreads();  // buf and red are reused by the next row
+    uint2 o;
+    o.x = quant4(f[0], f[1], f[2], f[3], inv);
+    o.y = quant4(f[4], f[5], f[6], f[7], inv);
+    *reinterpret_cast<uint2*>(xq + (row0 + r) * h + c8) = o;
+    if (c8 == 0) xscale[row0 + r] = am / 127.0f;
   }
 }
 
@@ -235,7 +336,7 @@ __global__ __launch_bounds__(NT) void quant_kernel(const void* __restrict__ x, i
       for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
     }
     const float am = block_max<NT>(amax, red);
-    const float inv = am > 0.0f ? 127.0f / am : 0.0f;
+    const float inv = pqd::inv_scale(am);
     if (t == 0) xscale[row] = am / 127.0f;
     for (int v = t; v < (h >> 3); v += NT) {
       float f[8];
@@ -270,20 +371,36 @@ void launch_rotate_dt(const void* x, void* y, const int16_t* idx, const void* th
 
 constexpr int64_t kMaxGrid = 1 << 20;
 
+// Rows per block: as many as fit a 96 KB row buffer, at most 8.
+inline int rq_rows_per_block(int h, bool mat16) {
+  const int bytes = h * (mat16 ? 2 : 4);
+  int r = (96 * 1024) / bytes;
+  return r < 1 ? 1 : (r > kRQMaxRows ? kRQMaxRows : r);
+}
+
+template <int DT, int KMAX, bool MAT16>
+void launch_rq(const void* x, const uint8_t* pairs, const float* cs, const float* scales, int8_t* xq, float* xscale,
+               void* xrot, int64_t rows, int h, int krot, unsigned flags, hipStream_t stream) {
+  const int R = rq_rows_per_block(h, MAT16);
+  const size_t lds = static_cast<size_t>(kRQWaves) * kRQMaxRows * 128 * sizeof(float) +
+                     static_cast<size_t>(R) * h * (MAT16 ? 2 : 4);
+  const int64_t blocks = (rows + R - 1) / R;
+  rotate_quant_kernel<DT, KMAX, MAT16><<<static_cast<unsigned>(blocks), kRQWaves * 64, lds, stream>>>(
+      x, pairs, reinterpret_cast<const float2*>(cs), scales, xq, xscale, static_cast<uint16_t*>(xrot), rows, h, krot,
+      flags, R);
+}
+
 template <int DT>
 void launch_rotate_quant(const void* x, const uint8_t* pairs, const float* cs, const float* scales, int8_t* xq,
                          float* xscale, void* xrot, int64_t rows, int h, int krot, unsigned flags,
                          hipStream_t stream) {
-  const size_t lds = static_cast<size_t>(h) * sizeof(float);
-  const unsigned grid = static_cast<unsigned>(rows < kMaxGrid ? rows : kMaxGrid);
-  const float2* cs2 = reinterpret_cast<const float2*>(cs);
-  uint16_t* xr = static_cast<uint16_t*>(xrot);
-  if (rows <= 64) {
-    rotate_quant_kernel<DT, 1024><<<grid, 1024, lds, stream>>>(x, pairs, cs2, scales, xq, xscale, xr, rows, h, krot,
-                                                               flags);
+  const bool mat16 = (flags & PQ_RQ_MATERIALIZE_FP16) != 0;
+  if (krot <= 8) {
+    if (mat16) launch_rq<DT, 8, true>(x, pairs, cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
+    else launch_rq<DT, 8, false>(x, pairs, cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
   } else {
-    rotate_quant_kernel<DT, 256><<<grid, 256, lds, stream>>>(x, pairs, cs2, scales, xq, xscale, xr, rows, h, krot,
-                                                             flags);
+    if (mat16) launch_rq<DT, 16, true>(x, pairs, cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
+    else launch_rq<DT, 16, false>(x, pairs, cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
   }
 }
 
@@ -332,9 +449,10 @@ extern "C" int pq_rotate_quant_i8(const void* x, int x_dtype, const uint8_t* pai
              "pq_rotate_quant_i8: unknown flags 0x%x", flags);
   if (rows == 0) return PQ_OK;
   PQ_REQUIRE(x && pairs && cos_sin && xq && xscale, PQ_ERR_ARG, "pq_rotate_quant_i8: null pointer");
-  PQ_REQUIRE(pq::aligned_to(x, 16) && pq::aligned_to(xq, 4) && pq::aligned_to(cos_sin, 8) &&
-                 (xrot == nullptr || pq::aligned_to(xrot, 8)),
-             PQ_ERR_ARG, "pq_rotate_quant_i8: x must be 16-byte, cos_sin 8-byte, xq 4-byte, xrot 8-byte aligned");
+  PQ_REQUIRE(pq::aligned_to(x, 16) && pq::aligned_to(xq, 8) && pq::aligned_to(cos_sin, 8) &&
+                 (xrot == nullptr || pq::aligned_to(xrot, 16)),
+             PQ_ERR_ARG, "pq_rotate_quant_i8: x must be 16-byte, cos_sin 8-byte, xq 8-byte, xrot 16-byte aligned");
+  PQ_REQUIRE(rows <= 0x7fffffffLL, PQ_ERR_ARG, "pq_rotate_quant_i8: too many rows");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int hh = static_cast<int>(h);
   switch (x_dtype) {

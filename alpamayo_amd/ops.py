@@ -358,8 +358,29 @@ def _linear_impl(x, pairs, cos_sin, scales, wpack, wmeta, bias, workspace, input
     dev = x.device
     n, k = _check_weights(wpack, wmeta, dev)
     _require(x.size(-1) == k, f"x has {x.size(-1)} features, the weights expect {k}")
-    xq, xs, _ = _rotate_quant(x, pairs, cos_sin, scales, input_fp16, materialize_fp16, False)
-    y = _gemm_launch(xq, xs, wpack, wmeta, bias, workspace, out_dtype, xq.size(0), n, k, dev)
+    h, krot = _check_rot_params(x, pairs, cos_sin, scales)
+    _require(out_dtype in _DT, f"out_dtype must be float32/float16/bfloat16, got {out_dtype}")
+    xc = x.contiguous()
+    m = xc.numel() // k
+    y = torch.empty((m, n), dtype=out_dtype, device=dev)
+    if bias is not None:
+        _require(bias.dtype in _DT and bias.numel() == n, f"bias must hold {n} float values")
+        _same_device("bias", bias, dev)
+        bias = bias.contiguous()
+    lib = _lib.load()
+    need = int(lib.pq_w4a8_linear_workspace_size(m, n, k, krot))
+    scratch = torch.empty(need, dtype=torch.uint8, device=dev) if need > 0 else None
+    flags = (_lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0) | (_lib.PQ_RQ_MATERIALIZE_FP16 if materialize_fp16 else 0)
+    pc, cc = pairs.contiguous(), cos_sin.contiguous()
+    sc = scales.contiguous() if scales is not None else None
+    with _DeviceGuard(dev):
+        st = lib.pq_w4a8_linear(xc.data_ptr(), _DT[x.dtype], pc.data_ptr(), cc.data_ptr(),
+                                sc.data_ptr() if sc is not None else None, wpack.data_ptr(), wmeta.data_ptr(),
+                                bias.data_ptr() if bias is not None else None,
+                                _DT[bias.dtype] if bias is not None else 0, y.data_ptr(), _DT[out_dtype], m, n, k,
+                                krot, flags, scratch.data_ptr() if scratch is not None else None, need,
+                                _stream(dev))
+    _lib.check(st, "paroquant::w4a8_linear")
     return y.view(*x.shape[:-1], n)
 
 

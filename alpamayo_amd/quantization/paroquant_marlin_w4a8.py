@@ -191,7 +191,9 @@ class MarlinW4A8Linear(nn.Module):
         self.register_buffer("g_idx", torch.empty(0, dtype=torch.int32))
         self.register_buffer("g_idx_sort_indices", torch.empty(0, dtype=torch.int32))
         self.register_buffer("input_global_scale", torch.ones(1, dtype=torch.float32))
-        self.bias = None
+        # registered up front so load_from_awq can assign it (the reference's
+        # register_buffer after `self.bias = None` raises KeyError for biased layers)
+        self.register_buffer("bias", None)
 
     @torch.no_grad()
     def load_from_awq(self, awq_qweight, awq_scales, awq_qzeros, bias=None):
@@ -211,10 +213,7 @@ class MarlinW4A8Linear(nn.Module):
         self.input_global_scale = torch.ones(1, dtype=torch.float32, device=dev)
         ws = max(_ops.workspace_bytes(m, N, K) for m in range(1, _WORKSPACE_MAX_M + 1))
         self.workspace = torch.zeros(max(ws, 1), dtype=torch.uint8, device=dev)
-        if bias is not None:
-            self.register_buffer("bias", bias.to(dev).contiguous())
-        else:
-            self.bias = None
+        self.bias = bias.to(dev).contiguous() if bias is not None else None
 
     def _check_loaded(self):
         if self.qweight.numel() == 0:

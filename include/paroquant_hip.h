@@ -22,6 +22,11 @@
  *   pq_w4a8_gemm         the Marlin int4 x int8 GEMM (same call site, launch #4)
  *   pq_w4a8_prepack      MarlinW4A8Linear.load_from_awq's repack of AWQ
  *                        buffers (paroquant_marlin_w4a8.py:274-312)
+ *   pq_w4a8_linear       the whole linear of a converted layer:
+ *                        BF16RotateLinearWrapper -> RotateLinearInt4 ->
+ *                        rotation::rotate -> MarlinW4A8Linear.forward
+ *                        (paroquant_marlin_w4a8.py:59-65, 314-333;
+ *                        rotation_linear.py:120-124)
  */
 #ifndef PAROQUANT_HIP_H
 #define PAROQUANT_HIP_H
@@ -80,10 +85,10 @@ int pq_rotate_quant_i8(const void* x, int x_dtype, const uint8_t* pairs, const f
 int pq_quant_i8(const void* x, int x_dtype, int8_t* xq, float* xscale, int64_t rows, int64_t h,
                 void* stream);
 
-/* Bytes of workspace pq_w4a8_gemm needs for this shape (0 if none).
- * The workspace must be zero-filled once before its first use; every call
- * leaves it zero-filled again, so it can be reused by later calls on the
- * same stream.  Calls that overlap in time must not share a workspace. */
+/* Bytes of workspace pq_w4a8_gemm needs for this shape.  No kernel of this
+ * version exchanges data between workgroups, so this is 0 and the workspace
+ * arguments of pq_w4a8_gemm are ignored; they stay in the ABI for kernels
+ * that may need one (a non-zero size would come with its own rules). */
 size_t pq_w4a8_workspace_size(int64_t m, int64_t n, int64_t k, int group_size);
 
 /* y[m, n] = xscale[m] * sum_g s[g, n] * sum_{k in g} (q[k, n] - z[g, n]) * xq[m, k]
@@ -112,6 +117,22 @@ int pq_w4a8_gemm_partials(const int8_t* xq, const uint8_t* wpack, const uint32_t
 int pq_w4a8_prepack(const int32_t* awq_qweight, const uint16_t* awq_scales,
                     const int32_t* awq_qzeros, uint8_t* wpack, uint32_t* wmeta, int64_t k,
                     int64_t n, int group_size, void* stream);
+
+/* Bytes of scratch pq_w4a8_linear needs (0 when it runs as one fused kernel:
+ * m <= 4 with krot <= 8 and small enough k; otherwise the int8 activations
+ * and their scales, m*k rounded up to 256 plus 4*m bytes).  The scratch is
+ * written before it is read; its content does not matter. */
+size_t pq_w4a8_linear_workspace_size(int64_t m, int64_t n, int64_t k, int krot);
+
+/* y = W4A8 GEMM of the per-token int8 quantization of the rotation of x:
+ * x [m, k] (x_dtype) -> y [m, n] (y_dtype), rotation operands as for
+ * pq_rotate_quant_i8, weights as for pq_w4a8_gemm, flags PQ_RQ_*.
+ * k <= 16384.  Same results as pq_rotate_quant_i8 followed by pq_w4a8_gemm.
+ * Reference: paroquant_marlin_w4a8.py:59-65, 314-333; rotation_linear.py:120-124. */
+int pq_w4a8_linear(const void* x, int x_dtype, const uint8_t* pairs, const float* cos_sin, const float* scales,
+                   const uint8_t* wpack, const uint32_t* wmeta, const void* bias, int bias_dtype, void* y,
+                   int y_dtype, int64_t m, int64_t n, int64_t k, int krot, unsigned flags, void* workspace,
+                   size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -62,23 +62,41 @@ def test_rotate_quant_and_gemm_argument_checks():
     assert lib.pq_w4a8_gemm(p, p, p, p, None, 0, p, 2, 4, 60, 256, 128, None, 0, None) == 1
     assert lib.pq_w4a8_gemm(p, p, p, p, None, 0, p, 2, 4, 64, 200, 128, None, 0, None) == 1
     assert lib.pq_w4a8_gemm(p, p, p, p, None, 0, p, 9, 4, 64, 256, 128, None, 0, None) == 2
-    need = lib.pq_w4a8_workspace_size(1, 1024, 4096, 128)
-    assert need > 0
-    assert lib.pq_w4a8_gemm(p, p, p, p, None, 0, p, 2, 1, 1024, 4096, 128, None, 0, None) == 4
-    assert "workspace" in _err(lib)
-    assert lib.pq_w4a8_gemm(p, p, p, p, None, 0, p, 2, 1, 1024, 4096, 128, p, need - 1, None) == 4
     assert lib.pq_w4a8_prepack(p, p, p, p, p, 100, 64, 128, None) == 1
     assert lib.pq_w4a8_gemm_partials(p, p, p, p, 0, 64, 256, 128, None) == 0
 
 
+def test_linear_argument_checks():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    args = lambda m, k, krot, flags, ws, wsb: (p, 2, p, p, None, p, p, None, 0, p, 2, m, 4096, k, krot, flags, ws, wsb,
+                                              None)
+    assert lib.pq_w4a8_linear(*args(1, 200, 8, 3, None, 0)) == 1
+    assert lib.pq_w4a8_linear(*args(1, 4096, 0, 3, None, 0)) == 2
+    assert lib.pq_w4a8_linear(*args(1, 4096, 8, 4, None, 0)) == 1
+    assert lib.pq_w4a8_linear(*args(1, 32768, 8, 3, None, 0)) == 1
+    assert lib.pq_w4a8_linear(*args(0, 4096, 8, 3, None, 0)) == 0
+    need = lib.pq_w4a8_linear_workspace_size(64, 4096, 4096, 8)
+    assert need == 64 * 4096 + 64 * 4
+    assert lib.pq_w4a8_linear(*args(64, 4096, 8, 3, None, 0)) == 4
+    assert "workspace" in _err(lib)
+    assert lib.pq_w4a8_linear(*args(64, 4096, 8, 3, p, need - 1)) == 4
+    assert lib.pq_w4a8_linear(*args(64, 4096, 8, 3, ctypes.c_void_p(272), need)) == 4   # not 256-aligned
+
+
 def test_workspace_size_rules():
     lib = _lib.load()
-    assert lib.pq_w4a8_workspace_size(64, 4096, 4096, 128) == 0        # tiled path needs none
-    assert lib.pq_w4a8_workspace_size(1, 64, 100, 128) == 0            # invalid shape -> 0
-    for m in (1, 4, 16):
+    for m in (1, 4, 16, 3072):
         for n, k in ((1024, 4096), (4096, 4096), (12288, 4096), (4096, 12288)):
-            ws = lib.pq_w4a8_workspace_size(m, n, k, 128)
-            assert ws == 0 or ws >= 4096 + m * n * 4
+            assert lib.pq_w4a8_workspace_size(m, n, k, 128) == 0        # no inter-workgroup exchange
+    # the one-kernel decode path needs no scratch; the two-kernel path holds xq and xscale
+    assert lib.pq_w4a8_linear_workspace_size(1, 4096, 4096, 8) == 0
+    assert lib.pq_w4a8_linear_workspace_size(4, 4096, 4096, 8) == 0
+    assert lib.pq_w4a8_linear_workspace_size(1, 4096, 12288, 8) == 0
+    assert lib.pq_w4a8_linear_workspace_size(1, 4096, 4096, 16) == 4096 + 4     # krot 16: two kernels
+    assert lib.pq_w4a8_linear_workspace_size(4, 4096, 12288, 8) == 4 * 12288 + 16
+    assert lib.pq_w4a8_linear_workspace_size(5, 4096, 4096, 8) == 5 * 4096 + 20
+    assert lib.pq_w4a8_linear_workspace_size(3, 64, 100, 8) == 0       # invalid shape -> 0
 
 
 def test_status_names_and_error_type():

@@ -3,6 +3,8 @@ RotateLinearInt4 / MarlinW4A8Linear / BF16RotateLinearWrapper call chain,
 paroquant_marlin_w4a8.py:59-65, 314-333; rotation_linear.py:120-124) on the
 benchmark configurations, against the oracle."""
 
+import zlib
+
 import numpy as np
 import pytest
 import torch
@@ -19,6 +21,7 @@ from alpamayo_amd.quantization import (
 )
 from oracle import gemm as ogemm
 from oracle import linear as olin
+from oracle import quant as oquant
 from oracle import rotation as orot
 from tests.gpu_util import assert_bf16_close, assert_codes_close, rel_fro, to_np
 
@@ -177,3 +180,29 @@ def test_config3_chain_two_layers_m16():
         a = h + d
     torch.cuda.synchronize()
     assert torch.isfinite(a.float()).all()
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("N,K", [(16, 128), (48, 2048), (1024, 12288), (12288, 4096)])
+@pytest.mark.parametrize("krot,flags", [(8, (True, True)), (1, (False, True)), (8, (True, False)), (16, (True, True))])
+def test_linear_op_decode_paths(M, N, K, krot, flags):
+    """paroquant::w4a8_linear (one fused kernel for M <= 4, krot <= 8; two kernels otherwise)."""
+    print(f"linear op M={M} N={N} K={K} krot={krot} flags={flags}", flush=True)
+    g = workloads.generator(zlib.crc32(f"{M}{N}{K}{krot}{flags}".encode()))
+    spec = workloads.linear_spec("x", N, K, g, keep_codes=True)
+    pairs = torch.cat([spec.pairs] * 2)[:krot]
+    theta = torch.cat([spec.theta] * 2)[:krot]
+    c, s = orot.cos_sin_table(theta.numpy())
+    cos_sin = torch.from_numpy(np.stack([c, s], axis=-1)).contiguous()
+    scales = spec.channel_scales.float().reshape(-1)
+    wp, wm = torch.ops.paroquant.w4a8_prepack(spec.w.awq_qweight.cuda(), spec.w.awq_scales.cuda(),
+                                              spec.w.awq_qzeros.cuda())
+    bias = torch.randn(N, generator=g).to(torch.bfloat16)
+    x = workloads.activations(M, K, g)
+    y = torch.ops.paroquant.w4a8_linear(x.cuda(), pairs.to(torch.uint8).cuda(), cos_sin.cuda(), scales.cuda(), wp, wm,
+                                        bias.cuda(), None, flags[0], flags[1], torch.bfloat16)
+    v = orot.rotate_path_f32(to_np(x), pairs.numpy(), c, s, scales.numpy(), 128, flags[0], flags[1])
+    q, sx = oquant.quant_int8_per_token(v)
+    ref = ogemm.w4a8_linear(q, sx, spec.w.codes.numpy(), spec.w.awq_scales.numpy(), spec.w.zeros.numpy(),
+                            bias.float().numpy())
+    assert_bf16_close(to_np(y), ref)
