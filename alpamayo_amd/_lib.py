@@ -22,6 +22,7 @@ PQ_RQ_INPUT_FP16 = 1
 PQ_RQ_MATERIALIZE_FP16 = 2
 
 STATUS_NAMES = {0: "PQ_OK", 1: "PQ_ERR_ARG", 2: "PQ_ERR_UNSUPPORTED", 3: "PQ_ERR_HIP", 4: "PQ_ERR_WORKSPACE"}
+STATUS_CODE = {v: k for k, v in STATUS_NAMES.items()}
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -40,6 +41,7 @@ SIGNATURES = {
     "pq_w4a8_gemm": (_INT, [_P, _P, _P, _P, _P, _INT, _P, _INT, _I64, _I64, _I64, _INT, _P, _SZ, _P]),
     "pq_w4a8_gemm_partials": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
     "pq_w4a8_prepack": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _INT, _P]),
+    "pq_rotation_pack": (_INT, [_P, _P, _I64, _INT, _P, _P]),
     "pq_w4a8_linear_workspace_size": (_SZ, [_I64, _I64, _I64, _INT]),
     "pq_w4a8_linear": (_INT, [_P, _INT, _P, _P, _P, _P, _P, _P, _INT, _P, _INT, _I64, _I64, _I64, _INT, _UINT, _P, _SZ,
                               _P]),

@@ -22,7 +22,8 @@ using pqd::quant4;
 namespace {
 
 constexpr int kRotRows = 4;   // rows per workgroup of the plain rotation kernel
-constexpr int kMaxKrot = 16;  // rotation layers the fused kernel holds in registers
+
+#define PQ_LDS_WAVE_FENCE() __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront", "local")
 
 // ---------------------------------------------------------------------------
 // rotation::rotate.  One wave per (4 rows x 128 channels); lane t owns pair t
@@ -130,73 +131,93 @@ __device__ __forceinline__ void load8(const void* base, int64_t elem, float f[8]
   }
 }
 
-// Orders this wave's LDS accesses across a Givens layer.  The wave's LDS
-// instructions already execute in order; this only stops the compiler from
-// moving them (it emits no wait on global loads).
-#define PQ_LDS_WAVE_FENCE() __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront", "local")
 
-// All KMAX layers' pair indices and (cos, sin) of one group, for lane = pair.
-// Layers past krot re-read layer krot-1 so every load is unconditional (the
-// loads then issue back to back instead of one round trip per layer).
-template <int KMAX>
-__device__ __forceinline__ void load_group_params(const uint8_t* __restrict__ pairs, const float2* __restrict__ cs,
-                                                  int h, int krot, int g, int lane, uint32_t (&pr)[KMAX],
-                                                  float2 (&cc)[KMAX]) {
+// One lane's packed rotation parameters for one group: KP layers of
+// (first | second << 8) in 16-byte words and of (cos, sin).  Layout (built by
+// pq_rotation_pack): rot_ij [G][64][KP] uint16, rot_cs [G][64][KP][2] float.
+template <int KP>
+struct LaneParams {
+  uint32_t ij[KP / 2];
+  float cs[2 * KP];
+};
+
+template <int KP>
+__device__ __forceinline__ void load_lane_params(const uint16_t* __restrict__ rot_ij, const float* __restrict__ rot_cs,
+                                                 int g, int lane, LaneParams<KP>& p) {
+  const int64_t o = (static_cast<int64_t>(g) * 64 + lane) * KP;
+  const uint4* ij = reinterpret_cast<const uint4*>(rot_ij + o);
 #pragma unroll
-  for (int r = 0; r < KMAX; ++r) {
-    const int rr = r < krot ? r : krot - 1;
-    pr[r] = *reinterpret_cast<const uint16_t*>(pairs + static_cast<int64_t>(rr) * h + g * 128 + 2 * lane);
-    cc[r] = cs[static_cast<int64_t>(rr) * (h >> 1) + g * 64 + lane];
+  for (int q = 0; q < KP / 8; ++q) {
+    const uint4 v = ij[q];
+    p.ij[4 * q] = v.x;
+    p.ij[4 * q + 1] = v.y;
+    p.ij[4 * q + 2] = v.z;
+    p.ij[4 * q + 3] = v.w;
+  }
+  const float4* cs = reinterpret_cast<const float4*>(rot_cs + 2 * o);
+#pragma unroll
+  for (int q = 0; q < KP / 2; ++q) {
+    const float4 v = cs[q];
+    p.cs[4 * q] = v.x;
+    p.cs[4 * q + 1] = v.y;
+    p.cs[4 * q + 2] = v.z;
+    p.cs[4 * q + 3] = v.w;
   }
 }
 
+template <int KP>
+__device__ __forceinline__ int pair_first(const LaneParams<KP>& p, int r) {
+  return (p.ij[r >> 1] >> (16 * (r & 1))) & 127;
+}
+template <int KP>
+__device__ __forceinline__ int pair_second(const LaneParams<KP>& p, int r) {
+  return (p.ij[r >> 1] >> (16 * (r & 1) + 8)) & 127;
+}
+
 // ---------------------------------------------------------------------------
-// Fused rotate + quant over blocks of R rows.  512 threads; wave w rotates
-// groups w, w+8, ... for all R rows of the block in a private fp32 scratch
-// [R][128] (lane t owns pair t; the R rows give R independent LDS chains per
-// layer), and stores the finished values in a row buffer [R][h] (fp16 when
-// the result is materialized in fp16, fp32 otherwise).  The next group's
-// parameters and inputs are requested before the current group's layers
-// run.  After a block-wide absmax per row, the row buffer is quantized with
-// coalesced stores.  Parameters are read once per group per R rows.
+// Fused rotate + quant over blocks of RB rows (RB a compile-time constant:
+// the RB rows are RB independent LDS chains per layer, with no per-row
+// branches).  512 threads; wave w rotates groups w, w+8, ... for the block's
+// rows in a private fp32 scratch [RB][128] (lane t owns the pair the packed
+// parameters give it; the packed order makes each layer's LDS accesses
+// bank-conflict free) and stores the finished values in a row buffer
+// [RB][h] (fp16 when the result is materialized in fp16, fp32 otherwise).
+// The next group's parameters and inputs are requested before the current
+// group's layers run.  After a block-wide absmax per row the row buffer is
+// quantized with coalesced stores.  Parameters are read once per group per
+// RB rows.
 // ---------------------------------------------------------------------------
 constexpr int kRQWaves = 8;
-constexpr int kRQMaxRows = 8;
 
-template <int DT, int KMAX, bool MAT16>
+template <int DT, int KP, bool MAT16, int RB>
 __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(
-    const void* __restrict__ x, const uint8_t* __restrict__ pairs, const float2* __restrict__ cs,
+    const void* __restrict__ x, const uint16_t* __restrict__ rot_ij, const float* __restrict__ rot_cs,
     const float* __restrict__ scales, int8_t* __restrict__ xq, float* __restrict__ xscale,
-    uint16_t* __restrict__ xrot, int64_t rows, int h, int krot, unsigned flags, int R) {
+    uint16_t* __restrict__ xrot, int64_t row_begin, int h, int krot, unsigned flags) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
-  __shared__ float red[kRQWaves][kRQMaxRows];
+  __shared__ float red[kRQWaves][RB];
   using RowT = typename std::conditional<MAT16, uint16_t, float>::type;
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int w = t >> 6;
   const bool in16 = (flags & PQ_RQ_INPUT_FP16) != 0;
   const int G = h >> 7;
-  float* scratch = reinterpret_cast<float*>(lds_raw) + w * (kRQMaxRows * 128);
-  RowT* rowbuf = reinterpret_cast<RowT*>(lds_raw + kRQWaves * kRQMaxRows * 128 * sizeof(float));
+  float* scratch = reinterpret_cast<float*>(lds_raw) + w * (RB * 128);
+  RowT* rowbuf = reinterpret_cast<RowT*>(lds_raw + kRQWaves * RB * 128 * sizeof(float));
+  const int64_t row0 = row_begin + static_cast<int64_t>(blockIdx.x) * RB;
 
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
-  const int nr = static_cast<int>(rows - row0 < R ? rows - row0 : R);
-  float rmax[kRQMaxRows];
+  float rmax[RB];
 #pragma unroll
-  for (int r = 0; r < kRQMaxRows; ++r) rmax[r] = 0.0f;
+  for (int r = 0; r < RB; ++r) rmax[r] = 0.0f;
 
-  uint32_t pr[KMAX], prn[KMAX];
-  float2 cc[KMAX], ccn[KMAX];
-  float xa[kRQMaxRows], xb[kRQMaxRows], xan[kRQMaxRows], xbn[kRQMaxRows];
+  LaneParams<KP> cur, nxt;
+  float xa[RB], xb[RB], xan[RB], xbn[RB];
   float sa = 1.0f, sb = 1.0f, san = 1.0f, sbn = 1.0f;
-
-  // Inputs of group g for the block's rows (row indices clamped to valid rows).
-  auto load_inputs = [&](int g, float (&va)[kRQMaxRows], float (&vb)[kRQMaxRows], float& s0, float& s1) {
+  auto load_inputs = [&](int g, float (&va)[RB], float (&vb)[RB], float& s0, float& s1) {
 #pragma unroll
-    for (int r = 0; r < kRQMaxRows; ++r) {
-      const int64_t row = row0 + (r < nr ? r : nr - 1);
-      va[r] = pq_load_as_f32<DT>(x, row * h + g * 128 + lane);
-      vb[r] = pq_load_as_f32<DT>(x, row * h + g * 128 + 64 + lane);
+    for (int r = 0; r < RB; ++r) {
+      va[r] = pq_load_as_f32<DT>(x, (row0 + r) * h + g * 128 + lane);
+      vb[r] = pq_load_as_f32<DT>(x, (row0 + r) * h + g * 128 + 64 + lane);
     }
     if (scales != nullptr) {
       s0 = scales[g * 128 + lane];
@@ -205,66 +226,63 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(
   };
 
   if (w < G) {
-    load_group_params<KMAX>(pairs, cs, h, krot, w, lane, pr, cc);
+    load_lane_params<KP>(rot_ij, rot_cs, w, lane, cur);
     load_inputs(w, xa, xb, sa, sb);
   }
   for (int g = w; g < G; g += kRQWaves) {
     const int gn = (g + kRQWaves < G) ? g + kRQWaves : g;   // clamped: the loads stay unconditional
-    load_group_params<KMAX>(pairs, cs, h, krot, gn, lane, prn, ccn);
+    load_lane_params<KP>(rot_ij, rot_cs, gn, lane, nxt);
     load_inputs(gn, xan, xbn, san, sbn);
 
 #pragma unroll
-    for (int r = 0; r < kRQMaxRows; ++r) {
-      if (r < nr) {
-        const float a = in16 ? pq_round_f16(xa[r]) : xa[r];
-        const float b = in16 ? pq_round_f16(xb[r]) : xb[r];
-        scratch[r * 128 + lane] = a * sa;
-        scratch[r * 128 + 64 + lane] = b * sb;
-      }
+    for (int r = 0; r < RB; ++r) {
+      const float a = in16 ? pq_round_f16(xa[r]) : xa[r];
+      const float b = in16 ? pq_round_f16(xb[r]) : xb[r];
+      scratch[r * 128 + lane] = a * sa;
+      scratch[r * 128 + 64 + lane] = b * sb;
     }
     PQ_LDS_WAVE_FENCE();
-    float ni[kRQMaxRows], nj[kRQMaxRows];
+    float ni[RB], nj[RB];
     int i = 0, j = 0;
 #pragma unroll
-    for (int k = 0; k < KMAX; ++k) {
+    for (int k = 0; k < KP; ++k) {
       if (k < krot) {
-        i = pr[k] & 127;
-        j = (pr[k] >> 8) & 127;
+        i = pair_first(cur, k);
+        j = pair_second(cur, k);
+        const float c = cur.cs[2 * k], sn = cur.cs[2 * k + 1];
+        float xi[RB], xj[RB];
 #pragma unroll
-        for (int r = 0; r < kRQMaxRows; ++r) {
-          if (r < nr) {
-            pqd::givens(scratch[r * 128 + i], scratch[r * 128 + j], cc[k].x, cc[k].y, ni[r], nj[r]);
-            scratch[r * 128 + i] = ni[r];
-            scratch[r * 128 + j] = nj[r];
-          }
+        for (int r = 0; r < RB; ++r) {
+          xi[r] = scratch[r * 128 + i];
+          xj[r] = scratch[r * 128 + j];
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+          pqd::givens(xi[r], xj[r], c, sn, ni[r], nj[r]);
+          scratch[r * 128 + i] = ni[r];
+          scratch[r * 128 + j] = nj[r];
         }
         PQ_LDS_WAVE_FENCE();
       }
     }
 #pragma unroll
-    for (int r = 0; r < kRQMaxRows; ++r) {
-      if (r < nr) {
-        float vi = ni[r], vj = nj[r];
-        if constexpr (MAT16) {
-          const uint16_t hi = pq_f32_to_f16(vi), hj = pq_f32_to_f16(vj);
-          rowbuf[r * h + g * 128 + i] = hi;
-          rowbuf[r * h + g * 128 + j] = hj;
-          vi = pq_f16_to_f32(hi);
-          vj = pq_f16_to_f32(hj);
-        } else {
-          rowbuf[r * h + g * 128 + i] = vi;
-          rowbuf[r * h + g * 128 + j] = vj;
-        }
-        rmax[r] = fmaxf(rmax[r], fmaxf(fabsf(vi), fabsf(vj)));
+    for (int r = 0; r < RB; ++r) {
+      float vi = ni[r], vj = nj[r];
+      if constexpr (MAT16) {
+        const uint16_t hi = pq_f32_to_f16(vi), hj = pq_f32_to_f16(vj);
+        rowbuf[r * h + g * 128 + i] = hi;
+        rowbuf[r * h + g * 128 + j] = hj;
+        vi = pq_f16_to_f32(hi);
+        vj = pq_f16_to_f32(hj);
+      } else {
+        rowbuf[r * h + g * 128 + i] = vi;
+        rowbuf[r * h + g * 128 + j] = vj;
       }
+      rmax[r] = fmaxf(rmax[r], fmaxf(fabsf(vi), fabsf(vj)));
     }
+    cur = nxt;
 #pragma unroll
-    for (int k = 0; k < KMAX; ++k) {
-      pr[k] = prn[k];
-      cc[k] = ccn[k];
-    }
-#pragma unroll
-    for (int r = 0; r < kRQMaxRows; ++r) {
+    for (int r = 0; r < RB; ++r) {
       xa[r] = xan[r];
       xb[r] = xbn[r];
     }
@@ -273,15 +291,15 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(
   }
 
 #pragma unroll
-  for (int r = 0; r < kRQMaxRows; ++r) {
+  for (int r = 0; r < RB; ++r) {
     const float v = pq_wave_max(rmax[r]);
     if (lane == 0) red[w][r] = v;
   }
   __syncthreads();
 
-  // Quantize the row buffer: 8 elements per thread per step (16-byte reads of fp16 rows).
+  // Quantize the row buffer: 8 elements per thread per step.
   const int per_row = h >> 3;
-  for (int e = t; e < nr * per_row; e += kRQWaves * 64) {
+  for (int e = t; e < RB * per_row; e += kRQWaves * 64) {
     const int r = e / per_row;
     const int c8 = (e - r * per_row) * 8;
     float am = 0.0f;
@@ -371,36 +389,52 @@ void launch_rotate_dt(const void* x, void* y, const int16_t* idx, const void* th
 
 constexpr int64_t kMaxGrid = 1 << 20;
 
-// Rows per block: as many as fit a 96 KB row buffer, at most 8.
-inline int rq_rows_per_block(int h, bool mat16) {
-  const int bytes = h * (mat16 ? 2 : 4);
-  int r = (96 * 1024) / bytes;
-  return r < 1 ? 1 : (r > kRQMaxRows ? kRQMaxRows : r);
+// Rows per block: more rows per block read the parameters fewer times, fewer
+// keep enough blocks in flight; the row buffer stays within 96 KB.
+inline int rq_rows_per_block(int64_t rows, int h, bool mat16) {
+  int rb = rows >= 4096 ? 8 : rows >= 1024 ? 4 : rows >= 256 ? 2 : 1;
+  while (rb > 1 && static_cast<int64_t>(rb) * h * (mat16 ? 2 : 4) > 96 * 1024) rb >>= 1;
+  return rb;
 }
 
-template <int DT, int KMAX, bool MAT16>
-void launch_rq(const void* x, const uint8_t* pairs, const float* cs, const float* scales, int8_t* xq, float* xscale,
-               void* xrot, int64_t rows, int h, int krot, unsigned flags, hipStream_t stream) {
-  const int R = rq_rows_per_block(h, MAT16);
-  const size_t lds = static_cast<size_t>(kRQWaves) * kRQMaxRows * 128 * sizeof(float) +
-                     static_cast<size_t>(R) * h * (MAT16 ? 2 : 4);
-  const int64_t blocks = (rows + R - 1) / R;
-  rotate_quant_kernel<DT, KMAX, MAT16><<<static_cast<unsigned>(blocks), kRQWaves * 64, lds, stream>>>(
-      x, pairs, reinterpret_cast<const float2*>(cs), scales, xq, xscale, static_cast<uint16_t*>(xrot), rows, h, krot,
-      flags, R);
+template <int DT, int KP, bool MAT16, int RB>
+void launch_rq_rb(const void* x, const uint16_t* rot_ij, const float* rot_cs, const float* scales, int8_t* xq,
+                  float* xscale, void* xrot, int64_t row_begin, int64_t nblocks, int h, int krot, unsigned flags,
+                  hipStream_t stream) {
+  if (nblocks <= 0) return;
+  const size_t lds = static_cast<size_t>(kRQWaves) * RB * 128 * sizeof(float) +
+                     static_cast<size_t>(RB) * h * (MAT16 ? 2 : 4);
+  rotate_quant_kernel<DT, KP, MAT16, RB><<<static_cast<unsigned>(nblocks), kRQWaves * 64, lds, stream>>>(
+      x, rot_ij, rot_cs, scales, xq, xscale, static_cast<uint16_t*>(xrot), row_begin, h, krot, flags);
+}
+
+template <int DT, int KP, bool MAT16>
+void launch_rq(const void* x, const uint16_t* rot_ij, const float* rot_cs, const float* scales, int8_t* xq,
+               float* xscale, void* xrot, int64_t rows, int h, int krot, unsigned flags, hipStream_t stream) {
+  const int rb = rq_rows_per_block(rows, h, MAT16);
+  const int64_t full = rows / rb;
+  switch (rb) {
+    case 8: launch_rq_rb<DT, KP, MAT16, 8>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, 0, full, h, krot, flags, stream); break;
+    case 4: launch_rq_rb<DT, KP, MAT16, 4>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, 0, full, h, krot, flags, stream); break;
+    case 2: launch_rq_rb<DT, KP, MAT16, 2>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, 0, full, h, krot, flags, stream); break;
+    default: break;
+  }
+  const int64_t done = rb > 1 ? full * rb : 0;   // the remaining rows, one block each
+  launch_rq_rb<DT, KP, MAT16, 1>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, done, rows - done, h, krot, flags,
+                                 stream);
 }
 
 template <int DT>
-void launch_rotate_quant(const void* x, const uint8_t* pairs, const float* cs, const float* scales, int8_t* xq,
+void launch_rotate_quant(const void* x, const uint16_t* rot_ij, const float* rot_cs, const float* scales, int8_t* xq,
                          float* xscale, void* xrot, int64_t rows, int h, int krot, unsigned flags,
                          hipStream_t stream) {
   const bool mat16 = (flags & PQ_RQ_MATERIALIZE_FP16) != 0;
   if (krot <= 8) {
-    if (mat16) launch_rq<DT, 8, true>(x, pairs, cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
-    else launch_rq<DT, 8, false>(x, pairs, cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
+    if (mat16) launch_rq<DT, 8, true>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
+    else launch_rq<DT, 8, false>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
   } else {
-    if (mat16) launch_rq<DT, 16, true>(x, pairs, cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
-    else launch_rq<DT, 16, false>(x, pairs, cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
+    if (mat16) launch_rq<DT, 16, true>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
+    else launch_rq<DT, 16, false>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
   }
 }
 
@@ -437,28 +471,29 @@ extern "C" int pq_rotate(const void* x, void* y, const int16_t* idx_ij, const vo
   return pq::launch_status("pq_rotate launch");
 }
 
-extern "C" int pq_rotate_quant_i8(const void* x, int x_dtype, const uint8_t* pairs, const float* cos_sin,
+extern "C" int pq_rotate_quant_i8(const void* x, int x_dtype, const uint16_t* rot_ij, const float* rot_cs,
                                   const float* scales, int8_t* xq, float* xscale, void* xrot, int64_t rows,
                                   int64_t h, int krot, unsigned flags, void* stream) {
-  PQ_REQUIRE(rows >= 0 && h > 0 && h % 128 == 0 && h <= 16384, PQ_ERR_ARG,
-             "pq_rotate_quant_i8: need h %% 128 == 0 and 0 < h <= 16384 (h=%lld)", (long long)h);
+  PQ_REQUIRE(rows >= 0 && rows <= 0x7fffffffLL && h > 0 && h % 128 == 0 && h <= 16384, PQ_ERR_ARG,
+             "pq_rotate_quant_i8: need h %% 128 == 0 and 0 < h <= 16384 (h=%lld, rows=%lld)", (long long)h,
+             (long long)rows);
   PQ_REQUIRE(krot >= 1 && krot <= 16, PQ_ERR_UNSUPPORTED, "pq_rotate_quant_i8: krot=%d not in 1..16", krot);
   PQ_REQUIRE(x_dtype == PQ_F32 || x_dtype == PQ_F16 || x_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED,
              "pq_rotate_quant_i8: dtype code %d", x_dtype);
   PQ_REQUIRE((flags & ~(PQ_RQ_INPUT_FP16 | PQ_RQ_MATERIALIZE_FP16)) == 0, PQ_ERR_ARG,
              "pq_rotate_quant_i8: unknown flags 0x%x", flags);
   if (rows == 0) return PQ_OK;
-  PQ_REQUIRE(x && pairs && cos_sin && xq && xscale, PQ_ERR_ARG, "pq_rotate_quant_i8: null pointer");
-  PQ_REQUIRE(pq::aligned_to(x, 16) && pq::aligned_to(xq, 8) && pq::aligned_to(cos_sin, 8) &&
-                 (xrot == nullptr || pq::aligned_to(xrot, 16)),
-             PQ_ERR_ARG, "pq_rotate_quant_i8: x must be 16-byte, cos_sin 8-byte, xq 8-byte, xrot 16-byte aligned");
-  PQ_REQUIRE(rows <= 0x7fffffffLL, PQ_ERR_ARG, "pq_rotate_quant_i8: too many rows");
+  PQ_REQUIRE(x && rot_ij && rot_cs && xq && xscale, PQ_ERR_ARG, "pq_rotate_quant_i8: null pointer");
+  PQ_REQUIRE(pq::aligned_to(x, 16) && pq::aligned_to(xq, 8) && pq::aligned_to(rot_ij, 16) &&
+                 pq::aligned_to(rot_cs, 16) && (xrot == nullptr || pq::aligned_to(xrot, 16)),
+             PQ_ERR_ARG,
+             "pq_rotate_quant_i8: x, rot_ij, rot_cs and xrot must be 16-byte aligned, xq 8-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int hh = static_cast<int>(h);
   switch (x_dtype) {
-    case PQ_F32: launch_rotate_quant<PQ_F32>(x, pairs, cos_sin, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
-    case PQ_F16: launch_rotate_quant<PQ_F16>(x, pairs, cos_sin, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
-    default: launch_rotate_quant<PQ_BF16>(x, pairs, cos_sin, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
+    case PQ_F32: launch_rotate_quant<PQ_F32>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
+    case PQ_F16: launch_rotate_quant<PQ_F16>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
+    default: launch_rotate_quant<PQ_BF16>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
   }
   return pq::launch_status("pq_rotate_quant_i8 launch");
 }

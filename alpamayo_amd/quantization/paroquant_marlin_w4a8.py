@@ -27,7 +27,8 @@ addresses, as in the reference 262-271):
   qweight    uint8 [N/16, K/128, 64, 16]   packed int4 codes
   scales     int32 [N/16, K/128, 16]       fp16 group scale | zero point << 16
   qzeros     empty (zero points live in ``scales``)
-  workspace  uint8                          split-K scratch for M <= 16 (zero at rest)
+  workspace  uint8                          scratch of paroquant::w4a8_linear for M <= 16
+                                            (int8 codes and scales between its two kernels)
   g_idx, g_idx_sort_indices   empty int32 (no act-order), kept for API parity
   input_global_scale          float32 [1] = 1 (the fp16 scales are used as is)
 """
@@ -211,7 +212,8 @@ class MarlinW4A8Linear(nn.Module):
         self.g_idx = torch.empty(0, dtype=torch.int32, device=dev)
         self.g_idx_sort_indices = torch.empty(0, dtype=torch.int32, device=dev)
         self.input_global_scale = torch.ones(1, dtype=torch.float32, device=dev)
-        ws = max(_ops.workspace_bytes(m, N, K) for m in range(1, _WORKSPACE_MAX_M + 1))
+        ws = max(max(_ops.workspace_bytes(m, N, K), _ops.linear_workspace_bytes(m, N, K, 16))
+                 for m in range(1, _WORKSPACE_MAX_M + 1))
         self.workspace = torch.zeros(max(ws, 1), dtype=torch.uint8, device=dev)
         self.bias = bias.to(dev).contiguous() if bias is not None else None
 
@@ -236,8 +238,8 @@ class MarlinW4A8Linear(nn.Module):
         if not rotation.prepared:
             rotation.prepare()
         return torch.ops.paroquant.w4a8_linear(
-            x, rotation.pairs_u8, rotation.cos_sin, rotation.scales_f32, self.qweight, self.scales, self.bias,
-            self.workspace, input_fp16, materialize_fp16, out_dtype)
+            x, rotation.rot_ij, rotation.rot_cs, rotation.scales_f32, rotation.krot, self.qweight, self.scales,
+            self.bias, self.workspace, input_fp16, materialize_fp16, out_dtype)
 
     def extra_repr(self) -> str:
         return f"in_features={self.in_features}, out_features={self.out_features}, group_size={self.group_size}"

@@ -7,12 +7,14 @@ constructor arguments, same persistent buffers (``theta`` [KROT, K/2],
 theta, channel_scales, 128)``.
 
 On top of that, ``Rotation.prepare()`` derives the operands of the fused
-rotate+quant kernel (non-persistent, so state-dict keys are unchanged):
-  pairs_u8   uint8 [KROT, K]        group-local indices (validated as one
-                                    perfect matching per group and layer)
-  cos_sin    float32 [KROT, K/2, 2] cos/sin of each pair's angle, evaluated
-                                    in float64 on the host and rounded once
-  scales_f32 float32 [K]            channel scales
+rotate+quant kernels (non-persistent, so state-dict keys are unchanged):
+  rot_ij     int16 [K/128, 64, 8]     packed pair indices (one pair per lane
+                                      and layer, assigned for conflict-free LDS
+                                      access; validated as one perfect matching
+                                      per group and layer)
+  rot_cs     float32 [K/128, 64, 8, 2] cos/sin of each pair's angle, evaluated
+                                      in float64 on the host and rounded once
+  scales_f32 float32 [K]              channel scales
 and ``RotateLinearInt4.forward`` runs rotation + int8 quant + GEMM through
 ``paroquant::w4a8_linear`` when its qlinear is a ``MarlinW4A8Linear``.
 """
@@ -64,8 +66,8 @@ class Rotation(nn.Module):
         self.register_buffer("theta", rotation_angles.clone().contiguous())
         self.register_buffer("pairs", rotation_pairs.clone().short().contiguous())
         self.register_buffer("channel_scales", channel_scales.clone().contiguous())
-        self.register_buffer("pairs_u8", torch.empty(0, dtype=torch.uint8), persistent=False)
-        self.register_buffer("cos_sin", torch.empty(0, dtype=torch.float32), persistent=False)
+        self.register_buffer("rot_ij", torch.empty(0, dtype=torch.int16), persistent=False)
+        self.register_buffer("rot_cs", torch.empty(0, dtype=torch.float32), persistent=False)
         self.register_buffer("scales_f32", torch.empty(0, dtype=torch.float32), persistent=False)
         self.group_size = group_size
 
@@ -75,17 +77,27 @@ class Rotation(nn.Module):
     @torch.no_grad()
     def prepare(self) -> None:
         """(Re)derive the fused kernel's operands from theta/pairs/channel_scales."""
+        from ..ops import pack_rotation
+
         dev = self.theta.device
         check_rotation_pairs(self.pairs, self.group_size)
-        th = self.theta.detach().to("cpu").float().double()
-        cs = torch.stack([torch.cos(th), torch.sin(th)], dim=-1).float()
-        self.pairs_u8 = self.pairs.detach().to(dev, torch.int16).to(torch.uint8).contiguous()
-        self.cos_sin = cs.to(dev).contiguous()
+        rot_ij, rot_cs = pack_rotation(self.pairs, self.cos_sin_table())
+        self.rot_ij = rot_ij.to(dev)
+        self.rot_cs = rot_cs.to(dev)
         self.scales_f32 = self.channel_scales.detach().reshape(-1).to(dev, torch.float32).contiguous()
+
+    def cos_sin_table(self) -> torch.Tensor:
+        """float32 [KROT, K/2, 2] (cos, sin) of theta, evaluated in float64 on the host."""
+        th = self.theta.detach().to("cpu").float().double()
+        return torch.stack([torch.cos(th), torch.sin(th)], dim=-1).float()
+
+    @property
+    def krot(self) -> int:
+        return self.pairs.size(0)
 
     @property
     def prepared(self) -> bool:
-        return self.cos_sin.numel() > 0 and self.cos_sin.device == self.theta.device
+        return self.rot_cs.numel() > 0 and self.rot_cs.device == self.theta.device
 
 
 class RotateLinearInt4(nn.Module):

@@ -58,6 +58,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--decode-m", type=str, default="1,4,16",
+                    help="comma-separated decode token counts to time (M = 1 gives value)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -127,7 +129,8 @@ def main() -> int:
 
     # ---- decode: M = 1 (value), 4, 16 -------------------------------------
     decode = {}
-    for M in (1, 4, 16):
+    decode_ms = sorted({int(v) for v in args.decode_m.split(",")} | {1})
+    for M in decode_ms:
         graphs, _, _ = capture_layers(M, 5000 + M)
         ms = time_graphs(graphs, args.steps, args.warmup)
         b = sum(linear_bytes(M, N, K) for N, K in shapes)
@@ -142,7 +145,7 @@ def main() -> int:
         row = []
         for m, x in zip(L, X):
             r = m.rotate_linear.rotation
-            row.append(torch.ops.paroquant.rotate_quant_i8(x, r.pairs_u8, r.cos_sin, r.scales_f32, True, True))
+            row.append(torch.ops.paroquant.rotate_quant_i8(x, r.rot_ij, r.rot_cs, r.scales_f32, r.krot, True, True))
         xq_all.append(row)
     gemm_launches = [(m.rotate_linear.qlinear, xq, xs) for L, row in zip(pool, xq_all) for m, (xq, xs) in zip(L, row)]
     gg = torch.cuda.CUDAGraph()
@@ -178,10 +181,10 @@ def main() -> int:
         ops = sum(2 * M * N * K for N, K in shapes)
         tops = ops / (ms * 1e-3) / 1e12
         # GEMM kernels alone
-        xq = [torch.ops.paroquant.rotate_quant_i8(x, m.rotate_linear.rotation.pairs_u8,
-                                                  m.rotate_linear.rotation.cos_sin,
-                                                  m.rotate_linear.rotation.scales_f32, True, True)
-              for m, x in zip(L, X)]
+        xq = []
+        for m, x in zip(L, X):
+            r = m.rotate_linear.rotation
+            xq.append(torch.ops.paroquant.rotate_quant_i8(x, r.rot_ij, r.rot_cs, r.scales_f32, r.krot, True, True))
         gg = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gg):
             for m, (q8, s8) in zip(L, xq):

@@ -15,6 +15,8 @@
  * Reference interfaces replaced (paths relative to the reference tree):
  *   pq_rotate            torch.ops.rotation.rotate
  *                        kernels/paroquant_kernels/src/rotation.cu:456-493, 576-584
+ *   pq_rotation_pack     load-time packing of Rotation's buffers (host)
+ *                        src/alpamayo_r1/utils/quantization/rotation_linear.py:26-43
  *   pq_rotate_quant_i8   rotation.rotate (fp16) followed by vLLM's per-token
  *                        int8 quant inside apply_awq_marlin_linear
  *                        src/alpamayo_r1/utils/quantization/paroquant_marlin_w4a8.py:59-65, 319-333
@@ -68,15 +70,29 @@ int pq_rotate(const void* x, void* y, const int16_t* idx_ij, const void* theta,
               const void* scales, int64_t rows, int64_t h, int krot, int group_size,
               int dtype, void* stream);
 
+/* Packs rotation parameters (host memory, host code; no GPU involved) into
+ * the operand layout of the fused kernels:
+ *   rot_ij [G][64][KP] uint16  first | second << 8 (group-local indices)
+ *   rot_cs [G][64][KP][2] float (cos, sin)
+ * G = h/128, KP = krot rounded up to a multiple of 8.  Input: pairs int16
+ * [krot][h] group-local (pair t of group g = pairs[r][g*128+2t], +1) and
+ * cos_sin float [krot][h/2][2] (the pair's angle in theta's layout).  Each
+ * lane owns one pair per layer; pairs are assigned to lanes (and possibly
+ * swapped, with sin negated, which is the same rotation) so that every
+ * layer's LDS accesses are bank-conflict free.  Fails with PQ_ERR_ARG unless
+ * every layer pairs each channel of each 128-group exactly once.
+ * Reference: the parameters of Rotation (rotation_linear.py:26-43). */
+int pq_rotation_pack(const int16_t* pairs, const float* cos_sin, int64_t h, int krot, uint16_t* rot_ij,
+                     float* rot_cs);
+
 /* Fused rotation + channel scale + per-token absmax + int8 quantization.
- * x: [rows, h] of x_dtype; pairs: uint8 [krot, h] group-local indices
- * (group 128); cos_sin: float32 [krot, h/2, 2] (cos, sin) of each pair's
- * angle; scales: float32 [h] or NULL.
+ * x: [rows, h] of x_dtype; rot_ij / rot_cs: packed parameters
+ * (pq_rotation_pack) of krot layers; scales: float32 [h] or NULL.
  * Outputs xq int8 [rows, h], xscale float32 [rows] (absmax/127), and, when
  * xrot is not NULL, the rotated activations as fp16 [rows, h].
  * flags: PQ_RQ_* bits.  krot in 1..16, h % 128 == 0, h <= 16384.
  * Reference: rotation.cu:15-60 + paroquant_marlin_w4a8.py:319-333. */
-int pq_rotate_quant_i8(const void* x, int x_dtype, const uint8_t* pairs, const float* cos_sin,
+int pq_rotate_quant_i8(const void* x, int x_dtype, const uint16_t* rot_ij, const float* rot_cs,
                        const float* scales, int8_t* xq, float* xscale, void* xrot,
                        int64_t rows, int64_t h, int krot, unsigned flags, void* stream);
 
@@ -129,7 +145,7 @@ size_t pq_w4a8_linear_workspace_size(int64_t m, int64_t n, int64_t k, int krot);
  * pq_rotate_quant_i8, weights as for pq_w4a8_gemm, flags PQ_RQ_*.
  * k <= 16384.  Same results as pq_rotate_quant_i8 followed by pq_w4a8_gemm.
  * Reference: paroquant_marlin_w4a8.py:59-65, 314-333; rotation_linear.py:120-124. */
-int pq_w4a8_linear(const void* x, int x_dtype, const uint8_t* pairs, const float* cos_sin, const float* scales,
+int pq_w4a8_linear(const void* x, int x_dtype, const uint16_t* rot_ij, const float* rot_cs, const float* scales,
                    const uint8_t* wpack, const uint32_t* wmeta, const void* bias, int bias_dtype, void* y,
                    int y_dtype, int64_t m, int64_t n, int64_t k, int krot, unsigned flags, void* workspace,
                    size_t workspace_bytes, void* stream);

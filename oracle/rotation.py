@@ -130,3 +130,34 @@ def rotate_path_f32(x_bf16_as_f32: np.ndarray, pairs: np.ndarray, cos: np.ndarra
     if materialize_fp16:
         y = y.astype(np.float16).astype(np.float32)
     return y
+
+
+def unpack_packed_params(rot_ij: np.ndarray, rot_cs: np.ndarray, krot: int):
+    """Packed kernel operands -> per (group, lane, layer) (first, second, cos, sin).
+
+    rot_ij [G, 64, KP] uint16 (first | second << 8); rot_cs [G, 64, KP, 2].
+    """
+    ij = np.asarray(rot_ij).view(np.uint16).astype(np.int64)[:, :, :krot]
+    first = ij & 0xFF
+    second = (ij >> 8) & 0xFF
+    cs = np.asarray(rot_cs, np.float32)[:, :, :krot]
+    return first, second, cs[..., 0], cs[..., 1]
+
+
+def rotate_f32_packed(xs: np.ndarray, rot_ij: np.ndarray, rot_cs: np.ndarray, krot: int) -> np.ndarray:
+    """The kernels' use of the packed operands: layer r, lane t of group g updates
+    (first, second) with xf' = fma(xf, c, xs*s), xs' = fma(xs, c, -(xf*s))."""
+    y = np.array(xs, dtype=np.float32, copy=True)
+    first, second, c, s = unpack_packed_params(rot_ij, rot_cs, krot)
+    G = first.shape[0]
+    base = (np.arange(G, dtype=np.int64) * 128)[:, None]
+    for r in range(krot):
+        gi = (first[:, :, r] + base).reshape(-1)
+        gj = (second[:, :, r] + base).reshape(-1)
+        cr = c[:, :, r].reshape(-1)
+        sr = s[:, :, r].reshape(-1)
+        xi = y[:, gi]
+        xj = y[:, gj]
+        y[:, gi] = _fma32(xi, cr, (xj * sr).astype(np.float32))
+        y[:, gj] = _fma32(xj, cr, -(xi * sr).astype(np.float32))
+    return y

@@ -39,3 +39,14 @@ def assert_bf16_close(got: np.ndarray, ref64: np.ndarray, tol_fro=1e-2):
     bad = np.abs(np.asarray(got, np.float64) - ref64) > bound
     assert not bad.any(), f"{bad.sum()} outputs beyond the elementwise bound; e.g. got {got[bad][:4]} ref {ref64[bad][:4]}"
     return e
+
+
+def packed_rotation(pairs: torch.Tensor, theta: torch.Tensor):
+    """(rot_ij, rot_cs, cos, sin) for Rotation-style pairs [krot, K] and angles [krot, K/2]."""
+    from alpamayo_amd.ops import pack_rotation
+    from oracle import rotation as orot
+
+    c, s = orot.cos_sin_table(theta.numpy())
+    cs = torch.from_numpy(np.stack([c, s], axis=-1)).contiguous()
+    rot_ij, rot_cs = pack_rotation(pairs.to(torch.int16), cs)
+    return rot_ij, rot_cs, c, s

@@ -57,6 +57,7 @@ def test_rotate_quant_and_gemm_argument_checks():
     assert lib.pq_rotate_quant_i8(p, 2, p, p, None, p, p, None, 4, 256, 8, 8, None) == 1
     assert "flags" in _err(lib)
     assert lib.pq_rotate_quant_i8(ctypes.c_void_p(18), 2, p, p, None, p, p, None, 4, 256, 8, 3, None) == 1
+    assert lib.pq_rotate_quant_i8(p, 2, ctypes.c_void_p(24), p, None, p, p, None, 4, 256, 8, 3, None) == 1
     assert "aligned" in _err(lib)
     assert lib.pq_w4a8_gemm(p, p, p, p, None, 0, p, 2, 4, 64, 256, 64, None, 0, None) == 2
     assert lib.pq_w4a8_gemm(p, p, p, p, None, 0, p, 2, 4, 60, 256, 128, None, 0, None) == 1
@@ -70,7 +71,7 @@ def test_linear_argument_checks():
     lib = _lib.load()
     p = ctypes.c_void_p(256)
     args = lambda m, k, krot, flags, ws, wsb: (p, 2, p, p, None, p, p, None, 0, p, 2, m, 4096, k, krot, flags, ws, wsb,
-                                              None)
+                                              None)   # noqa: E731
     assert lib.pq_w4a8_linear(*args(1, 200, 8, 3, None, 0)) == 1
     assert lib.pq_w4a8_linear(*args(1, 4096, 0, 3, None, 0)) == 2
     assert lib.pq_w4a8_linear(*args(1, 4096, 8, 4, None, 0)) == 1

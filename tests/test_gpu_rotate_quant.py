@@ -17,22 +17,26 @@ from alpamayo_amd import workloads
 from oracle import linear as olin
 from oracle import quant as oquant
 from oracle import rotation as orot
-from tests.gpu_util import assert_codes_close, rel_fro, to_np
+from tests.gpu_util import assert_codes_close, packed_rotation, rel_fro, to_np
 
 pytestmark = pytest.mark.gpu
 
 
+class _Rot:
+    def __init__(self, K, seed):
+        self.pairs, self.theta, self.cs = workloads.rotation_params(K, workloads.generator(seed))
+        self.rot_ij, self.rot_cs, self.c, self.s = packed_rotation(self.pairs, self.theta)
+        self.krot = self.pairs.shape[0]
+
+
 def _prepared(K, seed):
-    pairs, theta, cs = workloads.rotation_params(K, workloads.generator(seed))
-    c, s = orot.cos_sin_table(theta.numpy())
-    cos_sin = torch.from_numpy(np.stack([c, s], axis=-1)).contiguous()
-    return pairs, theta, cs, cos_sin
+    return _Rot(K, seed)
 
 
-def _run(x, pairs, cos_sin, scales_f32, input_fp16=True, materialize=True):
+def _run(x, rot, scales_f32, input_fp16=True, materialize=True):
     xq, xs, xr = torch.ops.paroquant.rotate_quant_i8_rot(
-        x.cuda(), pairs.to(torch.uint8).cuda(), cos_sin.cuda(),
-        scales_f32.cuda() if scales_f32 is not None else None, input_fp16, materialize)
+        x.cuda(), rot.rot_ij.cuda(), rot.rot_cs.cuda(),
+        scales_f32.cuda() if scales_f32 is not None else None, rot.krot, input_fp16, materialize)
     torch.cuda.synchronize()
     return to_np(xq), to_np(xs), to_np(xr)
 
@@ -43,12 +47,11 @@ def _run(x, pairs, cos_sin, scales_f32, input_fp16=True, materialize=True):
 def test_fused_matches_oracle(M, K, dtype):
     print(f"rotate_quant M={M} K={K} dtype={dtype}", flush=True)
     seed = zlib.crc32(f"{M}-{K}-{dtype}".encode())
-    pairs, theta, cs, cos_sin = _prepared(K, seed)
+    rot = _prepared(K, seed)
     x = workloads.activations(M, K, workloads.generator(seed + 1)).to(dtype)
-    sc = cs.float().reshape(-1)
-    q, s, r = _run(x, pairs, cos_sin, sc)
-    c, sn = cos_sin[..., 0].numpy(), cos_sin[..., 1].numpy()
-    v, qref, sref = olin.rotate_quant(to_np(x), pairs.numpy(), c, sn, sc.numpy())
+    sc = rot.cs.float().reshape(-1)
+    q, s, r = _run(x, rot, sc)
+    v, qref, sref = olin.rotate_quant(to_np(x), rot.pairs.numpy(), rot.c, rot.s, sc.numpy())
     assert rel_fro(r, v) < 1e-2
     ident = np.mean(r == v.astype(np.float16).astype(np.float32))
     assert ident >= 0.999, ident
@@ -59,11 +62,10 @@ def test_fused_matches_oracle(M, K, dtype):
 @pytest.mark.parametrize("input_fp16,materialize", [(False, False), (True, False), (False, True)])
 def test_flags(input_fp16, materialize):
     K, M = 1024, 9
-    pairs, theta, cs, cos_sin = _prepared(K, 11)
+    rot = _prepared(K, 11)
     x = workloads.activations(M, K, workloads.generator(12))
-    q, s, r = _run(x, pairs, cos_sin, None, input_fp16, materialize)
-    c, sn = cos_sin[..., 0].numpy(), cos_sin[..., 1].numpy()
-    v = orot.rotate_path_f32(to_np(x), pairs.numpy(), c, sn, None, 128, input_fp16, materialize)
+    q, s, r = _run(x, rot, None, input_fp16, materialize)
+    v = orot.rotate_path_f32(to_np(x), rot.pairs.numpy(), rot.c, rot.s, None, 128, input_fp16, materialize)
     qref, sref = oquant.quant_int8_per_token(v)
     assert_codes_close(q, qref)
     np.testing.assert_allclose(s, sref, rtol=1e-6)
@@ -72,10 +74,10 @@ def test_flags(input_fp16, materialize):
 
 def test_zero_rows_and_single_spike():
     K = 512
-    pairs, theta, cs, cos_sin = _prepared(K, 21)
+    rot = _prepared(K, 21)
     x = torch.zeros(3, K, dtype=torch.bfloat16)
     x[1, 100] = 5.0
-    q, s, r = _run(x, pairs, cos_sin, cs.float().reshape(-1))
+    q, s, r = _run(x, rot, rot.cs.float().reshape(-1))
     assert s[0] == 0 and np.all(q[0] == 0) and np.all(r[0] == 0)
     assert np.all(q[2] == 0)
     assert np.abs(q[1]).max() == 127 and s[1] > 0
@@ -94,12 +96,12 @@ def test_quant_only_kernel():
 def test_full_prefill_shape_row_subset():
     """M = 3072 (4 cameras x 4 frames x 192 tokens) at K = 4096 and 12288, checked on a row subset."""
     for K in (4096, 12288):
-        pairs, theta, cs, cos_sin = _prepared(K, 31 + K)
+        rot = _prepared(K, 31 + K)
         x = workloads.activations(3072, K, workloads.generator(32 + K))
-        q, s, _ = _run(x, pairs, cos_sin, cs.float().reshape(-1))
+        q, s, _ = _run(x, rot, rot.cs.float().reshape(-1))
         rows = np.array([0, 1, 777, 2048, 3071])
-        c, sn = cos_sin[..., 0].numpy(), cos_sin[..., 1].numpy()
-        _, qref, sref = olin.rotate_quant(to_np(x)[rows], pairs.numpy(), c, sn, cs.float().reshape(-1).numpy())
+        _, qref, sref = olin.rotate_quant(to_np(x)[rows], rot.pairs.numpy(), rot.c, rot.s,
+                                          rot.cs.float().reshape(-1).numpy())
         assert_codes_close(q[rows], qref)
         np.testing.assert_allclose(s[rows], sref, rtol=1e-6)
         assert np.all(np.abs(q).max(axis=1) == 127)   # every row reaches +-127
@@ -107,10 +109,25 @@ def test_full_prefill_shape_row_subset():
 
 def test_bad_params_rejected():
     x = torch.zeros(2, 256, dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(RuntimeError, match="pairs"):
-        torch.ops.paroquant.rotate_quant_i8(x, torch.zeros(8, 128, dtype=torch.uint8, device="cuda"),
-                                            torch.zeros(8, 128, 2, device="cuda"), None, True, True)
+    with pytest.raises(RuntimeError, match="rot_ij"):
+        torch.ops.paroquant.rotate_quant_i8(x, torch.zeros(1, 64, 8, dtype=torch.int16, device="cuda"),
+                                            torch.zeros(2, 64, 8, 2, device="cuda"), None, 8, True, True)
     with pytest.raises(RuntimeError, match="multiple of 128"):
         torch.ops.paroquant.rotate_quant_i8(torch.zeros(2, 200, dtype=torch.bfloat16, device="cuda"),
-                                            torch.zeros(8, 200, dtype=torch.uint8, device="cuda"),
-                                            torch.zeros(8, 100, 2, device="cuda"), None, True, True)
+                                            torch.zeros(1, 64, 8, dtype=torch.int16, device="cuda"),
+                                            torch.zeros(1, 64, 8, 2, device="cuda"), None, 8, True, True)
+
+
+@pytest.mark.parametrize("krot", [1, 3, 8, 12, 16])
+def test_krot_variants(krot):
+    """Layer counts other than 8 (padded packed layout KP = 8 or 16)."""
+    K, M = 512, 37
+    g = workloads.generator(40 + krot)
+    pairs, theta, cs = workloads.rotation_params(K, g, krot=krot)
+    rot_ij, rot_cs, c, s = packed_rotation(pairs, theta)
+    x = workloads.activations(M, K, g)
+    xq, xs = torch.ops.paroquant.rotate_quant_i8(x.cuda(), rot_ij.cuda(), rot_cs.cuda(), cs.float().reshape(-1).cuda(),
+                                                 krot, True, True)
+    _, qref, sref = olin.rotate_quant(to_np(x), pairs.numpy(), c, s, cs.float().reshape(-1).numpy())
+    assert_codes_close(to_np(xq), qref)
+    np.testing.assert_allclose(to_np(xs), sref, rtol=1e-6)
