@@ -72,6 +72,21 @@ __device__ __forceinline__ float pq_load_as_f32(const void* p, int64_t i) {
   else return pq_bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
 }
 
+// Split form of pq_load_as_f32: the raw bits now, the conversion later (so a
+// barrier can sit between issuing a load and consuming it).
+template <int DT>
+__device__ __forceinline__ uint32_t pq_load_raw(const void* p, int64_t i) {
+  if constexpr (DT == PQ_F32) return static_cast<const uint32_t*>(p)[i];
+  else return static_cast<const uint16_t*>(p)[i];
+}
+
+template <int DT>
+__device__ __forceinline__ float pq_raw_to_f32(uint32_t r) {
+  if constexpr (DT == PQ_F32) return __uint_as_float(r);
+  else if constexpr (DT == PQ_F16) return pq_f16_to_f32(static_cast<uint16_t>(r));
+  else return pq_bf16_to_f32(static_cast<uint16_t>(r));
+}
+
 template <int DT>
 __device__ __forceinline__ void pq_store_from_f32(void* p, int64_t i, float v) {
   if constexpr (DT == PQ_F32) static_cast<float*>(p)[i] = v;

@@ -64,4 +64,76 @@ __device__ __forceinline__ void givens(float xi, float xj, float c, float s, flo
   nj = fmaf(xj, c, -(xi * s));
 }
 
+// ---------------------------------------------------------------------------
+// Register-chain rotation of one 128-channel group by one wave (operands
+// built by pq_rotation_pack):
+//   rot_idx [G][64][KP/2] uint32: word 0 = Af | Bf << 8 | init << 16,
+//                                 byte 4 + r = src | flag << 7 (layer r)
+//   rot_cs  [G][64][KP][2] float: (cos, +-sin) of the lane's pair in layer r
+// Lane l loads channels l and l+64 into slots (a, b), swapped when init is
+// set.  Before layer r it fetches slot a of lane src (ds_bpermute) and puts
+// the value into slot a when flag is set (else into slot b), keeping its old
+// slot b in the other slot; then a' = fma(a, c, b*s), b' = fma(b, c, -(a*s)).
+// After the last layer slot a holds channel Af and slot b channel Bf.
+// ---------------------------------------------------------------------------
+template <int KP>
+struct RotLane {
+  uint32_t w[KP / 2];
+  float cs[2 * KP];
+};
+
+template <int KP>
+__device__ __forceinline__ void load_rot_lane(const uint32_t* __restrict__ rot_idx, const float* __restrict__ rot_cs,
+                                              int g, int lane, RotLane<KP>& p) {
+  const int64_t o = static_cast<int64_t>(g) * 64 + lane;
+  const uint4* wi = reinterpret_cast<const uint4*>(rot_idx + o * (KP / 2));
+#pragma unroll
+  for (int q = 0; q < KP / 8; ++q) {
+    const uint4 v = wi[q];
+    p.w[4 * q] = v.x;
+    p.w[4 * q + 1] = v.y;
+    p.w[4 * q + 2] = v.z;
+    p.w[4 * q + 3] = v.w;
+  }
+  const float4* c = reinterpret_cast<const float4*>(rot_cs + o * (2 * KP));
+#pragma unroll
+  for (int q = 0; q < KP / 2; ++q) {
+    const float4 v = c[q];
+    p.cs[4 * q] = v.x;
+    p.cs[4 * q + 1] = v.y;
+    p.cs[4 * q + 2] = v.z;
+    p.cs[4 * q + 3] = v.w;
+  }
+}
+
+template <int KP>
+__device__ __forceinline__ bool rot_init_swapped(const RotLane<KP>& p) { return (p.w[0] >> 16) & 1u; }
+template <int KP>
+__device__ __forceinline__ int rot_final_a(const RotLane<KP>& p) { return p.w[0] & 127u; }
+template <int KP>
+__device__ __forceinline__ int rot_final_b(const RotLane<KP>& p) { return (p.w[0] >> 8) & 127u; }
+
+// Layer r (compile-time after unrolling) for N value pairs sharing the lane's operands.
+template <int KP, int N>
+__device__ __forceinline__ void rot_layer(const RotLane<KP>& p, int r, float (&a)[N], float (&b)[N]) {
+  const uint32_t st = (p.w[(4 + r) >> 2] >> (8 * ((4 + r) & 3))) & 0xffu;
+  const int addr = static_cast<int>(st & 63u) << 2;
+  const bool fl = (st & 128u) != 0;
+#pragma unroll
+  for (int n = 0; n < N; ++n) {
+    const float recv = __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(a[n])));
+    const float keep = b[n];
+    a[n] = fl ? recv : keep;
+    b[n] = fl ? keep : recv;
+  }
+  const float c = p.cs[2 * r], s = p.cs[2 * r + 1];
+#pragma unroll
+  for (int n = 0; n < N; ++n) {
+    float na, nb;
+    givens(a[n], b[n], c, s, na, nb);
+    a[n] = na;
+    b[n] = nb;
+  }
+}
+
 }  // namespace pqd

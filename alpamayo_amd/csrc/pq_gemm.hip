@@ -31,6 +31,7 @@
 //                prefetched into registers, 2x2 waves of 64x64, each
 //                2x2 v_mfma_i32_32x32x32_i8 tiles per 32-deep K step.
 #include "pq_device.h"
+#include "pq_internal.h"
 
 using namespace pqd;
 
@@ -45,19 +46,31 @@ namespace {
 // workgroup ever communicates with another (no split-K workspace, no
 // device-scope fence).
 // ---------------------------------------------------------------------------
-template <int NT, int W, int U, bool PARTIALS>
-__global__ __launch_bounds__(W * 64) void gemm_skinny(
-    const int8_t* __restrict__ xq, const float* __restrict__ xs, const uint8_t* __restrict__ wpack,
-    const uint32_t* __restrict__ wmeta, const void* __restrict__ bias, int bias_dtype, void* __restrict__ y,
-    int y_dtype, int32_t* __restrict__ partials, int M, int N, int K) {
+//
+// AQ selects where A comes from: 0 = int8 codes and token scales in global
+// memory; 1 / 2 = rotated fp16 / fp32 rows plus per-group absmax (the split
+// rotation's output): the workgroup derives each row's token scale, writes
+// the int8 codes of all M rows into LDS (row stride K + 16 bytes, so the 16
+// rows of an A fragment hit distinct banks) and reads A from there.  The
+// first batch of weight loads is issued before that prologue.
+constexpr int kSkinnyRows = 16;
+
+template <int NT, int W, int U, bool PARTIALS, int AQ>
+__global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) void gemm_skinny(
+    const int8_t* __restrict__ xq, const float* __restrict__ xs, const void* __restrict__ xr,
+    const float* __restrict__ gmax, const uint8_t* __restrict__ wpack, const uint32_t* __restrict__ wmeta,
+    const void* __restrict__ bias, int bias_dtype, void* __restrict__ y, int y_dtype, int32_t* __restrict__ partials,
+    int M, int N, int K) {
   __shared__ float red[W][NT][4][64];
+  __shared__ float s_amax[kSkinnyRows];
+  extern __shared__ __attribute__((aligned(16))) int8_t aq[];
   const int G = K >> 7;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar branches
   const int lane = threadIdx.x & 63;
   const int c = lane & 15;
   const int j = lane >> 4;
   const bool arow = c < M;
-  const int8_t* ap = xq + static_cast<int64_t>(arow ? c : 0) * K + j * 32;
+  const int astride = K + 16;
   const int tile0 = blockIdx.x * NT;
 
   float acc[NT][4];
@@ -66,7 +79,56 @@ __global__ __launch_bounds__(W * 64) void gemm_skinny(
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc[nt][v] = 0.0f;
 
-  for (int g0 = wave; g0 < G; g0 += W * U) {
+  const int8_t* ap = xq + static_cast<int64_t>(arow ? c : 0) * K + j * 32;
+  const int8_t* al = aq + (arow ? c : 0) * astride + j * 32;
+  const int nthr = W * 64;
+  const int k8 = K >> 3;
+
+  // AQ prologue, part 1: request the per-group maxima and (when they fit in
+  // kPre 8-element chunks per thread) the rotated rows before any weight
+  // block, so that waiting for them does not mean waiting for the weights
+  // (a wave's loads complete in issue order).
+  constexpr int kPreMax = 2048 / (W * 64);    // gmax values per thread (covers M * G <= 2048)
+  constexpr int kPre = W >= 8 ? 2 : 4;        // 8-element chunks of A per thread
+  float gm[kPreMax];
+  uint4 pre[kPre][AQ == 2 ? 2 : 1];
+  bool preloaded = false;
+  if constexpr (AQ != 0) {
+#pragma unroll
+    for (int q = 0; q < kPreMax; ++q) {
+      const int i = threadIdx.x + q * nthr;
+      gm[q] = i < M * G ? gmax[i] : 0.0f;
+    }
+    preloaded = M * k8 <= kPre * nthr;
+    if (preloaded) {
+#pragma unroll
+      for (int q = 0; q < kPre; ++q) {
+        const int e = threadIdx.x + q * nthr;
+        if (e < M * k8) {
+          const int r = e / k8;
+          const int c8 = (e - r * k8) * 8;
+          if constexpr (AQ == 1) {
+            pre[q][0] =
+                *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(xr) + static_cast<int64_t>(r) * K + c8);
+          } else {
+            const uint4* src =
+                reinterpret_cast<const uint4*>(static_cast<const float*>(xr) + static_cast<int64_t>(r) * K + c8);
+            pre[q][0] = src[0];
+            pre[q][AQ == 2 ? 1 : 0] = src[1];
+          }
+        }
+      }
+    }
+  }
+
+  // Every wave runs the same number of batches (a batch past G loads
+  // nothing), so the prologue's barriers are reached by all waves.
+  const int batches = (G + W * U - 1) / (W * U);
+  // One batch of U groups per wave; batch 0 (which holds the prologue) is
+  // peeled off the loop, so the common single-batch case has no back edge
+  // (the compiler otherwise waits for earlier loads before reusing registers).
+  auto run_batch = [&](const int it) {
+    const int g0 = wave + it * W * U;
     v4i wb[U][NT];
     uint32_t wm[U][NT];
     v4i a0[U], a1[U];
@@ -80,19 +142,85 @@ __global__ __launch_bounds__(W * 64) void gemm_skinny(
           wb[u][nt] = *reinterpret_cast<const v4i*>(wpack + blk * 1024 + lane * 16);
           wm[u][nt] = wmeta[blk * 16 + c];
         }
-        if (arow) {
+        if constexpr (AQ == 0) {
+          // Unconditional (rows >= M read row 0 and are zeroed at use): a
+          // branch around the loads would make the compiler wait early.
           a0[u] = *reinterpret_cast<const v4i*>(ap + static_cast<int64_t>(g) * 128);
           a1[u] = *reinterpret_cast<const v4i*>(ap + static_cast<int64_t>(g) * 128 + 16);
-        } else {
-          a0[u] = v4i{0, 0, 0, 0};
-          a1[u] = v4i{0, 0, 0, 0};
         }
+      }
+    }
+    if constexpr (AQ != 0) {
+      if (it == 0) {
+        // Part 2: token scales, then the int8 image of A in LDS.
+        if (threadIdx.x < kSkinnyRows) s_amax[threadIdx.x] = 0.0f;
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < kPreMax; ++q) {   // absmax >= 0: unsigned order is float order
+          const int i = threadIdx.x + q * nthr;
+          if (i < M * G) atomicMax(reinterpret_cast<unsigned*>(&s_amax[i / G]), __float_as_uint(gm[q]));
+        }
+        for (int i = threadIdx.x + kPreMax * nthr; i < M * G; i += nthr)
+          atomicMax(reinterpret_cast<unsigned*>(&s_amax[i / G]), __float_as_uint(gmax[i]));
+        __syncthreads();
+        auto quant8 = [&](int e, const uint4* v) {
+          const int r = e / k8;
+          const int c8 = (e - r * k8) * 8;
+          float f[8];
+          if constexpr (AQ == 1) {
+            const uint32_t wds[4] = {v[0].x, v[0].y, v[0].z, v[0].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              f[2 * q] = pq_f16_to_f32(static_cast<uint16_t>(wds[q] & 0xffffu));
+              f[2 * q + 1] = pq_f16_to_f32(static_cast<uint16_t>(wds[q] >> 16));
+            }
+          } else {
+            f[0] = __uint_as_float(v[0].x); f[1] = __uint_as_float(v[0].y);
+            f[2] = __uint_as_float(v[0].z); f[3] = __uint_as_float(v[0].w);
+            f[4] = __uint_as_float(v[AQ == 2 ? 1 : 0].x); f[5] = __uint_as_float(v[AQ == 2 ? 1 : 0].y);
+            f[6] = __uint_as_float(v[AQ == 2 ? 1 : 0].z); f[7] = __uint_as_float(v[AQ == 2 ? 1 : 0].w);
+          }
+          const float inv = inv_scale(s_amax[r]);
+          uint2 o;
+          o.x = quant4(f[0], f[1], f[2], f[3], inv);
+          o.y = quant4(f[4], f[5], f[6], f[7], inv);
+          *reinterpret_cast<uint2*>(aq + r * astride + c8) = o;
+        };
+        if (preloaded) {
+#pragma unroll
+          for (int q = 0; q < kPre; ++q) {
+            const int e = threadIdx.x + q * nthr;
+            if (e < M * k8) quant8(e, pre[q]);
+          }
+        } else {
+          for (int e = threadIdx.x; e < M * k8; e += nthr) {
+            const int r = e / k8;
+            const int c8 = (e - r * k8) * 8;
+            uint4 v[2];
+            if constexpr (AQ == 1) {
+              v[0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(xr) + static_cast<int64_t>(r) * K + c8);
+            } else {
+              const uint4* src =
+                  reinterpret_cast<const uint4*>(static_cast<const float*>(xr) + static_cast<int64_t>(r) * K + c8);
+              v[0] = src[0];
+              v[1] = src[1];
+            }
+            quant8(e, v);
+          }
+        }
+        __syncthreads();
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int g = g0 + W * u;
       if (g < G) {
+        if constexpr (AQ != 0) {   // A from the LDS image, next to its use
+          a0[u] = *reinterpret_cast<const v4i*>(al + g * 128);
+          a1[u] = *reinterpret_cast<const v4i*>(al + g * 128 + 16);
+        }
+        const v4i zero = {0, 0, 0, 0};
+        const v4i av0 = arow ? a0[u] : zero, av1 = arow ? a1[u] : zero;
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const uint32_t meta = wm[u][nt];
@@ -101,8 +229,8 @@ __global__ __launch_bounds__(W * 64) void gemm_skinny(
           const v4i b0 = unpack16(static_cast<uint32_t>(w.x), static_cast<uint32_t>(w.y), zb);
           const v4i b1 = unpack16(static_cast<uint32_t>(w.z), static_cast<uint32_t>(w.w), zb);
           v4i p = {0, 0, 0, 0};
-          p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[u], b0, p, 0, 0, 0);
-          p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[u], b1, p, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, b0, p, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, b1, p, 0, 0, 0);
           if constexpr (PARTIALS) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
@@ -117,7 +245,9 @@ __global__ __launch_bounds__(W * 64) void gemm_skinny(
         }
       }
     }
-  }
+  };
+  run_batch(0);
+  for (int it = 1; it < batches; ++it) run_batch(it);
   if constexpr (PARTIALS) return;
 
 #pragma unroll
@@ -135,7 +265,8 @@ __global__ __launch_bounds__(W * 64) void gemm_skinny(
 #pragma unroll
     for (int w = 0; w < W; ++w) sum += red[w][nt][rv][rl];
     const int n = (tile0 + nt) * 16 + (rl & 15);
-    pq_store_dyn(y, y_dtype, static_cast<int64_t>(m) * N + n, epilogue(sum, xs[m], bias, bias_dtype, n));
+    const float xsm = AQ != 0 ? s_amax[m] / 127.0f : xs[m];
+    pq_store_dyn(y, y_dtype, static_cast<int64_t>(m) * N + n, epilogue(sum, xsm, bias, bias_dtype, n));
   }
 }
 
@@ -317,24 +448,25 @@ SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k) {
   return {nt, w};
 }
 
-template <int NT, int W, bool PARTIALS>
-void launch_skinny_nw(const int8_t* xq, const float* xs, const uint8_t* wpack, const uint32_t* wmeta,
-                      const void* bias, int bias_dtype, void* y, int y_dtype, int32_t* partials, int M, int N, int K,
-                      hipStream_t stream) {
+template <int NT, int W, bool PARTIALS, int AQ>
+void launch_skinny_nw(const int8_t* xq, const float* xs, const void* xr, const float* gmax, const uint8_t* wpack,
+                      const uint32_t* wmeta, const void* bias, int bias_dtype, void* y, int y_dtype,
+                      int32_t* partials, int M, int N, int K, hipStream_t stream) {
   constexpr int U = W >= 16 ? 4 : 8;
   const unsigned grid = static_cast<unsigned>((N / 16) / NT);
-  gemm_skinny<NT, W, U, PARTIALS><<<grid, W * 64, 0, stream>>>(xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype,
-                                                                partials, M, N, K);
+  const size_t lds = AQ != 0 ? static_cast<size_t>(M) * (K + 16) : 0;
+  gemm_skinny<NT, W, U, PARTIALS, AQ><<<grid, W * 64, lds, stream>>>(xq, xs, xr, gmax, wpack, wmeta, bias, bias_dtype,
+                                                                     y, y_dtype, partials, M, N, K);
 }
 
-template <bool PARTIALS>
-void launch_skinny(const SkinnyCfg& cfg, const int8_t* xq, const float* xs, const uint8_t* wpack,
-                   const uint32_t* wmeta, const void* bias, int bias_dtype, void* y, int y_dtype, int32_t* partials,
-                   int M, int N, int K, hipStream_t stream) {
+template <bool PARTIALS, int AQ>
+void launch_skinny(const SkinnyCfg& cfg, const int8_t* xq, const float* xs, const void* xr, const float* gmax,
+                   const uint8_t* wpack, const uint32_t* wmeta, const void* bias, int bias_dtype, void* y, int y_dtype,
+                   int32_t* partials, int M, int N, int K, hipStream_t stream) {
 #define PQ_SKINNY(NT_, W_)                                                                                      \
   if (cfg.nt == NT_ && cfg.w == W_) {                                                                           \
-    launch_skinny_nw<NT_, W_, PARTIALS>(xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype, partials, M, N, K, \
-                                        stream);                                                               \
+    launch_skinny_nw<NT_, W_, PARTIALS, AQ>(xq, xs, xr, gmax, wpack, wmeta, bias, bias_dtype, y, y_dtype, partials, \
+                                            M, N, K, stream);                                                   \
     return;                                                                                                     \
   }
   PQ_SKINNY(1, 4) PQ_SKINNY(1, 8) PQ_SKINNY(1, 16) PQ_SKINNY(2, 4) PQ_SKINNY(2, 8) PQ_SKINNY(2, 16)
@@ -352,6 +484,25 @@ int check_gemm_args(const char* who, int64_t m, int64_t n, int64_t k, int group_
 }
 
 }  // namespace
+
+namespace pq {
+bool gemm_rotated_supported(int64_t m, int64_t k) {
+  return m >= 1 && m <= kSkinnyRows && k % 128 == 0 && k <= 16384 && m * (k + 16) <= 80 * 1024;
+}
+
+void launch_gemm_rotated(const void* xr, bool xr_fp16, const float* gmax, const uint8_t* wpack, const uint32_t* wmeta,
+                         const void* bias, int bias_dtype, void* y, int y_dtype, int m, int n, int k,
+                         hipStream_t stream) {
+  SkinnyCfg cfg = choose_skinny(m, n, k);
+  if (cfg.w == 16) cfg.nt = 1;   // two tiles x 16 waves would spill next to the prologue
+  if (xr_fp16)
+    launch_skinny<false, 1>(cfg, nullptr, nullptr, xr, gmax, wpack, wmeta, bias, bias_dtype, y, y_dtype, nullptr, m,
+                            n, k, stream);
+  else
+    launch_skinny<false, 2>(cfg, nullptr, nullptr, xr, gmax, wpack, wmeta, bias, bias_dtype, y, y_dtype, nullptr, m,
+                            n, k, stream);
+}
+}  // namespace pq
 
 extern "C" size_t pq_w4a8_workspace_size(int64_t m, int64_t n, int64_t k, int group_size) {
   // No kernel of this version exchanges data between workgroups.
@@ -377,7 +528,7 @@ extern "C" int pq_w4a8_gemm(const int8_t* xq, const float* xscale, const uint8_t
   const int M = static_cast<int>(m), N = static_cast<int>(n), K = static_cast<int>(k);
   if (m <= kSkinnyMaxM) {
     (void)workspace, (void)workspace_bytes;
-    launch_skinny<false>(choose_skinny(m, n, k), xq, xscale, wpack, wmeta, bias, bias_dtype, y, y_dtype, nullptr, M,
+    launch_skinny<false, 0>(choose_skinny(m, n, k), xq, xscale, nullptr, nullptr, wpack, wmeta, bias, bias_dtype, y, y_dtype, nullptr, M,
                          N, K, s);
   } else {
     const unsigned grid = static_cast<unsigned>(((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN));
@@ -399,7 +550,7 @@ extern "C" int pq_w4a8_gemm_partials(const int8_t* xq, const uint8_t* wpack, con
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int M = static_cast<int>(m), N = static_cast<int>(n), K = static_cast<int>(k);
   if (m <= kSkinnyMaxM) {
-    launch_skinny<true>(choose_skinny(m, n, k), xq, nullptr, wpack, wmeta, nullptr, 0, nullptr, 0, partials, M, N,
+    launch_skinny<true, 0>(choose_skinny(m, n, k), xq, nullptr, nullptr, nullptr, wpack, wmeta, nullptr, 0, nullptr, 0, partials, M, N,
                         K, s);
   } else {
     const unsigned grid = static_cast<unsigned>(((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN));

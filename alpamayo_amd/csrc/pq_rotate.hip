@@ -16,6 +16,7 @@
 #include <type_traits>
 
 #include "pq_device.h"
+#include "pq_internal.h"
 
 using pqd::quant4;
 
@@ -23,7 +24,6 @@ namespace {
 
 constexpr int kRotRows = 4;   // rows per workgroup of the plain rotation kernel
 
-#define PQ_LDS_WAVE_FENCE() __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront", "local")
 
 // ---------------------------------------------------------------------------
 // rotation::rotate.  One wave per (4 rows x 128 channels); lane t owns pair t
@@ -132,66 +132,23 @@ __device__ __forceinline__ void load8(const void* base, int64_t elem, float f[8]
 }
 
 
-// One lane's packed rotation parameters for one group: KP layers of
-// (first | second << 8) in 16-byte words and of (cos, sin).  Layout (built by
-// pq_rotation_pack): rot_ij [G][64][KP] uint16, rot_cs [G][64][KP][2] float.
-template <int KP>
-struct LaneParams {
-  uint32_t ij[KP / 2];
-  float cs[2 * KP];
-};
-
-template <int KP>
-__device__ __forceinline__ void load_lane_params(const uint16_t* __restrict__ rot_ij, const float* __restrict__ rot_cs,
-                                                 int g, int lane, LaneParams<KP>& p) {
-  const int64_t o = (static_cast<int64_t>(g) * 64 + lane) * KP;
-  const uint4* ij = reinterpret_cast<const uint4*>(rot_ij + o);
-#pragma unroll
-  for (int q = 0; q < KP / 8; ++q) {
-    const uint4 v = ij[q];
-    p.ij[4 * q] = v.x;
-    p.ij[4 * q + 1] = v.y;
-    p.ij[4 * q + 2] = v.z;
-    p.ij[4 * q + 3] = v.w;
-  }
-  const float4* cs = reinterpret_cast<const float4*>(rot_cs + 2 * o);
-#pragma unroll
-  for (int q = 0; q < KP / 2; ++q) {
-    const float4 v = cs[q];
-    p.cs[4 * q] = v.x;
-    p.cs[4 * q + 1] = v.y;
-    p.cs[4 * q + 2] = v.z;
-    p.cs[4 * q + 3] = v.w;
-  }
-}
-
-template <int KP>
-__device__ __forceinline__ int pair_first(const LaneParams<KP>& p, int r) {
-  return (p.ij[r >> 1] >> (16 * (r & 1))) & 127;
-}
-template <int KP>
-__device__ __forceinline__ int pair_second(const LaneParams<KP>& p, int r) {
-  return (p.ij[r >> 1] >> (16 * (r & 1) + 8)) & 127;
-}
-
 // ---------------------------------------------------------------------------
-// Fused rotate + quant over blocks of RB rows (RB a compile-time constant:
-// the RB rows are RB independent LDS chains per layer, with no per-row
-// branches).  512 threads; wave w rotates groups w, w+8, ... for the block's
-// rows in a private fp32 scratch [RB][128] (lane t owns the pair the packed
-// parameters give it; the packed order makes each layer's LDS accesses
-// bank-conflict free) and stores the finished values in a row buffer
-// [RB][h] (fp16 when the result is materialized in fp16, fp32 otherwise).
-// The next group's parameters and inputs are requested before the current
-// group's layers run.  After a block-wide absmax per row the row buffer is
-// quantized with coalesced stores.  Parameters are read once per group per
-// RB rows.
+// Fused rotate + quant over blocks of RB rows (RB a compile-time constant, so
+// the RB rows are RB independent register chains with no per-row branches).
+// 512 threads; wave w rotates groups w, w+8, ... for the block's rows: lane l
+// loads channels l and l+64 of each row (coalesced) and runs the packed
+// register chain (one cross-lane fetch per layer, no LDS traffic inside the
+// layers), then stores the finished values into a row buffer [RB][h] (fp16
+// when the result is materialized in fp16, fp32 otherwise).  The next group's
+// parameters and inputs are requested before the current group's layers run.
+// After a block-wide absmax per row the row buffer is quantized with
+// coalesced stores.  Parameters are read once per group per RB rows.
 // ---------------------------------------------------------------------------
 constexpr int kRQWaves = 8;
 
 template <int DT, int KP, bool MAT16, int RB>
 __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(
-    const void* __restrict__ x, const uint16_t* __restrict__ rot_ij, const float* __restrict__ rot_cs,
+    const void* __restrict__ x, const uint32_t* __restrict__ rot_idx, const float* __restrict__ rot_cs,
     const float* __restrict__ scales, int8_t* __restrict__ xq, float* __restrict__ xscale,
     uint16_t* __restrict__ xrot, int64_t row_begin, int h, int krot, unsigned flags) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
@@ -199,84 +156,70 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(
   using RowT = typename std::conditional<MAT16, uint16_t, float>::type;
   const int t = threadIdx.x;
   const int lane = t & 63;
-  const int w = t >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);   // wave-uniform: scalar branches
   const bool in16 = (flags & PQ_RQ_INPUT_FP16) != 0;
   const int G = h >> 7;
-  float* scratch = reinterpret_cast<float*>(lds_raw) + w * (RB * 128);
-  RowT* rowbuf = reinterpret_cast<RowT*>(lds_raw + kRQWaves * RB * 128 * sizeof(float));
+  RowT* rowbuf = reinterpret_cast<RowT*>(lds_raw);
   const int64_t row0 = row_begin + static_cast<int64_t>(blockIdx.x) * RB;
+  // Channel-scale loads stay unconditional: without scales they read
+  // rot_cs[0] and the value is replaced by 1.
+  const bool has_scales = scales != nullptr;
+  const float* sp = has_scales ? scales : rot_cs;
+  const int smask = has_scales ? 0x7fffffff : 0;
 
   float rmax[RB];
 #pragma unroll
   for (int r = 0; r < RB; ++r) rmax[r] = 0.0f;
 
-  LaneParams<KP> cur, nxt;
-  float xa[RB], xb[RB], xan[RB], xbn[RB];
+  pqd::RotLane<KP> cur, nxt;
+  uint32_t xa[RB], xb[RB], xan[RB], xbn[RB];
   float sa = 1.0f, sb = 1.0f, san = 1.0f, sbn = 1.0f;
-  auto load_inputs = [&](int g, float (&va)[RB], float (&vb)[RB], float& s0, float& s1) {
+  auto load_inputs = [&](int g, uint32_t (&va)[RB], uint32_t (&vb)[RB], float& s0, float& s1) {
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-      va[r] = pq_load_as_f32<DT>(x, (row0 + r) * h + g * 128 + lane);
-      vb[r] = pq_load_as_f32<DT>(x, (row0 + r) * h + g * 128 + 64 + lane);
+      va[r] = pq_load_raw<DT>(x, (row0 + r) * h + g * 128 + lane);
+      vb[r] = pq_load_raw<DT>(x, (row0 + r) * h + g * 128 + 64 + lane);
     }
-    if (scales != nullptr) {
-      s0 = scales[g * 128 + lane];
-      s1 = scales[g * 128 + 64 + lane];
-    }
+    s0 = sp[(g * 128 + lane) & smask];
+    s1 = sp[(g * 128 + 64 + lane) & smask];
   };
 
   if (w < G) {
-    load_lane_params<KP>(rot_ij, rot_cs, w, lane, cur);
+    pqd::load_rot_lane<KP>(rot_idx, rot_cs, w, lane, cur);
     load_inputs(w, xa, xb, sa, sb);
   }
   for (int g = w; g < G; g += kRQWaves) {
     const int gn = (g + kRQWaves < G) ? g + kRQWaves : g;   // clamped: the loads stay unconditional
-    load_lane_params<KP>(rot_ij, rot_cs, gn, lane, nxt);
+    pqd::load_rot_lane<KP>(rot_idx, rot_cs, gn, lane, nxt);
     load_inputs(gn, xan, xbn, san, sbn);
 
+    const bool sw = pqd::rot_init_swapped(cur);
+    const float s0 = has_scales ? sa : 1.0f, s1 = has_scales ? sb : 1.0f;
+    float a[RB], b[RB];
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-      const float a = in16 ? pq_round_f16(xa[r]) : xa[r];
-      const float b = in16 ? pq_round_f16(xb[r]) : xb[r];
-      scratch[r * 128 + lane] = a * sa;
-      scratch[r * 128 + 64 + lane] = b * sb;
+      float lo = pq_raw_to_f32<DT>(xa[r]), hi = pq_raw_to_f32<DT>(xb[r]);
+      lo = (in16 ? pq_round_f16(lo) : lo) * s0;
+      hi = (in16 ? pq_round_f16(hi) : hi) * s1;
+      a[r] = sw ? hi : lo;
+      b[r] = sw ? lo : hi;
     }
-    PQ_LDS_WAVE_FENCE();
-    float ni[RB], nj[RB];
-    int i = 0, j = 0;
 #pragma unroll
-    for (int k = 0; k < KP; ++k) {
-      if (k < krot) {
-        i = pair_first(cur, k);
-        j = pair_second(cur, k);
-        const float c = cur.cs[2 * k], sn = cur.cs[2 * k + 1];
-        float xi[RB], xj[RB];
-#pragma unroll
-        for (int r = 0; r < RB; ++r) {
-          xi[r] = scratch[r * 128 + i];
-          xj[r] = scratch[r * 128 + j];
-        }
-#pragma unroll
-        for (int r = 0; r < RB; ++r) {
-          pqd::givens(xi[r], xj[r], c, sn, ni[r], nj[r]);
-          scratch[r * 128 + i] = ni[r];
-          scratch[r * 128 + j] = nj[r];
-        }
-        PQ_LDS_WAVE_FENCE();
-      }
-    }
+    for (int k = 0; k < KP; ++k)
+      if (k < krot) pqd::rot_layer<KP, RB>(cur, k, a, b);
+    const int fa = g * 128 + pqd::rot_final_a(cur), fb = g * 128 + pqd::rot_final_b(cur);
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-      float vi = ni[r], vj = nj[r];
+      float vi = a[r], vj = b[r];
       if constexpr (MAT16) {
         const uint16_t hi = pq_f32_to_f16(vi), hj = pq_f32_to_f16(vj);
-        rowbuf[r * h + g * 128 + i] = hi;
-        rowbuf[r * h + g * 128 + j] = hj;
+        rowbuf[r * h + fa] = hi;
+        rowbuf[r * h + fb] = hj;
         vi = pq_f16_to_f32(hi);
         vj = pq_f16_to_f32(hj);
       } else {
-        rowbuf[r * h + g * 128 + i] = vi;
-        rowbuf[r * h + g * 128 + j] = vj;
+        rowbuf[r * h + fa] = vi;
+        rowbuf[r * h + fb] = vj;
       }
       rmax[r] = fmaxf(rmax[r], fmaxf(fabsf(vi), fabsf(vj)));
     }
@@ -335,6 +278,103 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(
     o.y = quant4(f[4], f[5], f[6], f[7], inv);
     *reinterpret_cast<uint2*>(xq + (row0 + r) * h + c8) = o;
     if (c8 == 0) xscale[row0 + r] = am / 127.0f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Split rotation for decode-size inputs: one wave per 128-channel group and
+// MR rows (M <= MR <= 16; rows past M repeat row M-1 and are not stored), so
+// the K/128 groups run on K/128 waves spread over the chip and every
+// parameter byte is read once.  Writes the rotated rows (fp16 when
+// materialized in fp16, else fp32) and each row's absmax per group; the
+// GEMM that follows derives the token scale and quantizes.
+// ---------------------------------------------------------------------------
+constexpr int kSplitWaves = 4;
+
+template <int DT, int KP, bool MAT16, int MR>
+__global__ __launch_bounds__(kSplitWaves * 64) void rotate_split_kernel(
+    const void* __restrict__ x, const uint32_t* __restrict__ rot_idx, const float* __restrict__ rot_cs,
+    const float* __restrict__ scales, void* __restrict__ xr, float* __restrict__ gmax, int M, int h, int krot,
+    unsigned flags) {
+  const int lane = threadIdx.x & 63;
+  const int G = h >> 7;
+  const int g = blockIdx.x * kSplitWaves + (threadIdx.x >> 6);
+  if (g >= G) return;   // whole waves only; this kernel has no barrier
+  const bool in16 = (flags & PQ_RQ_INPUT_FP16) != 0;
+  const bool has_scales = scales != nullptr;
+  const float* sp = has_scales ? scales : rot_cs;
+  const int smask = has_scales ? 0x7fffffff : 0;
+
+  pqd::RotLane<KP> p;
+  pqd::load_rot_lane<KP>(rot_idx, rot_cs, g, lane, p);
+  uint32_t xa[MR], xb[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    const int mm = m < M ? m : M - 1;
+    xa[m] = pq_load_raw<DT>(x, static_cast<int64_t>(mm) * h + g * 128 + lane);
+    xb[m] = pq_load_raw<DT>(x, static_cast<int64_t>(mm) * h + g * 128 + 64 + lane);
+  }
+  const float s0r = sp[(g * 128 + lane) & smask];
+  const float s1r = sp[(g * 128 + 64 + lane) & smask];
+  const float s0 = has_scales ? s0r : 1.0f, s1 = has_scales ? s1r : 1.0f;
+  const bool sw = pqd::rot_init_swapped(p);
+  float a[MR], b[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    float lo = pq_raw_to_f32<DT>(xa[m]), hi = pq_raw_to_f32<DT>(xb[m]);
+    lo = (in16 ? pq_round_f16(lo) : lo) * s0;
+    hi = (in16 ? pq_round_f16(hi) : hi) * s1;
+    a[m] = sw ? hi : lo;
+    b[m] = sw ? lo : hi;
+  }
+#pragma unroll
+  for (int k = 0; k < KP; ++k)
+    if (k < krot) pqd::rot_layer<KP, MR>(p, k, a, b);
+  const int fa = g * 128 + pqd::rot_final_a(p), fb = g * 128 + pqd::rot_final_b(p);
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    float va = a[m], vb = b[m];
+    if (m < M) {
+      if constexpr (MAT16) {
+        const uint16_t ha = pq_f32_to_f16(va), hb = pq_f32_to_f16(vb);
+        static_cast<uint16_t*>(xr)[static_cast<int64_t>(m) * h + fa] = ha;
+        static_cast<uint16_t*>(xr)[static_cast<int64_t>(m) * h + fb] = hb;
+        va = pq_f16_to_f32(ha);
+        vb = pq_f16_to_f32(hb);
+      } else {
+        static_cast<float*>(xr)[static_cast<int64_t>(m) * h + fa] = va;
+        static_cast<float*>(xr)[static_cast<int64_t>(m) * h + fb] = vb;
+      }
+    }
+    const float mx = pq_wave_max(fmaxf(fabsf(va), fabsf(vb)));
+    if (m < M && lane == 0) gmax[static_cast<int64_t>(m) * G + g] = mx;
+  }
+}
+
+template <int DT, int KP, bool MAT16>
+void launch_split_kp(const void* x, const uint32_t* rot_idx, const float* rot_cs, const float* scales, void* xr,
+                     float* gmax, int M, int h, int krot, unsigned flags, hipStream_t stream) {
+  const unsigned grid = static_cast<unsigned>((h / 128 + kSplitWaves - 1) / kSplitWaves);
+#define PQ_SPLIT(MR_)                                                                                            \
+  if (M <= MR_) {                                                                                                \
+    rotate_split_kernel<DT, KP, MAT16, MR_><<<grid, kSplitWaves * 64, 0, stream>>>(x, rot_idx, rot_cs, scales, xr, \
+                                                                                   gmax, M, h, krot, flags);    \
+    return;                                                                                                      \
+  }
+  PQ_SPLIT(1) PQ_SPLIT(2) PQ_SPLIT(4) PQ_SPLIT(8) PQ_SPLIT(16)
+#undef PQ_SPLIT
+}
+
+template <int DT>
+void launch_split_dt(const void* x, const uint32_t* rot_idx, const float* rot_cs, const float* scales, void* xr,
+                     float* gmax, int M, int h, int krot, unsigned flags, hipStream_t stream) {
+  const bool mat16 = (flags & PQ_RQ_MATERIALIZE_FP16) != 0;
+  if (krot <= 8) {
+    if (mat16) launch_split_kp<DT, 8, true>(x, rot_idx, rot_cs, scales, xr, gmax, M, h, krot, flags, stream);
+    else launch_split_kp<DT, 8, false>(x, rot_idx, rot_cs, scales, xr, gmax, M, h, krot, flags, stream);
+  } else {
+    if (mat16) launch_split_kp<DT, 16, true>(x, rot_idx, rot_cs, scales, xr, gmax, M, h, krot, flags, stream);
+    else launch_split_kp<DT, 16, false>(x, rot_idx, rot_cs, scales, xr, gmax, M, h, krot, flags, stream);
   }
 }
 
@@ -398,43 +438,42 @@ inline int rq_rows_per_block(int64_t rows, int h, bool mat16) {
 }
 
 template <int DT, int KP, bool MAT16, int RB>
-void launch_rq_rb(const void* x, const uint16_t* rot_ij, const float* rot_cs, const float* scales, int8_t* xq,
+void launch_rq_rb(const void* x, const uint32_t* rot_idx, const float* rot_cs, const float* scales, int8_t* xq,
                   float* xscale, void* xrot, int64_t row_begin, int64_t nblocks, int h, int krot, unsigned flags,
                   hipStream_t stream) {
   if (nblocks <= 0) return;
-  const size_t lds = static_cast<size_t>(kRQWaves) * RB * 128 * sizeof(float) +
-                     static_cast<size_t>(RB) * h * (MAT16 ? 2 : 4);
+  const size_t lds = static_cast<size_t>(RB) * h * (MAT16 ? 2 : 4);
   rotate_quant_kernel<DT, KP, MAT16, RB><<<static_cast<unsigned>(nblocks), kRQWaves * 64, lds, stream>>>(
-      x, rot_ij, rot_cs, scales, xq, xscale, static_cast<uint16_t*>(xrot), row_begin, h, krot, flags);
+      x, rot_idx, rot_cs, scales, xq, xscale, static_cast<uint16_t*>(xrot), row_begin, h, krot, flags);
 }
 
 template <int DT, int KP, bool MAT16>
-void launch_rq(const void* x, const uint16_t* rot_ij, const float* rot_cs, const float* scales, int8_t* xq,
+void launch_rq(const void* x, const uint32_t* rot_idx, const float* rot_cs, const float* scales, int8_t* xq,
                float* xscale, void* xrot, int64_t rows, int h, int krot, unsigned flags, hipStream_t stream) {
   const int rb = rq_rows_per_block(rows, h, MAT16);
   const int64_t full = rows / rb;
   switch (rb) {
-    case 8: launch_rq_rb<DT, KP, MAT16, 8>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, 0, full, h, krot, flags, stream); break;
-    case 4: launch_rq_rb<DT, KP, MAT16, 4>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, 0, full, h, krot, flags, stream); break;
-    case 2: launch_rq_rb<DT, KP, MAT16, 2>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, 0, full, h, krot, flags, stream); break;
+    case 8: launch_rq_rb<DT, KP, MAT16, 8>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, 0, full, h, krot, flags, stream); break;
+    case 4: launch_rq_rb<DT, KP, MAT16, 4>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, 0, full, h, krot, flags, stream); break;
+    case 2: launch_rq_rb<DT, KP, MAT16, 2>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, 0, full, h, krot, flags, stream); break;
     default: break;
   }
   const int64_t done = rb > 1 ? full * rb : 0;   // the remaining rows, one block each
-  launch_rq_rb<DT, KP, MAT16, 1>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, done, rows - done, h, krot, flags,
+  launch_rq_rb<DT, KP, MAT16, 1>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, done, rows - done, h, krot, flags,
                                  stream);
 }
 
 template <int DT>
-void launch_rotate_quant(const void* x, const uint16_t* rot_ij, const float* rot_cs, const float* scales, int8_t* xq,
+void launch_rotate_quant(const void* x, const uint32_t* rot_idx, const float* rot_cs, const float* scales, int8_t* xq,
                          float* xscale, void* xrot, int64_t rows, int h, int krot, unsigned flags,
                          hipStream_t stream) {
   const bool mat16 = (flags & PQ_RQ_MATERIALIZE_FP16) != 0;
   if (krot <= 8) {
-    if (mat16) launch_rq<DT, 8, true>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
-    else launch_rq<DT, 8, false>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
+    if (mat16) launch_rq<DT, 8, true>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
+    else launch_rq<DT, 8, false>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
   } else {
-    if (mat16) launch_rq<DT, 16, true>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
-    else launch_rq<DT, 16, false>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
+    if (mat16) launch_rq<DT, 16, true>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
+    else launch_rq<DT, 16, false>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
   }
 }
 
@@ -445,6 +484,18 @@ void launch_quant(const void* x, int8_t* xq, float* xscale, int64_t rows, int h,
 }
 
 }  // namespace
+
+namespace pq {
+void launch_rotate_split(const void* x, int x_dtype, const uint32_t* rot_idx, const float* rot_cs,
+                         const float* scales, void* xr, float* gmax, int m, int h, int krot, unsigned flags,
+                         hipStream_t stream) {
+  switch (x_dtype) {
+    case PQ_F32: launch_split_dt<PQ_F32>(x, rot_idx, rot_cs, scales, xr, gmax, m, h, krot, flags, stream); break;
+    case PQ_F16: launch_split_dt<PQ_F16>(x, rot_idx, rot_cs, scales, xr, gmax, m, h, krot, flags, stream); break;
+    default: launch_split_dt<PQ_BF16>(x, rot_idx, rot_cs, scales, xr, gmax, m, h, krot, flags, stream); break;
+  }
+}
+}  // namespace pq
 
 extern "C" int pq_rotate(const void* x, void* y, const int16_t* idx_ij, const void* theta, const void* scales,
                          int64_t rows, int64_t h, int krot, int group_size, int dtype, void* stream) {
@@ -471,7 +522,7 @@ extern "C" int pq_rotate(const void* x, void* y, const int16_t* idx_ij, const vo
   return pq::launch_status("pq_rotate launch");
 }
 
-extern "C" int pq_rotate_quant_i8(const void* x, int x_dtype, const uint16_t* rot_ij, const float* rot_cs,
+extern "C" int pq_rotate_quant_i8(const void* x, int x_dtype, const uint32_t* rot_idx, const float* rot_cs,
                                   const float* scales, int8_t* xq, float* xscale, void* xrot, int64_t rows,
                                   int64_t h, int krot, unsigned flags, void* stream) {
   PQ_REQUIRE(rows >= 0 && rows <= 0x7fffffffLL && h > 0 && h % 128 == 0 && h <= 16384, PQ_ERR_ARG,
@@ -483,17 +534,17 @@ extern "C" int pq_rotate_quant_i8(const void* x, int x_dtype, const uint16_t* ro
   PQ_REQUIRE((flags & ~(PQ_RQ_INPUT_FP16 | PQ_RQ_MATERIALIZE_FP16)) == 0, PQ_ERR_ARG,
              "pq_rotate_quant_i8: unknown flags 0x%x", flags);
   if (rows == 0) return PQ_OK;
-  PQ_REQUIRE(x && rot_ij && rot_cs && xq && xscale, PQ_ERR_ARG, "pq_rotate_quant_i8: null pointer");
-  PQ_REQUIRE(pq::aligned_to(x, 16) && pq::aligned_to(xq, 8) && pq::aligned_to(rot_ij, 16) &&
+  PQ_REQUIRE(x && rot_idx && rot_cs && xq && xscale, PQ_ERR_ARG, "pq_rotate_quant_i8: null pointer");
+  PQ_REQUIRE(pq::aligned_to(x, 16) && pq::aligned_to(xq, 8) && pq::aligned_to(rot_idx, 16) &&
                  pq::aligned_to(rot_cs, 16) && (xrot == nullptr || pq::aligned_to(xrot, 16)),
              PQ_ERR_ARG,
-             "pq_rotate_quant_i8: x, rot_ij, rot_cs and xrot must be 16-byte aligned, xq 8-byte aligned");
+             "pq_rotate_quant_i8: x, rot_idx, rot_cs and xrot must be 16-byte aligned, xq 8-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int hh = static_cast<int>(h);
   switch (x_dtype) {
-    case PQ_F32: launch_rotate_quant<PQ_F32>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
-    case PQ_F16: launch_rotate_quant<PQ_F16>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
-    default: launch_rotate_quant<PQ_BF16>(x, rot_ij, rot_cs, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
+    case PQ_F32: launch_rotate_quant<PQ_F32>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
+    case PQ_F16: launch_rotate_quant<PQ_F16>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
+    default: launch_rotate_quant<PQ_BF16>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
   }
   return pq::launch_status("pq_rotate_quant_i8 launch");
 }

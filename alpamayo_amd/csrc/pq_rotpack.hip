@@ -3,25 +3,37 @@
 // Reference parameters (src/alpamayo_r1/utils/quantization/rotation_linear.py:
 // 39-43): pairs int16 [krot][h] with group-local indices (pair t of group g in
 // layer r = pairs[r][g*128+2t], pairs[r][g*128+2t+1]) and angles [krot][h/2].
-// Kernel layout (one entry per (group, lane, layer); the lane owns one pair):
-//   rot_ij [G][64][KP]     uint16  first | second << 8
-//   rot_cs [G][64][KP][2]  float32 (cos, sin)
-// with KP = krot rounded up to a multiple of 8, so one lane's indices for 8
-// layers are 16 contiguous bytes and its angles 64 contiguous bytes.
 //
-// Which lane owns which pair, and which element of a pair comes first, is
-// free: a Givens update on (i, j) with angle theta equals the update on
-// (j, i) with -theta, bit for bit in the kernels' float32 form
-// (fma(xi, c, xj*s) with s -> -s is fma(xi, c, -(xj*(-s)))...).  The packer
-// uses that freedom to make every layer's LDS accesses bank-conflict free
-// (32 banks of 4 bytes, a wave64 LDS access served as two halves of 32
-// lanes): bank(ch) = ch mod 32, so the 64 pairs of a group and layer form a
-// 4-regular multigraph on the 32 banks.  Orienting each component along an
-// Euler circuit gives every bank in- and out-degree 2; the oriented edges
-// then form a 2-regular bipartite graph (tail bank -> head bank), which
-// splits into two perfect matchings.  Matching 0 goes to lanes 0..31 and
-// matching 1 to lanes 32..63, lane = 32*m + tail bank, so in each half the
-// first elements hit 32 distinct banks and so do the second elements.
+// The kernels rotate a 128-channel group with one wave and keep the data in
+// registers: lane l loads channels l and l+64 (coalesced), and in every layer
+// it holds the two channels of one pair in two slots A and B.  Before each
+// layer a lane keeps one of its channels and fetches the other from the lane
+// that holds it, with one ds_bpermute.  That works because the pairs of two
+// consecutive layers form a union of even cycles (alternating between the
+// two layers): walking each cycle, call the channel a pair shares with the
+// next pair of the following layer "kept" and its other channel "given"; the
+// lane of a pair then moves on to the pair of the next layer that contains
+// its kept channel and receives the given channel of the next pair on the
+// walk.  The load layout counts as a layer before the first one, with lane l
+// holding the pair (l, l+64).  Slot A always holds the channel given away
+// next, so every fetch reads slot A of its source lane; a per-layer flag says
+// whether the received value enters slot A or slot B.
+//
+// Operands (KP = 8 for krot <= 8, else 16):
+//   rot_idx [G][64][KP/2] uint32, per lane:
+//     word 0      Af | Bf << 8 | init << 16: the channels in slots A and B
+//                 after the last layer, and whether slot A starts with
+//                 channel l+64 (else l)
+//     byte 4 + r  (layer r = 0 .. krot-1) src | flag << 7: the lane the
+//                 channel received before layer r comes from, and whether it
+//                 enters slot A
+//   rot_cs  [G][64][KP][2] float32 (cos, sin) of the lane's pair in layer r,
+//                 sin negated when slot A holds the pair's second channel.
+// A Givens update on (i, j) with angle theta equals the update on (j, i)
+// with -theta bit for bit in the kernels' float32 form
+//   a' = fma(a, c, b*s),  b' = fma(b, c, -(a*s))
+// since b*(-s) == -(b*s) exactly, so the slot order is free.
+#include <algorithm>
 #include <cstring>
 #include <vector>
 
@@ -29,90 +41,39 @@
 
 namespace {
 
-struct Edge {
-  int a, b;      // channels of the pair (a first)
-  float c, s;
-  int u, v;      // banks of a, b
-  int tail = -1, head = -1;
-  int color = -1;
+struct Layer {
+  int i[64], j[64];   // pair t = (first, second) as stored
+  float c[64], s[64];
+  int pos[128];       // channel -> pair index
 };
-
-// Orients every edge of the bank multigraph along Euler circuits.
-void orient(std::vector<Edge>& e) {
-  const int nb = 32;
-  std::vector<std::vector<int>> adj(nb);
-  for (int k = 0; k < static_cast<int>(e.size()); ++k) {
-    adj[e[k].u].push_back(k);
-    if (e[k].v != e[k].u) adj[e[k].v].push_back(k);
-    else adj[e[k].u].push_back(k);   // a loop appears twice in its bank's list
-  }
-  std::vector<size_t> next(nb, 0);
-  std::vector<char> used(e.size(), 0);
-  for (int start = 0; start < nb; ++start) {
-    // Hierholzer walk: each traversed edge is oriented from where we stand.
-    std::vector<int> stack{start};
-    while (!stack.empty()) {
-      const int x = stack.back();
-      while (next[x] < adj[x].size() && used[adj[x][next[x]]]) ++next[x];
-      if (next[x] == adj[x].size()) {
-        stack.pop_back();
-        continue;
-      }
-      const int k = adj[x][next[x]++];
-      used[k] = 1;
-      const int y = (e[k].u == x) ? e[k].v : e[k].u;
-      e[k].tail = x;
-      e[k].head = y;
-      stack.push_back(y);
-    }
-  }
-}
-
-// Splits the oriented edges (every bank: out 2, in 2) into two matchings.
-bool split(std::vector<Edge>& e) {
-  const int nb = 32;
-  std::vector<std::vector<int>> out(nb), in(nb);
-  for (int k = 0; k < static_cast<int>(e.size()); ++k) {
-    out[e[k].tail].push_back(k);
-    in[e[k].head].push_back(k);
-  }
-  for (int b = 0; b < nb; ++b)
-    if (out[b].size() != 2 || in[b].size() != 2) return false;
-  for (int k0 = 0; k0 < static_cast<int>(e.size()); ++k0) {
-    if (e[k0].color >= 0) continue;
-    // Walk the alternating cycle: tail side shares color pairs 0/1, head side too.
-    int k = k0, color = 0;
-    while (e[k].color < 0) {
-      e[k].color = color;
-      // the other edge entering the same head gets the other color
-      const int h = e[k].head;
-      const int k2 = in[h][0] == k ? in[h][1] : in[h][0];
-      if (e[k2].color >= 0) break;
-      e[k2].color = 1 - color;
-      // the other edge leaving k2's tail continues the cycle with `color`
-      const int t = e[k2].tail;
-      k = out[t][0] == k2 ? out[t][1] : out[t][0];
-    }
-  }
-  int count0 = 0;
-  for (auto& x : e) count0 += x.color == 0;
-  return count0 == 32;
-}
 
 }  // namespace
 
-extern "C" int pq_rotation_pack(const int16_t* pairs, const float* cos_sin, int64_t h, int krot, uint16_t* rot_ij,
+extern "C" int pq_rotation_pack(const int16_t* pairs, const float* cos_sin, int64_t h, int krot, uint32_t* rot_idx,
                                 float* rot_cs) {
-  PQ_REQUIRE(pairs && cos_sin && rot_ij && rot_cs, PQ_ERR_ARG, "pq_rotation_pack: null pointer");
+  PQ_REQUIRE(pairs && cos_sin && rot_idx && rot_cs, PQ_ERR_ARG, "pq_rotation_pack: null pointer");
   PQ_REQUIRE(h > 0 && h % 128 == 0 && h <= (1 << 20), PQ_ERR_ARG, "pq_rotation_pack: h=%lld", (long long)h);
-  PQ_REQUIRE(krot >= 1 && krot <= 64, PQ_ERR_ARG, "pq_rotation_pack: krot=%d", krot);
+  PQ_REQUIRE(krot >= 1 && krot <= 16, PQ_ERR_ARG, "pq_rotation_pack: krot=%d not in 1..16", krot);
   const int G = static_cast<int>(h / 128);
-  const int KP = (krot + 7) / 8 * 8;
-  std::memset(rot_ij, 0, sizeof(uint16_t) * G * 64 * KP);
+  const int KP = krot <= 8 ? 8 : 16;
+  const int KW = KP / 2;
+  const int NL = krot + 1;   // layer 0 = the load layout (l, l+64); layer k = reference layer k-1
+  std::memset(rot_idx, 0, sizeof(uint32_t) * G * 64 * KW);
   std::memset(rot_cs, 0, sizeof(float) * G * 64 * KP * 2);
-  std::vector<Edge> e(64);
+  std::vector<Layer> L(NL);
+  for (int t = 0; t < 64; ++t) {
+    L[0].i[t] = t;
+    L[0].j[t] = t + 64;
+    L[0].c[t] = 1.0f;
+    L[0].s[t] = 0.0f;
+    L[0].pos[t] = t;
+    L[0].pos[t + 64] = t;
+  }
+  std::vector<int> give(NL * 64), nextpair(NL * 64), srcpair(NL * 64), lane_of(NL * 64);
+  std::vector<int> slotA(NL * 64), slotB(NL * 64), src(NL * 64), flag(NL * 64);
   for (int g = 0; g < G; ++g) {
     for (int r = 0; r < krot; ++r) {
+      Layer& l = L[r + 1];
       int seen[128] = {0};
       for (int t = 0; t < 64; ++t) {
         const int a = pairs[static_cast<int64_t>(r) * h + g * 128 + 2 * t];
@@ -121,33 +82,79 @@ extern "C" int pq_rotation_pack(const int16_t* pairs, const float* cos_sin, int6
                    "pq_rotation_pack: pair index out of [0,128) in layer %d group %d", r, g);
         ++seen[a];
         ++seen[b];
-        Edge x;
-        x.a = a;
-        x.b = b;
-        x.c = cos_sin[(static_cast<int64_t>(r) * (h / 2) + g * 64 + t) * 2];
-        x.s = cos_sin[(static_cast<int64_t>(r) * (h / 2) + g * 64 + t) * 2 + 1];
-        x.u = a & 31;
-        x.v = b & 31;
-        e[t] = x;
+        l.i[t] = a;
+        l.j[t] = b;
+        l.c[t] = cos_sin[(static_cast<int64_t>(r) * (h / 2) + g * 64 + t) * 2];
+        l.s[t] = cos_sin[(static_cast<int64_t>(r) * (h / 2) + g * 64 + t) * 2 + 1];
+        l.pos[a] = t;
+        l.pos[b] = t;
       }
       for (int ch = 0; ch < 128; ++ch)
         PQ_REQUIRE(seen[ch] == 1, PQ_ERR_ARG,
                    "pq_rotation_pack: layer %d group %d does not pair every channel exactly once", r, g);
-      orient(e);
-      PQ_REQUIRE(split(e), PQ_ERR_ARG, "pq_rotation_pack: internal error splitting layer %d group %d", r, g);
-      for (const Edge& x : e) {
-        const int lane = 32 * x.color + x.tail;
-        int first = x.a, second = x.b;
-        float s = x.s;
-        if ((x.a & 31) != x.tail) {   // oriented against the stored order: swap, negate sin
-          first = x.b;
-          second = x.a;
-          s = -x.s;
+    }
+    // Orientation of layer k's pairs from the cycles of layers k and k+1.
+    std::fill(give.begin(), give.end(), -1);
+    for (int k = 0; k + 1 < NL; ++k) {
+      const Layer& a = L[k];
+      const Layer& b = L[k + 1];
+      for (int t0 = 0; t0 < 64; ++t0) {
+        if (give[k * 64 + t0] >= 0) continue;
+        int e = t0;
+        int gv = a.i[e];   // the walk enters pair e through its given channel
+        while (give[k * 64 + e] < 0) {
+          const int keep = (a.i[e] == gv) ? a.j[e] : a.i[e];
+          give[k * 64 + e] = gv;
+          const int f = b.pos[keep];
+          const int z = (b.i[f] == keep) ? b.j[f] : b.i[f];   // f's other channel
+          const int e2 = a.pos[z];                              // the pair that gives z to f
+          nextpair[k * 64 + e] = f;
+          srcpair[(k + 1) * 64 + f] = e2;
+          e = e2;
+          gv = z;
         }
-        const int64_t o = (static_cast<int64_t>(g) * 64 + lane) * KP + r;
-        rot_ij[o] = static_cast<uint16_t>(first | (second << 8));
-        rot_cs[2 * o] = x.c;
-        rot_cs[2 * o + 1] = s;
+      }
+    }
+    // Lanes: layer 0 pair t is lane t; later layers inherit.
+    for (int t = 0; t < 64; ++t) lane_of[t] = t;
+    for (int k = 0; k + 1 < NL; ++k)
+      for (int t = 0; t < 64; ++t) lane_of[(k + 1) * 64 + nextpair[k * 64 + t]] = lane_of[k * 64 + t];
+    // Slots: A = the channel given away next (the last layer keeps its fetch order).
+    for (int k = 0; k < NL; ++k) {
+      const Layer& l = L[k];
+      for (int t = 0; t < 64; ++t) {
+        const int lane = lane_of[k * 64 + t];
+        int A, B;
+        if (k == 0) {
+          A = give[t];
+          B = (A == l.i[t]) ? l.j[t] : l.i[t];
+        } else {
+          const int e2 = srcpair[k * 64 + t];
+          const int recv = give[(k - 1) * 64 + e2];
+          const int keep = (l.i[t] == recv) ? l.j[t] : l.i[t];
+          const int want = give[k * 64 + t] >= 0 ? give[k * 64 + t] : recv;
+          const int fl = (want == recv) ? 1 : 0;
+          A = fl ? recv : keep;
+          B = fl ? keep : recv;
+          src[k * 64 + lane] = lane_of[(k - 1) * 64 + e2];
+          flag[k * 64 + lane] = fl;
+          const int64_t o = (static_cast<int64_t>(g) * 64 + lane) * KP + (k - 1);
+          rot_cs[2 * o] = l.c[t];
+          rot_cs[2 * o + 1] = (A == l.i[t]) ? l.s[t] : -l.s[t];
+        }
+        slotA[k * 64 + lane] = A;
+        slotB[k * 64 + lane] = B;
+      }
+    }
+    for (int lane = 0; lane < 64; ++lane) {
+      uint32_t* w = rot_idx + (static_cast<int64_t>(g) * 64 + lane) * KW;
+      w[0] = static_cast<uint32_t>(slotA[krot * 64 + lane]) | static_cast<uint32_t>(slotB[krot * 64 + lane]) << 8 |
+             static_cast<uint32_t>(slotA[lane] == lane + 64 ? 1 : 0) << 16;
+      for (int r = 0; r < krot; ++r) {
+        const int byte = 4 + r;
+        const uint32_t v =
+            static_cast<uint32_t>(src[(r + 1) * 64 + lane]) | static_cast<uint32_t>(flag[(r + 1) * 64 + lane]) << 7;
+        w[byte / 4] |= v << (8 * (byte % 4));
       }
     }
   }

@@ -5,16 +5,16 @@
 the ``paroquant`` namespace:
 
   rotation::rotate(x, idx_ij, theta, scales?, group_size) -> y
-  paroquant::rotate_quant_i8(x, rot_ij, rot_cs, scales?, krot, input_fp16, materialize_fp16) -> (xq, xscale)
+  paroquant::rotate_quant_i8(x, rot_idx, rot_cs, scales?, krot, input_fp16, materialize_fp16) -> (xq, xscale)
   paroquant::rotate_quant_i8_rot(...)                 -> (xq, xscale, xrot fp16)
   paroquant::quant_i8(x) -> (xq, xscale)
   paroquant::w4a8_gemm(xq, xscale, wpack, wmeta, bias?, workspace?, out_dtype) -> y
   paroquant::w4a8_gemm_partials(xq, wpack, wmeta) -> int32 [m, k/128, n]
   paroquant::w4a8_prepack(awq_qweight, awq_scales, awq_qzeros) -> (wpack, wmeta)
-  paroquant::w4a8_linear(x, rot_ij, rot_cs, scales?, krot, wpack, wmeta, bias?, workspace?,
+  paroquant::w4a8_linear(x, rot_idx, rot_cs, scales?, krot, wpack, wmeta, bias?, workspace?,
                          input_fp16, materialize_fp16, out_dtype) -> y
 
-``pack_rotation`` (host) turns Rotation's pairs/angles into rot_ij/rot_cs.
+``pack_rotation`` (host) turns Rotation's pairs/angles into rot_idx/rot_cs.
 
 Implementations are registered for the CUDA (HIP) dispatch key only, like the
 reference (rotation.cu:581-584); CPU tensors raise from the dispatcher.  Each
@@ -35,16 +35,16 @@ _rotation_lib = torch.library.Library("rotation", "DEF")
 _rotation_lib.define("rotate(Tensor x, Tensor idx_ij, Tensor theta, Tensor? scales, int group_size) -> Tensor")
 
 _pq_lib = torch.library.Library("paroquant", "DEF")
-_pq_lib.define("rotate_quant_i8(Tensor x, Tensor rot_ij, Tensor rot_cs, Tensor? scales, int krot, bool input_fp16, "
+_pq_lib.define("rotate_quant_i8(Tensor x, Tensor rot_idx, Tensor rot_cs, Tensor? scales, int krot, bool input_fp16, "
                "bool materialize_fp16) -> (Tensor, Tensor)")
-_pq_lib.define("rotate_quant_i8_rot(Tensor x, Tensor rot_ij, Tensor rot_cs, Tensor? scales, int krot, "
+_pq_lib.define("rotate_quant_i8_rot(Tensor x, Tensor rot_idx, Tensor rot_cs, Tensor? scales, int krot, "
                "bool input_fp16, bool materialize_fp16) -> (Tensor, Tensor, Tensor)")
 _pq_lib.define("quant_i8(Tensor x) -> (Tensor, Tensor)")
 _pq_lib.define("w4a8_gemm(Tensor xq, Tensor xscale, Tensor wpack, Tensor wmeta, Tensor? bias, Tensor? workspace, "
                "ScalarType out_dtype) -> Tensor")
 _pq_lib.define("w4a8_gemm_partials(Tensor xq, Tensor wpack, Tensor wmeta) -> Tensor")
 _pq_lib.define("w4a8_prepack(Tensor awq_qweight, Tensor awq_scales, Tensor awq_qzeros) -> (Tensor, Tensor)")
-_pq_lib.define("w4a8_linear(Tensor x, Tensor rot_ij, Tensor rot_cs, Tensor? scales, int krot, Tensor wpack, "
+_pq_lib.define("w4a8_linear(Tensor x, Tensor rot_idx, Tensor rot_cs, Tensor? scales, int krot, Tensor wpack, "
                "Tensor wmeta, Tensor? bias, Tensor? workspace, bool input_fp16, bool materialize_fp16, "
                "ScalarType out_dtype) -> Tensor")
 
@@ -100,7 +100,7 @@ def workspace_bytes(m: int, n: int, k: int) -> int:
 
 
 def linear_workspace_bytes(m: int, n: int, k: int, krot: int) -> int:
-    """Scratch bytes paroquant::w4a8_linear needs for m tokens (0 when one fused kernel runs)."""
+    """Scratch bytes paroquant::w4a8_linear needs between its two kernels for m tokens."""
     return int(_lib.load().pq_w4a8_linear_workspace_size(m, n, k, krot))
 
 
@@ -153,50 +153,52 @@ def _rotate_fake(x, idx_ij, theta, scales, group_size):
 # ---------------------------------------------------------------------------
 
 def packed_rotation_shapes(h: int, krot: int) -> tuple[tuple, tuple]:
-    kp = (krot + 7) // 8 * 8
-    return (h // 128, 64, kp), (h // 128, 64, kp, 2)
+    kp = 8 if krot <= 8 else 16
+    return (h // 128, 64, kp // 2), (h // 128, 64, kp, 2)
 
 
 def pack_rotation(pairs: torch.Tensor, cos_sin: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Host packing of pairs int16 [krot, h] and cos_sin float32 [krot, h/2, 2] into
-    (rot_ij int16 [h/128, 64, KP], rot_cs float32 [h/128, 64, KP, 2]) on the CPU."""
+    (rot_idx int32 [h/128, 64, KP/2], rot_cs float32 [h/128, 64, KP, 2]) on the CPU,
+    KP = 8 for krot <= 8 else 16.  Raises ValueError unless every layer pairs each
+    channel of each 128-group exactly once."""
     p = pairs.detach().to("cpu", torch.int16).contiguous()
     cs = cos_sin.detach().to("cpu", torch.float32).contiguous()
     krot, h = p.shape
     _require(tuple(cs.shape) == (krot, h // 2, 2), f"cos_sin must be [{krot}, {h // 2}, 2]")
     sij, scs = packed_rotation_shapes(h, krot)
-    rot_ij = torch.empty(sij, dtype=torch.int16)
+    rot_idx = torch.empty(sij, dtype=torch.int32)
     rot_cs = torch.empty(scs, dtype=torch.float32)
-    st = _lib.load().pq_rotation_pack(p.data_ptr(), cs.data_ptr(), h, krot, rot_ij.data_ptr(), rot_cs.data_ptr())
+    st = _lib.load().pq_rotation_pack(p.data_ptr(), cs.data_ptr(), h, krot, rot_idx.data_ptr(), rot_cs.data_ptr())
     if st == _lib.STATUS_CODE["PQ_ERR_ARG"]:
         raise ValueError(_lib.load().pq_last_error().decode())
     _lib.check(st, "pack_rotation")
-    return rot_ij, rot_cs
+    return rot_idx, rot_cs
 
 
-def _check_rot_params(x, rot_ij, rot_cs, scales, krot):
+def _check_rot_params(x, rot_idx, rot_cs, scales, krot):
     h = x.size(-1)
     _require(x.dtype in _DT, f"x must be float32/float16/bfloat16, got {x.dtype}")
     _require(h % 128 == 0 and 0 < h <= 16384, f"in_features={h} must be a multiple of 128 and <= 16384")
     _require(1 <= krot <= 16, f"KROT={krot} must be in 1..16")
     sij, scs = packed_rotation_shapes(h, krot)
-    _require(rot_ij.dtype in (torch.int16, torch.uint16) and tuple(rot_ij.shape) == sij,
-             f"rot_ij must be int16 {sij}, got {rot_ij.dtype} {tuple(rot_ij.shape)}")
+    _require(rot_idx.dtype in (torch.int32, torch.uint32) and tuple(rot_idx.shape) == sij,
+             f"rot_idx must be int32 {sij}, got {rot_idx.dtype} {tuple(rot_idx.shape)}")
     _require(rot_cs.dtype == torch.float32 and tuple(rot_cs.shape) == scs,
              f"rot_cs must be float32 {scs}, got {rot_cs.dtype} {tuple(rot_cs.shape)}")
     if scales is not None:
         _require(scales.dtype == torch.float32 and scales.numel() == h,
                  f"scales must be float32 with {h} values, got {scales.dtype} {scales.numel()}")
     dev = x.device
-    _same_device("rot_ij", rot_ij, dev)
+    _same_device("rot_idx", rot_idx, dev)
     _same_device("rot_cs", rot_cs, dev)
     if scales is not None:
         _same_device("scales", scales, dev)
     return h
 
 
-def _rotate_quant(x, rot_ij, rot_cs, scales, krot, input_fp16, materialize_fp16, want_rot):
-    h = _check_rot_params(x, rot_ij, rot_cs, scales, krot)
+def _rotate_quant(x, rot_idx, rot_cs, scales, krot, input_fp16, materialize_fp16, want_rot):
+    h = _check_rot_params(x, rot_idx, rot_cs, scales, krot)
     dev = x.device
     xc = x.contiguous()
     rows = xc.numel() // h
@@ -204,24 +206,24 @@ def _rotate_quant(x, rot_ij, rot_cs, scales, krot, input_fp16, materialize_fp16,
     xs = torch.empty((rows,), dtype=torch.float32, device=dev)
     xr = torch.empty((rows, h), dtype=torch.float16, device=dev) if want_rot else None
     flags = (_lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0) | (_lib.PQ_RQ_MATERIALIZE_FP16 if materialize_fp16 else 0)
-    ij, cs = rot_ij.contiguous(), rot_cs.contiguous()
+    idx, cs = rot_idx.contiguous(), rot_cs.contiguous()
     sc = scales.contiguous() if scales is not None else None
     lib = _lib.load()
     with _DeviceGuard(dev):
-        st = lib.pq_rotate_quant_i8(xc.data_ptr(), _DT[x.dtype], ij.data_ptr(), cs.data_ptr(),
+        st = lib.pq_rotate_quant_i8(xc.data_ptr(), _DT[x.dtype], idx.data_ptr(), cs.data_ptr(),
                                     sc.data_ptr() if sc is not None else None, xq.data_ptr(), xs.data_ptr(),
                                     xr.data_ptr() if xr is not None else None, rows, h, krot, flags, _stream(dev))
     _lib.check(st, "paroquant::rotate_quant_i8")
     return xq, xs, xr
 
 
-def _rotate_quant_impl(x, rot_ij, rot_cs, scales, krot, input_fp16, materialize_fp16):
-    xq, xs, _ = _rotate_quant(x, rot_ij, rot_cs, scales, krot, input_fp16, materialize_fp16, False)
+def _rotate_quant_impl(x, rot_idx, rot_cs, scales, krot, input_fp16, materialize_fp16):
+    xq, xs, _ = _rotate_quant(x, rot_idx, rot_cs, scales, krot, input_fp16, materialize_fp16, False)
     return xq, xs
 
 
-def _rotate_quant_rot_impl(x, rot_ij, rot_cs, scales, krot, input_fp16, materialize_fp16):
-    return _rotate_quant(x, rot_ij, rot_cs, scales, krot, input_fp16, materialize_fp16, True)
+def _rotate_quant_rot_impl(x, rot_idx, rot_cs, scales, krot, input_fp16, materialize_fp16):
+    return _rotate_quant(x, rot_idx, rot_cs, scales, krot, input_fp16, materialize_fp16, True)
 
 
 _pq_lib.impl("rotate_quant_i8", _rotate_quant_impl, "CUDA")
@@ -229,14 +231,14 @@ _pq_lib.impl("rotate_quant_i8_rot", _rotate_quant_rot_impl, "CUDA")
 
 
 @torch.library.register_fake("paroquant::rotate_quant_i8")
-def _rotate_quant_fake(x, rot_ij, rot_cs, scales, krot, input_fp16, materialize_fp16):
+def _rotate_quant_fake(x, rot_idx, rot_cs, scales, krot, input_fp16, materialize_fp16):
     h = x.size(-1)
     rows = x.numel() // h
     return (x.new_empty((rows, h), dtype=torch.int8), x.new_empty((rows,), dtype=torch.float32))
 
 
 @torch.library.register_fake("paroquant::rotate_quant_i8_rot")
-def _rotate_quant_rot_fake(x, rot_ij, rot_cs, scales, krot, input_fp16, materialize_fp16):
+def _rotate_quant_rot_fake(x, rot_idx, rot_cs, scales, krot, input_fp16, materialize_fp16):
     h = x.size(-1)
     rows = x.numel() // h
     return (x.new_empty((rows, h), dtype=torch.int8), x.new_empty((rows,), dtype=torch.float32),
@@ -383,12 +385,12 @@ def _prepack_fake(awq_qweight, awq_scales, awq_qzeros):
             awq_qweight.new_empty((n // 16, k // 128, 16), dtype=torch.int32))
 
 
-def _linear_impl(x, rot_ij, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16, materialize_fp16,
+def _linear_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16, materialize_fp16,
                  out_dtype):
     dev = x.device
     n, k = _check_weights(wpack, wmeta, dev)
     _require(x.size(-1) == k, f"x has {x.size(-1)} features, the weights expect {k}")
-    _check_rot_params(x, rot_ij, rot_cs, scales, krot)
+    _check_rot_params(x, rot_idx, rot_cs, scales, krot)
     _require(out_dtype in _DT, f"out_dtype must be float32/float16/bfloat16, got {out_dtype}")
     xc = x.contiguous()
     m = xc.numel() // k
@@ -409,10 +411,10 @@ def _linear_impl(x, rot_ij, rot_cs, scales, krot, wpack, wmeta, bias, workspace,
         else:
             scratch = torch.empty(need, dtype=torch.uint8, device=dev)
     flags = (_lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0) | (_lib.PQ_RQ_MATERIALIZE_FP16 if materialize_fp16 else 0)
-    ij, cs = rot_ij.contiguous(), rot_cs.contiguous()
+    idx, cs = rot_idx.contiguous(), rot_cs.contiguous()
     sc = scales.contiguous() if scales is not None else None
     with _DeviceGuard(dev):
-        st = lib.pq_w4a8_linear(xc.data_ptr(), _DT[x.dtype], ij.data_ptr(), cs.data_ptr(),
+        st = lib.pq_w4a8_linear(xc.data_ptr(), _DT[x.dtype], idx.data_ptr(), cs.data_ptr(),
                                 sc.data_ptr() if sc is not None else None, wpack.data_ptr(), wmeta.data_ptr(),
                                 bias.data_ptr() if bias is not None else None,
                                 _DT[bias.dtype] if bias is not None else 0, y.data_ptr(), _DT[out_dtype], m, n, k,
@@ -427,6 +429,6 @@ _pq_lib.impl("w4a8_linear", _linear_impl, "CUDA")
 
 
 @torch.library.register_fake("paroquant::w4a8_linear")
-def _linear_fake(x, rot_ij, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16, materialize_fp16,
+def _linear_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16, materialize_fp16,
                  out_dtype):
     return x.new_empty((*x.shape[:-1], wpack.size(0) * 16), dtype=out_dtype)

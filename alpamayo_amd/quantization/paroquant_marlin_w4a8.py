@@ -238,7 +238,7 @@ class MarlinW4A8Linear(nn.Module):
         if not rotation.prepared:
             rotation.prepare()
         return torch.ops.paroquant.w4a8_linear(
-            x, rotation.rot_ij, rotation.rot_cs, rotation.scales_f32, rotation.krot, self.qweight, self.scales,
+            x, rotation.rot_idx, rotation.rot_cs, rotation.scales_f32, rotation.krot, self.qweight, self.scales,
             self.bias, self.workspace, input_fp16, materialize_fp16, out_dtype)
 
     def extra_repr(self) -> str:

@@ -8,10 +8,10 @@ theta, channel_scales, 128)``.
 
 On top of that, ``Rotation.prepare()`` derives the operands of the fused
 rotate+quant kernels (non-persistent, so state-dict keys are unchanged):
-  rot_ij     int16 [K/128, 64, 8]     packed pair indices (one pair per lane
-                                      and layer, assigned for conflict-free LDS
-                                      access; validated as one perfect matching
-                                      per group and layer)
+  rot_idx    int32 [K/128, 64, 4]     per lane: the channels it starts and
+                                      ends with and, per layer, the lane it
+                                      fetches its next channel from (validated
+                                      as one perfect matching per group and layer)
   rot_cs     float32 [K/128, 64, 8, 2] cos/sin of each pair's angle, evaluated
                                       in float64 on the host and rounded once
   scales_f32 float32 [K]              channel scales
@@ -66,7 +66,7 @@ class Rotation(nn.Module):
         self.register_buffer("theta", rotation_angles.clone().contiguous())
         self.register_buffer("pairs", rotation_pairs.clone().short().contiguous())
         self.register_buffer("channel_scales", channel_scales.clone().contiguous())
-        self.register_buffer("rot_ij", torch.empty(0, dtype=torch.int16), persistent=False)
+        self.register_buffer("rot_idx", torch.empty(0, dtype=torch.int32), persistent=False)
         self.register_buffer("rot_cs", torch.empty(0, dtype=torch.float32), persistent=False)
         self.register_buffer("scales_f32", torch.empty(0, dtype=torch.float32), persistent=False)
         self.group_size = group_size
@@ -81,8 +81,8 @@ class Rotation(nn.Module):
 
         dev = self.theta.device
         check_rotation_pairs(self.pairs, self.group_size)
-        rot_ij, rot_cs = pack_rotation(self.pairs, self.cos_sin_table())
-        self.rot_ij = rot_ij.to(dev)
+        rot_idx, rot_cs = pack_rotation(self.pairs, self.cos_sin_table())
+        self.rot_idx = rot_idx.to(dev)
         self.rot_cs = rot_cs.to(dev)
         self.scales_f32 = self.channel_scales.detach().reshape(-1).to(dev, torch.float32).contiguous()
 

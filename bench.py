@@ -145,7 +145,7 @@ def main() -> int:
         row = []
         for m, x in zip(L, X):
             r = m.rotate_linear.rotation
-            row.append(torch.ops.paroquant.rotate_quant_i8(x, r.rot_ij, r.rot_cs, r.scales_f32, r.krot, True, True))
+            row.append(torch.ops.paroquant.rotate_quant_i8(x, r.rot_idx, r.rot_cs, r.scales_f32, r.krot, True, True))
         xq_all.append(row)
     gemm_launches = [(m.rotate_linear.qlinear, xq, xs) for L, row in zip(pool, xq_all) for m, (xq, xs) in zip(L, row)]
     gg = torch.cuda.CUDAGraph()
@@ -184,7 +184,7 @@ def main() -> int:
         xq = []
         for m, x in zip(L, X):
             r = m.rotate_linear.rotation
-            xq.append(torch.ops.paroquant.rotate_quant_i8(x, r.rot_ij, r.rot_cs, r.scales_f32, r.krot, True, True))
+            xq.append(torch.ops.paroquant.rotate_quant_i8(x, r.rot_idx, r.rot_cs, r.scales_f32, r.krot, True, True))
         gg = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gg):
             for m, (q8, s8) in zip(L, xq):

@@ -71,28 +71,32 @@ int pq_rotate(const void* x, void* y, const int16_t* idx_ij, const void* theta,
               int dtype, void* stream);
 
 /* Packs rotation parameters (host memory, host code; no GPU involved) into
- * the operand layout of the fused kernels:
- *   rot_ij [G][64][KP] uint16  first | second << 8 (group-local indices)
- *   rot_cs [G][64][KP][2] float (cos, sin)
- * G = h/128, KP = krot rounded up to a multiple of 8.  Input: pairs int16
- * [krot][h] group-local (pair t of group g = pairs[r][g*128+2t], +1) and
- * cos_sin float [krot][h/2][2] (the pair's angle in theta's layout).  Each
- * lane owns one pair per layer; pairs are assigned to lanes (and possibly
- * swapped, with sin negated, which is the same rotation) so that every
- * layer's LDS accesses are bank-conflict free.  Fails with PQ_ERR_ARG unless
+ * the operand layout of the fused kernels, G = h/128, KP = 8 for krot <= 8,
+ * else 16:
+ *   rot_idx [G][64][KP/2] uint32  per lane: word 0 = Af | Bf << 8 | init << 16,
+ *                                 byte 4 + r = src | flag << 7 (layer r)
+ *   rot_cs  [G][64][KP][2] float  (cos, +-sin) of the lane's pair in layer r
+ * The kernels rotate a group with one wave in registers: lane l starts with
+ * channels l and l+64 in slots (a, b) (swapped if init), fetches before each
+ * layer slot a of lane `src` with one cross-lane read (into slot a if flag,
+ * else slot b, its old slot b going to the other slot), applies
+ * a' = fma(a, c, b*s), b' = fma(b, c, -(a*s)), and ends with channels Af, Bf
+ * in slots a, b.  Input: pairs int16 [krot][h] group-local (pair t of group
+ * g = pairs[r][g*128+2t], +1) and cos_sin float [krot][h/2][2] (the pair's
+ * angle in theta's layout).  krot in 1..16.  Fails with PQ_ERR_ARG unless
  * every layer pairs each channel of each 128-group exactly once.
  * Reference: the parameters of Rotation (rotation_linear.py:26-43). */
-int pq_rotation_pack(const int16_t* pairs, const float* cos_sin, int64_t h, int krot, uint16_t* rot_ij,
+int pq_rotation_pack(const int16_t* pairs, const float* cos_sin, int64_t h, int krot, uint32_t* rot_idx,
                      float* rot_cs);
 
 /* Fused rotation + channel scale + per-token absmax + int8 quantization.
- * x: [rows, h] of x_dtype; rot_ij / rot_cs: packed parameters
+ * x: [rows, h] of x_dtype; rot_idx / rot_cs: packed parameters
  * (pq_rotation_pack) of krot layers; scales: float32 [h] or NULL.
  * Outputs xq int8 [rows, h], xscale float32 [rows] (absmax/127), and, when
  * xrot is not NULL, the rotated activations as fp16 [rows, h].
  * flags: PQ_RQ_* bits.  krot in 1..16, h % 128 == 0, h <= 16384.
  * Reference: rotation.cu:15-60 + paroquant_marlin_w4a8.py:319-333. */
-int pq_rotate_quant_i8(const void* x, int x_dtype, const uint16_t* rot_ij, const float* rot_cs,
+int pq_rotate_quant_i8(const void* x, int x_dtype, const uint32_t* rot_idx, const float* rot_cs,
                        const float* scales, int8_t* xq, float* xscale, void* xrot,
                        int64_t rows, int64_t h, int krot, unsigned flags, void* stream);
 
@@ -134,10 +138,11 @@ int pq_w4a8_prepack(const int32_t* awq_qweight, const uint16_t* awq_scales,
                     const int32_t* awq_qzeros, uint8_t* wpack, uint32_t* wmeta, int64_t k,
                     int64_t n, int group_size, void* stream);
 
-/* Bytes of scratch pq_w4a8_linear needs (0 when it runs as one fused kernel:
- * m <= 4 with krot <= 8 and small enough k; otherwise the int8 activations
- * and their scales, m*k rounded up to 256 plus 4*m bytes).  The scratch is
- * written before it is read; its content does not matter. */
+/* Bytes of scratch pq_w4a8_linear needs between its two kernels: for decode
+ * sizes (m*k <= 12288) the rotated rows and per-group maxima, m*k*4 rounded
+ * up to 256 plus 4*m*(k/128) bytes; otherwise the int8 activations and their
+ * scales, m*k rounded up to 256 plus 4*m bytes.  The scratch is written
+ * before it is read; its content does not matter. */
 size_t pq_w4a8_linear_workspace_size(int64_t m, int64_t n, int64_t k, int krot);
 
 /* y = W4A8 GEMM of the per-token int8 quantization of the rotation of x:
@@ -145,7 +150,7 @@ size_t pq_w4a8_linear_workspace_size(int64_t m, int64_t n, int64_t k, int krot);
  * pq_rotate_quant_i8, weights as for pq_w4a8_gemm, flags PQ_RQ_*.
  * k <= 16384.  Same results as pq_rotate_quant_i8 followed by pq_w4a8_gemm.
  * Reference: paroquant_marlin_w4a8.py:59-65, 314-333; rotation_linear.py:120-124. */
-int pq_w4a8_linear(const void* x, int x_dtype, const uint16_t* rot_ij, const float* rot_cs, const float* scales,
+int pq_w4a8_linear(const void* x, int x_dtype, const uint32_t* rot_idx, const float* rot_cs, const float* scales,
                    const uint8_t* wpack, const uint32_t* wmeta, const void* bias, int bias_dtype, void* y,
                    int y_dtype, int64_t m, int64_t n, int64_t k, int krot, unsigned flags, void* workspace,
                    size_t workspace_bytes, void* stream);

@@ -132,32 +132,51 @@ def rotate_path_f32(x_bf16_as_f32: np.ndarray, pairs: np.ndarray, cos: np.ndarra
     return y
 
 
-def unpack_packed_params(rot_ij: np.ndarray, rot_cs: np.ndarray, krot: int):
-    """Packed kernel operands -> per (group, lane, layer) (first, second, cos, sin).
+def unpack_packed_params(rot_idx: np.ndarray, rot_cs: np.ndarray, krot: int):
+    """Packed kernel operands -> (init, Af, Bf, src, flag, cos, sin).
 
-    rot_ij [G, 64, KP] uint16 (first | second << 8); rot_cs [G, 64, KP, 2].
+    rot_idx [G, 64, KP/2] uint32: word 0 = Af | Bf << 8 | init << 16 (channels
+    in slots A/B after the last layer; slot A starts with channel lane+64 when
+    init is set, else with channel lane); byte 4 + r = src | flag << 7 for the
+    fetch before layer r.  rot_cs [G, 64, KP, 2] float32.
+    src / flag / cos / sin are [G, 64, krot].
     """
-    ij = np.asarray(rot_ij).view(np.uint16).astype(np.int64)[:, :, :krot]
-    first = ij & 0xFF
-    second = (ij >> 8) & 0xFF
+    w = np.ascontiguousarray(rot_idx).view(np.uint32)
+    b = w.view(np.uint8).reshape(w.shape[0], w.shape[1], -1).astype(np.int64)
+    w0 = w[:, :, 0].astype(np.int64)
+    Af, Bf = w0 & 0xFF, (w0 >> 8) & 0xFF
+    init = ((w0 >> 16) & 1) != 0
+    src = b[:, :, 4:4 + krot] & 0x3F
+    flag = (b[:, :, 4:4 + krot] >> 7) != 0
     cs = np.asarray(rot_cs, np.float32)[:, :, :krot]
-    return first, second, cs[..., 0], cs[..., 1]
+    return init, Af, Bf, src, flag, cs[..., 0], cs[..., 1]
 
 
-def rotate_f32_packed(xs: np.ndarray, rot_ij: np.ndarray, rot_cs: np.ndarray, krot: int) -> np.ndarray:
-    """The kernels' use of the packed operands: layer r, lane t of group g updates
-    (first, second) with xf' = fma(xf, c, xs*s), xs' = fma(xs, c, -(xf*s))."""
-    y = np.array(xs, dtype=np.float32, copy=True)
-    first, second, c, s = unpack_packed_params(rot_ij, rot_cs, krot)
-    G = first.shape[0]
-    base = (np.arange(G, dtype=np.int64) * 128)[:, None]
+def rotate_f32_packed(xs: np.ndarray, rot_idx: np.ndarray, rot_cs: np.ndarray, krot: int) -> np.ndarray:
+    """The kernels' use of the packed operands, lane by lane: lane l loads
+    channels l and l+64 into slots (a, b) (swapped when init is set); before
+    layer r it fetches slot a of lane src and puts it into slot a (flag) or b,
+    keeping its old slot b in the other; every layer is a' = fma(a, c, b*s),
+    b' = fma(b, c, -(a*s)); at the end slot a holds channel Af and b channel Bf."""
+    x = np.asarray(xs, dtype=np.float32)
+    init, Af, Bf, src, flag, c, s = unpack_packed_params(rot_idx, rot_cs, krot)
+    G = init.shape[0]
+    rows = x.shape[0]
+    xg = x.reshape(rows, G, 128)
+    gi = np.arange(G)[:, None]
+    lo, hi = xg[:, :, :64], xg[:, :, 64:]
+    a = np.where(init[None], hi, lo)          # [rows, G, 64]
+    b = np.where(init[None], lo, hi)
     for r in range(krot):
-        gi = (first[:, :, r] + base).reshape(-1)
-        gj = (second[:, :, r] + base).reshape(-1)
-        cr = c[:, :, r].reshape(-1)
-        sr = s[:, :, r].reshape(-1)
-        xi = y[:, gi]
-        xj = y[:, gj]
-        y[:, gi] = _fma32(xi, cr, (xj * sr).astype(np.float32))
-        y[:, gj] = _fma32(xj, cr, -(xi * sr).astype(np.float32))
-    return y
+        recv = a[:, gi, src[:, :, r]]
+        fl = flag[:, :, r][None]
+        a, b = np.where(fl, recv, b), np.where(fl, b, recv)
+        cr = c[:, :, r][None]
+        sr = s[:, :, r][None]
+        na = _fma32(a, cr, (b * sr).astype(np.float32))
+        nb = _fma32(b, cr, -(a * sr).astype(np.float32))
+        a, b = na, nb
+    y = np.empty_like(xg)
+    y[:, gi, Af] = a
+    y[:, gi, Bf] = b
+    return y.reshape(rows, G * 128)

@@ -42,11 +42,11 @@ def assert_bf16_close(got: np.ndarray, ref64: np.ndarray, tol_fro=1e-2):
 
 
 def packed_rotation(pairs: torch.Tensor, theta: torch.Tensor):
-    """(rot_ij, rot_cs, cos, sin) for Rotation-style pairs [krot, K] and angles [krot, K/2]."""
+    """(rot_idx, rot_cs, cos, sin) for Rotation-style pairs [krot, K] and angles [krot, K/2]."""
     from alpamayo_amd.ops import pack_rotation
     from oracle import rotation as orot
 
     c, s = orot.cos_sin_table(theta.numpy())
     cs = torch.from_numpy(np.stack([c, s], axis=-1)).contiguous()
-    rot_ij, rot_cs = pack_rotation(pairs.to(torch.int16), cs)
-    return rot_ij, rot_cs, c, s
+    rot_idx, rot_cs = pack_rotation(pairs.to(torch.int16), cs)
+    return rot_idx, rot_cs, c, s

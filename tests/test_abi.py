@@ -90,13 +90,16 @@ def test_workspace_size_rules():
     for m in (1, 4, 16, 3072):
         for n, k in ((1024, 4096), (4096, 4096), (12288, 4096), (4096, 12288)):
             assert lib.pq_w4a8_workspace_size(m, n, k, 128) == 0        # no inter-workgroup exchange
-    # the one-kernel decode path needs no scratch; the two-kernel path holds xq and xscale
-    assert lib.pq_w4a8_linear_workspace_size(1, 4096, 4096, 8) == 0
-    assert lib.pq_w4a8_linear_workspace_size(4, 4096, 4096, 8) == 0
-    assert lib.pq_w4a8_linear_workspace_size(1, 4096, 12288, 8) == 0
-    assert lib.pq_w4a8_linear_workspace_size(1, 4096, 4096, 16) == 4096 + 4     # krot 16: two kernels
-    assert lib.pq_w4a8_linear_workspace_size(4, 4096, 12288, 8) == 4 * 12288 + 16
-    assert lib.pq_w4a8_linear_workspace_size(5, 4096, 4096, 8) == 5 * 4096 + 20
+    # decode (m * k <= 12288): rotated rows (fp32 bound) + per-group absmax
+    def split(m, k):
+        return (m * k * 4 + 255) // 256 * 256 + m * (k // 128) * 4
+    assert lib.pq_w4a8_linear_workspace_size(1, 4096, 4096, 8) == split(1, 4096)
+    assert lib.pq_w4a8_linear_workspace_size(1, 4096, 12288, 16) == split(1, 12288)
+    assert lib.pq_w4a8_linear_workspace_size(3, 4096, 4096, 8) == split(3, 4096)
+    # otherwise the row path holds xq and xscale
+    assert lib.pq_w4a8_linear_workspace_size(4, 4096, 4096, 8) == 4 * 4096 + 16
+    assert lib.pq_w4a8_linear_workspace_size(2, 4096, 12288, 8) == 2 * 12288 + 8
+    assert lib.pq_w4a8_linear_workspace_size(17, 4096, 4096, 8) == 17 * 4096 + 68
     assert lib.pq_w4a8_linear_workspace_size(3, 64, 100, 8) == 0       # invalid shape -> 0
 
 

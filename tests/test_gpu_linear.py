@@ -99,7 +99,7 @@ def test_unfused_reference_chain_matches_fused():
     fused = wrapper(x)
     xr = rl.rotation(x.half())                         # the reference's fp16 rotation op
     xq_u, xs_u = torch.ops.paroquant.quant_i8(xr)
-    xq_f, xs_f = torch.ops.paroquant.rotate_quant_i8(x, rl.rotation.rot_ij, rl.rotation.rot_cs,
+    xq_f, xs_f = torch.ops.paroquant.rotate_quant_i8(x, rl.rotation.rot_idx, rl.rotation.rot_cs,
                                                      rl.rotation.scales_f32, rl.rotation.krot, True, True)
     assert_codes_close(to_np(xq_u), to_np(xq_f))
     unfused = MarlinW4A8Linear.forward(rl.qlinear, xr).to(torch.bfloat16)
@@ -186,19 +186,20 @@ def test_config3_chain_two_layers_m16():
 @pytest.mark.parametrize("N,K", [(16, 128), (48, 2048), (32, 8192), (1024, 12288), (12288, 4096)])
 @pytest.mark.parametrize("krot,flags", [(8, (True, True)), (1, (False, True)), (8, (True, False)), (16, (True, True))])
 def test_linear_op_decode_paths(M, N, K, krot, flags):
-    """paroquant::w4a8_linear (one fused kernel for M <= 4, krot <= 8; two kernels otherwise)."""
+    """paroquant::w4a8_linear on both of its paths: split rotation + prologue-quantizing GEMM
+    (M * K <= 12288) and row rotate+quant + GEMM (otherwise)."""
     print(f"linear op M={M} N={N} K={K} krot={krot} flags={flags}", flush=True)
     g = workloads.generator(zlib.crc32(f"{M}{N}{K}{krot}{flags}".encode()))
     spec = workloads.linear_spec("x", N, K, g, keep_codes=True)
     pairs = torch.cat([spec.pairs] * 2)[:krot]
     theta = torch.cat([spec.theta] * 2)[:krot]
-    rot_ij, rot_cs, c, s = packed_rotation(pairs, theta)
+    rot_idx, rot_cs, c, s = packed_rotation(pairs, theta)
     scales = spec.channel_scales.float().reshape(-1)
     wp, wm = torch.ops.paroquant.w4a8_prepack(spec.w.awq_qweight.cuda(), spec.w.awq_scales.cuda(),
                                               spec.w.awq_qzeros.cuda())
     bias = torch.randn(N, generator=g).to(torch.bfloat16)
     x = workloads.activations(M, K, g)
-    y = torch.ops.paroquant.w4a8_linear(x.cuda(), rot_ij.cuda(), rot_cs.cuda(), scales.cuda(), krot, wp, wm,
+    y = torch.ops.paroquant.w4a8_linear(x.cuda(), rot_idx.cuda(), rot_cs.cuda(), scales.cuda(), krot, wp, wm,
                                         bias.cuda(), None, flags[0], flags[1], torch.bfloat16)
     v = orot.rotate_path_f32(to_np(x), pairs.numpy(), c, s, scales.numpy(), 128, flags[0], flags[1])
     q, sx = oquant.quant_int8_per_token(v)
@@ -215,15 +216,14 @@ def test_linear_op_input_dtypes(M, dtype):
     print(f"linear op dtype={dtype} M={M}", flush=True)
     g = workloads.generator(zlib.crc32(f"dt{M}{dtype}".encode()))
     spec = workloads.linear_spec("x", N, K, g, keep_codes=True)
-    rot_ij, rot_cs, c, s = packed_rotation(spec.pairs, spec.theta)
+    rot_idx, rot_cs, c, s = packed_rotation(spec.pairs, spec.theta)
     scales = spec.channel_scales.float().reshape(-1)
     wp, wm = torch.ops.paroquant.w4a8_prepack(spec.w.awq_qweight.cuda(), spec.w.awq_scales.cuda(),
                                               spec.w.awq_qzeros.cuda())
     x = workloads.activations(M, K, g).to(dtype)
     need = alpamayo_amd.ops.linear_workspace_bytes(M, N, K, 8)
-    assert (need == 0) == (M <= 4)
     ws = torch.empty(need, dtype=torch.uint8, device="cuda") if need else None
-    y = torch.ops.paroquant.w4a8_linear(x.cuda(), rot_ij.cuda(), rot_cs.cuda(), scales.cuda(), 8, wp, wm, None,
+    y = torch.ops.paroquant.w4a8_linear(x.cuda(), rot_idx.cuda(), rot_cs.cuda(), scales.cuda(), 8, wp, wm, None,
                                         ws, False, True, dtype)
     assert y.dtype == dtype
     v = orot.rotate_path_f32(to_np(x), spec.pairs.numpy(), c, s, scales.numpy(), 128, False, True)

@@ -25,7 +25,7 @@ pytestmark = pytest.mark.gpu
 class _Rot:
     def __init__(self, K, seed):
         self.pairs, self.theta, self.cs = workloads.rotation_params(K, workloads.generator(seed))
-        self.rot_ij, self.rot_cs, self.c, self.s = packed_rotation(self.pairs, self.theta)
+        self.rot_idx, self.rot_cs, self.c, self.s = packed_rotation(self.pairs, self.theta)
         self.krot = self.pairs.shape[0]
 
 
@@ -35,7 +35,7 @@ def _prepared(K, seed):
 
 def _run(x, rot, scales_f32, input_fp16=True, materialize=True):
     xq, xs, xr = torch.ops.paroquant.rotate_quant_i8_rot(
-        x.cuda(), rot.rot_ij.cuda(), rot.rot_cs.cuda(),
+        x.cuda(), rot.rot_idx.cuda(), rot.rot_cs.cuda(),
         scales_f32.cuda() if scales_f32 is not None else None, rot.krot, input_fp16, materialize)
     torch.cuda.synchronize()
     return to_np(xq), to_np(xs), to_np(xr)
@@ -109,12 +109,12 @@ def test_full_prefill_shape_row_subset():
 
 def test_bad_params_rejected():
     x = torch.zeros(2, 256, dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(RuntimeError, match="rot_ij"):
-        torch.ops.paroquant.rotate_quant_i8(x, torch.zeros(1, 64, 8, dtype=torch.int16, device="cuda"),
+    with pytest.raises(RuntimeError, match="rot_idx"):
+        torch.ops.paroquant.rotate_quant_i8(x, torch.zeros(1, 64, 4, dtype=torch.int32, device="cuda"),
                                             torch.zeros(2, 64, 8, 2, device="cuda"), None, 8, True, True)
     with pytest.raises(RuntimeError, match="multiple of 128"):
         torch.ops.paroquant.rotate_quant_i8(torch.zeros(2, 200, dtype=torch.bfloat16, device="cuda"),
-                                            torch.zeros(1, 64, 8, dtype=torch.int16, device="cuda"),
+                                            torch.zeros(1, 64, 4, dtype=torch.int32, device="cuda"),
                                             torch.zeros(1, 64, 8, 2, device="cuda"), None, 8, True, True)
 
 
@@ -124,9 +124,9 @@ def test_krot_variants(krot):
     K, M = 512, 37
     g = workloads.generator(40 + krot)
     pairs, theta, cs = workloads.rotation_params(K, g, krot=krot)
-    rot_ij, rot_cs, c, s = packed_rotation(pairs, theta)
+    rot_idx, rot_cs, c, s = packed_rotation(pairs, theta)
     x = workloads.activations(M, K, g)
-    xq, xs = torch.ops.paroquant.rotate_quant_i8(x.cuda(), rot_ij.cuda(), rot_cs.cuda(), cs.float().reshape(-1).cuda(),
+    xq, xs = torch.ops.paroquant.rotate_quant_i8(x.cuda(), rot_idx.cuda(), rot_cs.cuda(), cs.float().reshape(-1).cuda(),
                                                  krot, True, True)
     _, qref, sref = olin.rotate_quant(to_np(x), pairs.numpy(), c, s, cs.float().reshape(-1).numpy())
     assert_codes_close(to_np(xq), qref)

@@ -36,14 +36,14 @@ def test_meta_kernels_propagate_shapes():
     y = torch.ops.rotation.rotate(x, torch.empty(8, 256, device=m, dtype=torch.int16),
                                   torch.empty(8, 128, device=m, dtype=torch.float16), None, 128)
     assert y.shape == x.shape and y.dtype == x.dtype
-    xq, xs = torch.ops.paroquant.rotate_quant_i8(x, torch.empty(2, 64, 8, device=m, dtype=torch.int16),
+    xq, xs = torch.ops.paroquant.rotate_quant_i8(x, torch.empty(2, 64, 4, device=m, dtype=torch.int32),
                                                  torch.empty(2, 64, 8, 2, device=m), None, 8, True, True)
     assert xq.shape == (6, 256) and xq.dtype == torch.int8 and xs.shape == (6,)
     wp = torch.empty(64, 2, 64, 16, device=m, dtype=torch.uint8)
     wm = torch.empty(64, 2, 16, device=m, dtype=torch.int32)
     out = torch.ops.paroquant.w4a8_gemm(xq, xs, wp, wm, None, None, torch.bfloat16)
     assert out.shape == (6, 1024) and out.dtype == torch.bfloat16
-    lin = torch.ops.paroquant.w4a8_linear(x, torch.empty(2, 64, 8, device=m, dtype=torch.int16),
+    lin = torch.ops.paroquant.w4a8_linear(x, torch.empty(2, 64, 4, device=m, dtype=torch.int32),
                                           torch.empty(2, 64, 8, 2, device=m), None, 8, wp, wm, None, None, True, True,
                                           torch.bfloat16)
     assert lin.shape == (2, 3, 1024)
@@ -117,14 +117,14 @@ def test_rotation_prepare_builds_fused_operands():
     pairs, theta, cs = workloads.rotation_params(256, g)
     rot = Rotation(256, rotation_angles=theta, rotation_pairs=pairs, channel_scales=cs)
     rot.prepare()
-    assert rot.rot_ij.shape == (2, 64, 8) and rot.rot_cs.shape == (2, 64, 8, 2) and rot.krot == 8
+    assert rot.rot_idx.shape == (2, 64, 4) and rot.rot_cs.shape == (2, 64, 8, 2) and rot.krot == 8
     c, s = np.cos(theta.float().double().numpy()), np.sin(theta.float().double().numpy())
     tab = rot.cos_sin_table().numpy()
     np.testing.assert_array_equal(tab[..., 0], c.astype(np.float32))
     np.testing.assert_array_equal(tab[..., 1], s.astype(np.float32))
     np.testing.assert_array_equal(np.sort(np.abs(rot.rot_cs[..., 1].numpy()).ravel()),
                                   np.sort(np.abs(s.astype(np.float32)).ravel()))
-    assert "rot_ij" not in rot.state_dict() and "rot_cs" not in rot.state_dict()
+    assert "rot_idx" not in rot.state_dict() and "rot_cs" not in rot.state_dict()
     bad = pairs.clone()
     bad[0, 1] = bad[0, 0]
     with pytest.raises(ValueError):
