@@ -26,10 +26,9 @@
 //                v_mfma_i32_16x16x64_i8 per block (activation rows padded to
 //                16); the waves of a workgroup split K and add their partial
 //                sums in LDS in a fixed order.
-//   gemm_tiled   M > 16: 128x128 output tiles, A (int8) and B (int4) staged
-//                through LDS one group at a time with the next group
-//                prefetched into registers, 2x2 waves of 64x64, each
-//                2x2 v_mfma_i32_32x32x32_i8 tiles per 32-deep K step.
+//   gemm_prefill M > 16: 192x128 (or 128x64) output tiles, 2x2 waves, operands
+//                staged through a 3-stage LDS ring fed by two register
+//                stages, v_mfma_i32_32x32x32_i8 tiles.
 #include "pq_device.h"
 #include "pq_internal.h"
 
@@ -272,156 +271,233 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
 
 // ---------------------------------------------------------------------------
 // Prefill-size GEMM (M > 16)
+//
+// Workgroup tile BM x BN; WM x WN waves, each a (BM/WM) x (BN/WN) block of
+// TM x TN 32 x 32 tiles (v_mfma_i32_32x32x32_i8).  The operands of one K
+// group -- A as BM rows of 128 int8, B as BN/16 packed 1 KB blocks, and BN
+// metadata words -- go straight from global memory to LDS (global_load_lds,
+// no register staging) into a 3-stage ring, so the loads of group g+2 are in
+// flight while group g is computed.  Every wave issues the same number of
+// loads per stage, so "stage g has landed" is one vmcnt wait plus a barrier.
+// A rows keep their 16-byte chunks XOR-swizzled by row and B blocks sit at a
+// 1152-byte stride, which keeps the fragment reads free of bank conflicts.
+// B is unpacked to signed int8 (q - z) in registers at use.  After each
+// group the int32 tiles are scaled by the group's fp16 scales into fp32
+// accumulators.
 // ---------------------------------------------------------------------------
-constexpr int kBM = 128;
-constexpr int kBN = 128;
-constexpr int kAPad = 144;  // LDS row stride of the A tile (bytes)
+constexpr int kPfStages = 3;
+constexpr int kPfBStride = 1024 + 128;
 
-template <bool PARTIALS>
-__global__ __launch_bounds__(256) void gemm_tiled(const int8_t* __restrict__ xq, const float* __restrict__ xs,
-                                                  const uint8_t* __restrict__ wpack,
-                                                  const uint32_t* __restrict__ wmeta, const void* __restrict__ bias,
-                                                  int bias_dtype, void* __restrict__ y, int y_dtype,
-                                                  int32_t* __restrict__ partials, int M, int N, int K) {
-  __shared__ __attribute__((aligned(16))) int8_t As[kBM * kAPad];
-  __shared__ __attribute__((aligned(16))) uint8_t Bs[8 * 1024];
-  __shared__ uint32_t Ms[8 * 16];
+__device__ __forceinline__ int pf_swz(int line) { return (line >> 1) & 7; }
+
+// Global -> LDS copies of 16 (4) bytes per lane: lane l's bytes land at LDS
+// address lds + 16*l (4*l).  Written as inline asm on purpose: the compiler
+// would otherwise treat every later LDS read as possibly aliasing the copy
+// and wait for all outstanding loads (vmcnt(0)) before it, which serializes
+// the stage ring.  The kernels wait for these loads explicitly (wait_vmcnt).
+// M0 is used only here.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
+}
+__device__ __forceinline__ void lds_copy16(const void* gsrc, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(gsrc) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_copy4(const void* gsrc, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(gsrc) : "memory", "m0");
+}
+
+// s_waitcnt with vmcnt(n), any lgkmcnt/expcnt (gfx9 immediate encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int BM, int BN, int WM, int WN, bool PARTIALS>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
+    const int8_t* __restrict__ xq, const float* __restrict__ xs, const uint8_t* __restrict__ wpack,
+    const uint32_t* __restrict__ wmeta, const void* __restrict__ bias, int bias_dtype, void* __restrict__ y,
+    int y_dtype, int32_t* __restrict__ partials, int M, int N, int K) {
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  constexpr int A_BYTES = BM * 128;                 // BM/8 blocks of 1 KB (8 rows each)
+  constexpr int B_BYTES = (BN / 16) * kPfBStride;   // BN/16 packed blocks
+  constexpr int STAGE = A_BYTES + B_BYTES + BN * 4;
+  constexpr int A_LD = BM / 8 / NW, B_LD = BN / 16 / NW, M_LD = 1;   // loads per wave per stage
+  constexpr int LOADS = A_LD + B_LD + M_LD;
+  static_assert(TM >= 1 && TN >= 1 && BM % (32 * WM) == 0 && BN % (32 * WN) == 0, "tile shape");
+  static_assert((BM / 8) % NW == 0 && (BN / 16) % NW == 0 && BN / NW <= 64, "loads split evenly over the waves");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const int G = K >> 7;
   const int ntiles16 = N >> 4;
-  const int nbn = (N + kBN - 1) / kBN;
+  const int nbn = (N + BN - 1) / BN;
   const int bm = blockIdx.x / nbn;
   const int bn = blockIdx.x % nbn;
-  const int t = threadIdx.x;
-  const int wave = t >> 6;
-  const int lane = t & 63;
-  const int wm = wave >> 1;
-  const int wn = wave & 1;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN;
+  const int wn = wave % WN;
   const int r32 = lane & 31;
   const int hj = lane >> 5;
 
-  // Global -> register mapping of one group's tiles.
-  const int a_row = t >> 1;
-  const int a_half = t & 1;
-  const int64_t a_grow = static_cast<int64_t>(bm) * kBM + a_row;
-  const bool a_ok = a_grow < M;
-  const int8_t* a_src = xq + (a_ok ? a_grow : 0) * K + a_half * 64;
-  const int b_tile = t >> 5;
-  const int b_off = (t & 31) * 32;
-  const int b_gtile = bn * 8 + b_tile;
-  const bool b_ok = b_gtile < ntiles16;
-  const uint8_t* b_src = wpack + static_cast<int64_t>(b_ok ? b_gtile : 0) * G * 1024 + b_off;
-  const int m_gtile = bn * 8 + (t >> 4);
-  const bool m_ok = t < 128 && m_gtile < ntiles16;
-  const uint32_t* m_src = wmeta + static_cast<int64_t>(m_ok ? m_gtile : 0) * G * 16 + (t & 15);
+  // Sources of this wave's loads (32-bit element offsets; rows past M and
+  // blocks past N are clamped, their results are never stored; the host
+  // keeps M*K and N*K/2 below 2^31).
+  int a_off[A_LD], b_off[B_LD];
+#pragma unroll
+  for (int i = 0; i < A_LD; ++i) {
+    const int blk = wave * A_LD + i;          // rows 8*blk .. 8*blk+7
+    const int row = blk * 8 + (lane >> 3);
+    const int q = (lane & 7) ^ pf_swz(row);   // LDS chunk lane&7 of the row holds global chunk q
+    a_off[i] = min(bm * BM + row, M - 1) * K + q * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < B_LD; ++i) {
+    const int blk = wave * B_LD + i;
+    b_off[i] = min(bn * (BN / 16) + blk, ntiles16 - 1) * G * 1024 + lane * 16;
+  }
+  constexpr int MCOLS = BN / NW;   // metadata words per wave
+  const int mcol = wave * MCOLS + (lane < MCOLS ? lane : 0);
+  const int m_off = min(bn * (BN / 16) + (mcol >> 4), ntiles16 - 1) * G * 16 + (mcol & 15);
 
-  v4i ra[4];
-  v4i rb[2];
-  uint32_t rm = 0;
-  auto gload = [&](int g) {
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+  auto issue = [&](int g, int stage) {
+    const uint32_t base = lds0 + stage * STAGE;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      ra[q] = a_ok ? *reinterpret_cast<const v4i*>(a_src + static_cast<int64_t>(g) * 128 + q * 16) : v4i{0, 0, 0, 0};
+    for (int i = 0; i < A_LD; ++i) lds_copy16(xq + a_off[i] + g * 128, base + (wave * A_LD + i) * 1024);
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
-      rb[q] = b_ok ? *reinterpret_cast<const v4i*>(b_src + static_cast<int64_t>(g) * 1024 + q * 16) : v4i{0, 0, 0, 0};
-    rm = m_ok ? m_src[static_cast<int64_t>(g) * 16] : 0u;
+    for (int i = 0; i < B_LD; ++i)
+      lds_copy16(wpack + b_off[i] + g * 1024, base + A_BYTES + (wave * B_LD + i) * kPfBStride);
+    if (lane < MCOLS) lds_copy4(wmeta + m_off + g * 16, base + A_BYTES + B_BYTES + wave * MCOLS * 4);
   };
 
-  float acc[2][2][16];
+  float acc[TM][TN][16];
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
+  for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni)
+    for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.0f;
+      for (int v = 0; v < 16; ++v) acc[tm][tn][v] = 0.0f;
 
-  int bt[2], bc[2];
+  int arow[TM], bcol[TN];
 #pragma unroll
-  for (int ni = 0; ni < 2; ++ni) {
-    const int nl = wn * 64 + ni * 32 + r32;
-    bt[ni] = nl >> 4;
-    bc[ni] = nl & 15;
-  }
+  for (int tm = 0; tm < TM; ++tm) arow[tm] = wm * (BM / WM) + tm * 32 + r32;
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) bcol[tn] = wn * (BN / WN) + tn * 32 + r32;
 
-  gload(0);
-  for (int g = 0; g < G; ++g) {
-    __syncthreads();
+  auto compute = [&](int stage, int g) {
+    const uint8_t* As = smem + stage * STAGE;
+    const uint8_t* Bs = As + A_BYTES;
+    const uint32_t* Ms = reinterpret_cast<const uint32_t*>(Bs + B_BYTES);
+    uint32_t zb[TN];
+    float sc[TN];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) *reinterpret_cast<v4i*>(As + a_row * kAPad + a_half * 64 + q * 16) = ra[q];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) *reinterpret_cast<v4i*>(Bs + b_tile * 1024 + b_off + q * 16) = rb[q];
-    if (t < 128) Ms[t] = rm;
-    __syncthreads();
-    if (g + 1 < G) gload(g + 1);
-
-    uint32_t zb[2];
-    float sc[2];
-#pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
-      const uint32_t meta = Ms[bt[ni] * 16 + bc[ni]];
-      zb[ni] = zero_bias((meta >> 16) & 0xfu);
-      sc[ni] = pq_f16_to_f32(static_cast<uint16_t>(meta & 0xffffu));
+    for (int tn = 0; tn < TN; ++tn) {
+      const uint32_t meta = Ms[bcol[tn]];
+      zb[tn] = meta_zero_bias(meta);
+      sc[tn] = meta_scale(meta);
     }
-    v16i T[2][2];
+    v16i T[TM][TN];
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
+    for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-      for (int ni = 0; ni < 2; ++ni) T[mi][ni] = v16i{};
+      for (int tn = 0; tn < TN; ++tn) T[tm][tn] = v16i{};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      v4i a[2], b[2];
+      const int q = hj * 4 + i;   // this lane's 16 k of the step: 16q .. 16q+15
+      v4i a[TM], b[TN];
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
-        a[mi] = *reinterpret_cast<const v4i*>(As + (wm * 64 + mi * 32 + r32) * kAPad + hj * 64 + i * 16);
+      for (int tm = 0; tm < TM; ++tm)
+        a[tm] = *reinterpret_cast<const v4i*>(As + arow[tm] * 128 + ((q ^ pf_swz(arow[tm])) << 4));
 #pragma unroll
-      for (int ni = 0; ni < 2; ++ni) {
-        const uint2 w =
-            *reinterpret_cast<const uint2*>(Bs + bt[ni] * 1024 + ((2 * hj + (i >> 1)) * 16 + bc[ni]) * 16 + (i & 1) * 8);
-        b[ni] = unpack16(w.x, w.y, zb[ni]);
+      for (int tn = 0; tn < TN; ++tn) {
+        // packed slot (2*hj + i/2)*16 + col%16 of the column's block, bytes (i%2)*8 .. +8
+        const uint2 w = *reinterpret_cast<const uint2*>(Bs + (bcol[tn] >> 4) * kPfBStride +
+                                                        ((2 * hj + (i >> 1)) * 16 + (bcol[tn] & 15)) * 16 + (i & 1) * 8);
+        b[tn] = unpack16(w.x, w.y, zb[tn]);
       }
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
+      for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
-          T[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[mi], b[ni], T[mi][ni], 0, 0, 0);
+        for (int tn = 0; tn < TN; ++tn)
+          T[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[tm], b[tn], T[tm][tn], 0, 0, 0);
     }
     if constexpr (PARTIALS) {
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
+      for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
+        for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
-            const int64_t m = static_cast<int64_t>(bm) * kBM + wm * 64 + mi * 32 + 8 * (v >> 2) + 4 * hj + (v & 3);
-            const int n = bn * kBN + wn * 64 + ni * 32 + r32;
-            if (m < M && n < N) partials[(m * G + g) * N + n] = T[mi][ni][v];
+            const int64_t m = static_cast<int64_t>(bm) * BM + arow[tm] - r32 + 8 * (v >> 2) + 4 * hj + (v & 3);
+            const int n = bn * BN + bcol[tn];
+            if (m < M && n < N) partials[(m * G + g) * N + n] = T[tm][tn][v];
           }
     } else {
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
+      for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
+        for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
           for (int v = 0; v < 16; ++v)
-            acc[mi][ni][v] = fmaf(static_cast<float>(T[mi][ni][v]), sc[ni], acc[mi][ni][v]);
+            acc[tm][tn][v] = fmaf(static_cast<float>(T[tm][tn][v]), sc[tn], acc[tm][tn][v]);
     }
+  };
+
+  // Stage g % 3 holds group g.  Before computing g, each wave waits for its
+  // own loads of g (those of g+1 may stay in flight), then a barrier makes
+  // everybody's loads of g visible and retires everybody's use of the stage
+  // that group g+2 is about to overwrite.
+  issue(0, 0);
+  if (G > 1) issue(1, 1);
+  for (int g = 0; g < G; ++g) {
+    if (g + 1 < G) wait_vmcnt<LOADS>();
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    if (g + 2 < G) issue(g + 2, (g + 2) % kPfStages);
+    compute(g % kPfStages, g);
   }
   if constexpr (PARTIALS) return;
 
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
+  for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int64_t m = static_cast<int64_t>(bm) * kBM + wm * 64 + mi * 32 + 8 * (v >> 2) + 4 * hj + (v & 3);
+      const int64_t m = static_cast<int64_t>(bm) * BM + arow[tm] - r32 + 8 * (v >> 2) + 4 * hj + (v & 3);
       if (m >= M) continue;
       const float xsm = xs[m];
 #pragma unroll
-      for (int ni = 0; ni < 2; ++ni) {
-        const int n = bn * kBN + wn * 64 + ni * 32 + r32;
-        if (n < N) pq_store_dyn(y, y_dtype, m * N + n, epilogue(acc[mi][ni][v], xsm, bias, bias_dtype, n));
+      for (int tn = 0; tn < TN; ++tn) {
+        const int n = bn * BN + bcol[tn];
+        if (n < N) pq_store_dyn(y, y_dtype, m * N + n, epilogue(acc[tm][tn][v], xsm, bias, bias_dtype, n));
       }
     }
+}
+
+template <int BM, int BN, int WM, int WN, bool PARTIALS>
+void launch_prefill_t(const int8_t* xq, const float* xs, const uint8_t* wpack, const uint32_t* wmeta,
+                      const void* bias, int bias_dtype, void* y, int y_dtype, int32_t* partials, int M, int N, int K,
+                      hipStream_t stream) {
+  constexpr int STAGE = BM * 128 + (BN / 16) * kPfBStride + BN * 4;
+  const unsigned grid = static_cast<unsigned>(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
+  gemm_prefill<BM, BN, WM, WN, PARTIALS><<<grid, WM * WN * 64, kPfStages * STAGE, stream>>>(
+      xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype, partials, M, N, K);
+}
+
+// 192 x 256 tiles (8 waves of 96 x 64) when there are enough of them to fill
+// the chip, else 128 x 128 (4 waves, several workgroups per CU).
+template <bool PARTIALS>
+void launch_prefill(const int8_t* xq, const float* xs, const uint8_t* wpack, const uint32_t* wmeta, const void* bias,
+                    int bias_dtype, void* y, int y_dtype, int32_t* partials, int M, int N, int K,
+                    hipStream_t stream) {
+  const int64_t big = static_cast<int64_t>((M + 191) / 192) * ((N + 255) / 256);
+  if (big >= 256)
+    launch_prefill_t<192, 256, 2, 4, PARTIALS>(xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype, partials, M, N, K,
+                                               stream);
+  else
+    launch_prefill_t<128, 128, 2, 2, PARTIALS>(xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype, partials, M, N, K,
+                                               stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -480,6 +556,9 @@ int check_gemm_args(const char* who, int64_t m, int64_t n, int64_t k, int group_
              (long long)n);
   PQ_REQUIRE(k > 0 && k % 128 == 0 && k <= (1 << 20), PQ_ERR_ARG, "%s: k=%lld must be a positive multiple of 128",
              who, (long long)k);
+  // the kernels address A and the packed weights with 32-bit element offsets
+  PQ_REQUIRE(m * k < (int64_t(1) << 31) && n * k / 2 < (int64_t(1) << 31), PQ_ERR_ARG,
+             "%s: m*k=%lld and n*k/2=%lld must stay below 2^31", who, (long long)(m * k), (long long)(n * k / 2));
   return PQ_OK;
 }
 
@@ -531,8 +610,7 @@ extern "C" int pq_w4a8_gemm(const int8_t* xq, const float* xscale, const uint8_t
     launch_skinny<false, 0>(choose_skinny(m, n, k), xq, xscale, nullptr, nullptr, wpack, wmeta, bias, bias_dtype, y, y_dtype, nullptr, M,
                          N, K, s);
   } else {
-    const unsigned grid = static_cast<unsigned>(((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN));
-    gemm_tiled<false><<<grid, 256, 0, s>>>(xq, xscale, wpack, wmeta, bias, bias_dtype, y, y_dtype, nullptr, M, N, K);
+    launch_prefill<false>(xq, xscale, wpack, wmeta, bias, bias_dtype, y, y_dtype, nullptr, M, N, K, s);
   }
   return pq::launch_status("pq_w4a8_gemm launch");
 }
@@ -553,8 +631,7 @@ extern "C" int pq_w4a8_gemm_partials(const int8_t* xq, const uint8_t* wpack, con
     launch_skinny<true, 0>(choose_skinny(m, n, k), xq, nullptr, nullptr, nullptr, wpack, wmeta, nullptr, 0, nullptr, 0, partials, M, N,
                         K, s);
   } else {
-    const unsigned grid = static_cast<unsigned>(((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN));
-    gemm_tiled<true><<<grid, 256, 0, s>>>(xq, nullptr, wpack, wmeta, nullptr, 0, nullptr, 0, partials, M, N, K);
+    launch_prefill<true>(xq, nullptr, wpack, wmeta, nullptr, 0, nullptr, 0, partials, M, N, K, s);
   }
   return pq::launch_status("pq_w4a8_gemm_partials launch");
 }

@@ -42,10 +42,13 @@ def test_prepack_bit_exact(N, K):
 
 
 SHAPES = [(1, 16, 128), (3, 64, 256), (16, 1024, 4096), (4, 4096, 4096), (1, 1024, 4096), (17, 128, 256),
-          (33, 48, 256), (130, 256, 512), (257, 384, 1024), (64, 1024, 12288)]
+          (33, 48, 256), (130, 256, 512), (257, 384, 1024), (64, 1024, 12288), (200, 1552, 384)]
+# prefill tiling: 192 x 128 workgroup tiles once there are >= 384 of them (odd group count,
+# ragged M and a partial last column tile included); 128 x 64 otherwise.
+BIG_TILE_SHAPES = [(1100, 8176, 384), (1152, 8192, 512)]
 
 
-@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("M,N,K", SHAPES + BIG_TILE_SHAPES)
 def test_partials_bit_exact(M, N, K):
     print(f"partials M={M} N={N} K={K}", flush=True)
     w, xq, _ = _case(M, N, K, zlib.crc32(f"p{M}-{N}-{K}".encode()))
