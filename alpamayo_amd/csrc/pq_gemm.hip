@@ -286,6 +286,7 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
 // accumulators.
 // ---------------------------------------------------------------------------
 constexpr int kPfStages = 3;
+constexpr int kPfGroupM = 4;   // tile rows walked together by one XCD's run of tiles
 constexpr int kPfBStride = 1024 + 128;
 
 __device__ __forceinline__ int pf_swz(int line) { return (line >> 1) & 7; }
@@ -332,8 +333,17 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
   const int G = K >> 7;
   const int ntiles16 = N >> 4;
   const int nbn = (N + BN - 1) / BN;
-  const int bm = blockIdx.x / nbn;
-  const int bn = blockIdx.x % nbn;
+  // Tile order: workgroup b runs on XCD b % 8, so the grid is first cut
+  // into 8 contiguous runs of tiles (one per XCD, when the count divides),
+  // and each run walks kPfGroupM tile rows at a time, column by column:
+  // the tiles one XCD holds at once share A rows and B columns in its L2.
+  int t = blockIdx.x;
+  if (gridDim.x % 8 == 0) t = (t % 8) * (gridDim.x / 8) + t / 8;
+  const int nbm = (M + BM - 1) / BM;
+  const int first_bm = t / (kPfGroupM * nbn) * kPfGroupM;
+  const int gm = min(nbm - first_bm, kPfGroupM);
+  const int bm = first_bm + (t % (kPfGroupM * nbn)) % gm;
+  const int bn = (t % (kPfGroupM * nbn)) / gm;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN;
@@ -449,6 +459,12 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
   // own loads of g (those of g+1 may stay in flight), then a barrier makes
   // everybody's loads of g visible and retires everybody's use of the stage
   // that group g+2 is about to overwrite.
+  // The tile's activation scales go to LDS past the ring ahead of every
+  // other load, so the first wait covers them (the partials mode has none).
+  if (!PARTIALS && wave * 64 < BM) {
+    const int r = min(wave * 64 + lane, BM - 1);
+    lds_copy4(xs + min(bm * BM + r, M - 1), lds0 + kPfStages * STAGE + wave * 256);
+  }
   issue(0, 0);
   if (G > 1) issue(1, 1);
   for (int g = 0; g < G; ++g) {
@@ -460,19 +476,43 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
   }
   if constexpr (PARTIALS) return;
 
+  // Output, one 32-row slice per wave row at a time (WM*32 rows of the
+  // tile): the waves write their values in the output type to LDS, then
+  // every lane stores 16 contiguous bytes along n.  The row pitch keeps the
+  // two half-waves' writes (rows 4 apart) in different banks.
+  const int esz = y_dtype == PQ_F32 ? 4 : 2;
+  const int pitch = BN * esz + 32;
+  const int cpr = BN * esz / 16;   // 16-byte chunks per staged row
+  static_assert(kPfStages * STAGE >= WM * 32 * (BN * 4 + 32), "output slice fits in the stage ring");
+  const float* xs_tile = reinterpret_cast<const float*>(smem + kPfStages * STAGE);
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm)
+  for (int tm = 0; tm < TM; ++tm) {
+    __syncthreads();   // the stages (or the previous slice) are no longer read
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int64_t m = static_cast<int64_t>(bm) * BM + arow[tm] - r32 + 8 * (v >> 2) + 4 * hj + (v & 3);
-      if (m >= M) continue;
-      const float xsm = xs[m];
+      const int r = 8 * (v >> 2) + 4 * hj + (v & 3);
+      const int64_t m = static_cast<int64_t>(bm) * BM + wm * (BM / WM) + tm * 32 + r;
+      const float xsm = xs_tile[wm * (BM / WM) + tm * 32 + r];
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn) {
-        const int n = bn * BN + bcol[tn];
-        if (n < N) pq_store_dyn(y, y_dtype, m * N + n, epilogue(acc[tm][tn][v], xsm, bias, bias_dtype, n));
+        const int n = min(bn * BN + bcol[tn], N - 1);
+        const float val = epilogue(acc[tm][tn][v], xsm, bias, bias_dtype, n);
+        uint8_t* dst = smem + (wm * 32 + r) * pitch + bcol[tn] * esz;
+        if (y_dtype == PQ_F32) *reinterpret_cast<float*>(dst) = val;
+        else if (y_dtype == PQ_F16) *reinterpret_cast<uint16_t*>(dst) = pq_f32_to_f16(val);
+        else *reinterpret_cast<uint16_t*>(dst) = pq_f32_to_bf16(val);
       }
     }
+    __syncthreads();
+    for (int c = threadIdx.x; c < WM * 32 * cpr; c += NW * 64) {
+      const int sr = c / cpr, cc = c % cpr;
+      const int64_t m = static_cast<int64_t>(bm) * BM + (sr >> 5) * (BM / WM) + tm * 32 + (sr & 31);
+      const int n0 = bn * BN + cc * (16 / esz);
+      if (m < M && n0 < N)
+        *reinterpret_cast<uint4*>(static_cast<uint8_t*>(y) + (m * N + n0) * esz) =
+            *reinterpret_cast<const uint4*>(smem + sr * pitch + cc * 16);
+    }
+  }
 }
 
 template <int BM, int BN, int WM, int WN, bool PARTIALS>
@@ -481,7 +521,7 @@ void launch_prefill_t(const int8_t* xq, const float* xs, const uint8_t* wpack, c
                       hipStream_t stream) {
   constexpr int STAGE = BM * 128 + (BN / 16) * kPfBStride + BN * 4;
   const unsigned grid = static_cast<unsigned>(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
-  gemm_prefill<BM, BN, WM, WN, PARTIALS><<<grid, WM * WN * 64, kPfStages * STAGE, stream>>>(
+  gemm_prefill<BM, BN, WM, WN, PARTIALS><<<grid, WM * WN * 64, kPfStages * STAGE + BM * 4, stream>>>(
       xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype, partials, M, N, K);
 }
 

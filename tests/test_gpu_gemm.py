@@ -43,9 +43,9 @@ def test_prepack_bit_exact(N, K):
 
 SHAPES = [(1, 16, 128), (3, 64, 256), (16, 1024, 4096), (4, 4096, 4096), (1, 1024, 4096), (17, 128, 256),
           (33, 48, 256), (130, 256, 512), (257, 384, 1024), (64, 1024, 12288), (200, 1552, 384)]
-# prefill tiling: 192 x 128 workgroup tiles once there are >= 384 of them (odd group count,
-# ragged M and a partial last column tile included); 128 x 64 otherwise.
-BIG_TILE_SHAPES = [(1100, 8176, 384), (1152, 8192, 512)]
+# prefill tiling: 192 x 256 workgroup tiles once there are >= 256 of them, 128 x 128 otherwise.
+# These reach the big tiles with an odd group count, ragged M and a partial last column tile.
+BIG_TILE_SHAPES = [(1500, 8176, 384), (3000, 4112, 256)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES + BIG_TILE_SHAPES)
@@ -58,7 +58,7 @@ def test_partials_bit_exact(M, N, K):
     np.testing.assert_array_equal(to_np(P), ref)
 
 
-@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("M,N,K", SHAPES + BIG_TILE_SHAPES)
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_gemm_matches_oracle(M, N, K, out_dtype):
     print(f"gemm M={M} N={N} K={K} {out_dtype}", flush=True)
@@ -84,6 +84,18 @@ def test_gemm_bias_and_repeatability():
     ref = ogemm.w4a8_linear(xq.numpy(), xs.numpy(), w.codes.numpy(), w.awq_scales.numpy(), w.zeros.numpy(),
                             bias.float().numpy())
     assert_bf16_close(to_np(y1), ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(5, 1024, 4096), (1500, 8176, 384)])
+def test_gemm_bias_f32_out(M, N, K):
+    w, xq, xs = _case(M, N, K, 7 + M)
+    wp, wm = _prepack(w)
+    bias = torch.randn(N).half()
+    ws = torch.zeros(max(pqops.workspace_bytes(M, N, K), 1), dtype=torch.uint8, device="cuda")
+    y = torch.ops.paroquant.w4a8_gemm(xq.cuda(), xs.cuda(), wp, wm, bias.cuda(), ws, torch.float32)
+    ref = ogemm.w4a8_linear(xq.numpy(), xs.numpy(), w.codes.numpy(), w.awq_scales.numpy(), w.zeros.numpy(),
+                            bias.float().numpy())
+    assert_bf16_close(to_np(y), ref)
 
 
 def test_gemm_extreme_operands_exact():
