@@ -136,4 +136,69 @@ __device__ __forceinline__ void rot_layer(const RotLane<KP>& p, int r, float (&a
   }
 }
 
+// One wave rotates 128-channel group g of the first min(M, MR) rows: channel
+// scale, the krot register-chain layers, then the rotated values go to xr
+// (fp16 when MAT16, else fp32; row stride h) and each row's absmax over the
+// group to gmax[m * (h / 128) + g].  With PQ_RQ_INPUT_FP16 the scaled input
+// is first rounded through fp16.  Rows past M repeat row M-1 and store
+// nothing.
+template <int DT, int KP, bool MAT16, int MR>
+__device__ __forceinline__ void rotate_group_rows(const void* __restrict__ x, const uint32_t* __restrict__ rot_idx,
+                                                  const float* __restrict__ rot_cs, const float* __restrict__ scales,
+                                                  void* __restrict__ xr, float* __restrict__ gmax, int M, int h,
+                                                  int krot, unsigned flags, int g, int lane) {
+  const int G = h >> 7;
+  const bool in16 = (flags & PQ_RQ_INPUT_FP16) != 0;
+  const bool has_scales = scales != nullptr;
+  // unconditional scale loads (from rot_cs when there are no scales): a
+  // branch around them would make the compiler wait for them early
+  const float* sp = has_scales ? scales : rot_cs;
+  const int smask = has_scales ? 0x7fffffff : 0;
+
+  RotLane<KP> p;
+  load_rot_lane<KP>(rot_idx, rot_cs, g, lane, p);
+  uint32_t xa[MR], xb[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    const int mm = m < M ? m : M - 1;
+    xa[m] = pq_load_raw<DT>(x, static_cast<int64_t>(mm) * h + g * 128 + lane);
+    xb[m] = pq_load_raw<DT>(x, static_cast<int64_t>(mm) * h + g * 128 + 64 + lane);
+  }
+  const float s0r = sp[(g * 128 + lane) & smask];
+  const float s1r = sp[(g * 128 + 64 + lane) & smask];
+  const float s0 = has_scales ? s0r : 1.0f, s1 = has_scales ? s1r : 1.0f;
+  const bool sw = rot_init_swapped(p);
+  float a[MR], b[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    float lo = pq_raw_to_f32<DT>(xa[m]), hi = pq_raw_to_f32<DT>(xb[m]);
+    lo = (in16 ? pq_round_f16(lo) : lo) * s0;
+    hi = (in16 ? pq_round_f16(hi) : hi) * s1;
+    a[m] = sw ? hi : lo;
+    b[m] = sw ? lo : hi;
+  }
+#pragma unroll
+  for (int k = 0; k < KP; ++k)
+    if (k < krot) rot_layer<KP, MR>(p, k, a, b);
+  const int fa = g * 128 + rot_final_a(p), fb = g * 128 + rot_final_b(p);
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    float va = a[m], vb = b[m];
+    if (m < M) {
+      if constexpr (MAT16) {
+        const uint16_t ha = pq_f32_to_f16(va), hb = pq_f32_to_f16(vb);
+        static_cast<uint16_t*>(xr)[static_cast<int64_t>(m) * h + fa] = ha;
+        static_cast<uint16_t*>(xr)[static_cast<int64_t>(m) * h + fb] = hb;
+        va = pq_f16_to_f32(ha);
+        vb = pq_f16_to_f32(hb);
+      } else {
+        static_cast<float*>(xr)[static_cast<int64_t>(m) * h + fa] = va;
+        static_cast<float*>(xr)[static_cast<int64_t>(m) * h + fb] = vb;
+      }
+    }
+    const float mx = pq_wave_max(fmaxf(fabsf(va), fabsf(vb)));
+    if (m < M && lane == 0) gmax[static_cast<int64_t>(m) * G + g] = mx;
+  }
+}
+
 }  // namespace pqd

@@ -296,59 +296,10 @@ __global__ __launch_bounds__(kSplitWaves * 64) void rotate_split_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ rot_idx, const float* __restrict__ rot_cs,
     const float* __restrict__ scales, void* __restrict__ xr, float* __restrict__ gmax, int M, int h, int krot,
     unsigned flags) {
-  const int lane = threadIdx.x & 63;
-  const int G = h >> 7;
   const int g = blockIdx.x * kSplitWaves + (threadIdx.x >> 6);
-  if (g >= G) return;   // whole waves only; this kernel has no barrier
-  const bool in16 = (flags & PQ_RQ_INPUT_FP16) != 0;
-  const bool has_scales = scales != nullptr;
-  const float* sp = has_scales ? scales : rot_cs;
-  const int smask = has_scales ? 0x7fffffff : 0;
-
-  pqd::RotLane<KP> p;
-  pqd::load_rot_lane<KP>(rot_idx, rot_cs, g, lane, p);
-  uint32_t xa[MR], xb[MR];
-#pragma unroll
-  for (int m = 0; m < MR; ++m) {
-    const int mm = m < M ? m : M - 1;
-    xa[m] = pq_load_raw<DT>(x, static_cast<int64_t>(mm) * h + g * 128 + lane);
-    xb[m] = pq_load_raw<DT>(x, static_cast<int64_t>(mm) * h + g * 128 + 64 + lane);
-  }
-  const float s0r = sp[(g * 128 + lane) & smask];
-  const float s1r = sp[(g * 128 + 64 + lane) & smask];
-  const float s0 = has_scales ? s0r : 1.0f, s1 = has_scales ? s1r : 1.0f;
-  const bool sw = pqd::rot_init_swapped(p);
-  float a[MR], b[MR];
-#pragma unroll
-  for (int m = 0; m < MR; ++m) {
-    float lo = pq_raw_to_f32<DT>(xa[m]), hi = pq_raw_to_f32<DT>(xb[m]);
-    lo = (in16 ? pq_round_f16(lo) : lo) * s0;
-    hi = (in16 ? pq_round_f16(hi) : hi) * s1;
-    a[m] = sw ? hi : lo;
-    b[m] = sw ? lo : hi;
-  }
-#pragma unroll
-  for (int k = 0; k < KP; ++k)
-    if (k < krot) pqd::rot_layer<KP, MR>(p, k, a, b);
-  const int fa = g * 128 + pqd::rot_final_a(p), fb = g * 128 + pqd::rot_final_b(p);
-#pragma unroll
-  for (int m = 0; m < MR; ++m) {
-    float va = a[m], vb = b[m];
-    if (m < M) {
-      if constexpr (MAT16) {
-        const uint16_t ha = pq_f32_to_f16(va), hb = pq_f32_to_f16(vb);
-        static_cast<uint16_t*>(xr)[static_cast<int64_t>(m) * h + fa] = ha;
-        static_cast<uint16_t*>(xr)[static_cast<int64_t>(m) * h + fb] = hb;
-        va = pq_f16_to_f32(ha);
-        vb = pq_f16_to_f32(hb);
-      } else {
-        static_cast<float*>(xr)[static_cast<int64_t>(m) * h + fa] = va;
-        static_cast<float*>(xr)[static_cast<int64_t>(m) * h + fb] = vb;
-      }
-    }
-    const float mx = pq_wave_max(fmaxf(fabsf(va), fabsf(vb)));
-    if (m < M && lane == 0) gmax[static_cast<int64_t>(m) * G + g] = mx;
-  }
+  if (g >= (h >> 7)) return;   // whole waves only; this kernel has no barrier
+  pqd::rotate_group_rows<DT, KP, MAT16, MR>(x, rot_idx, rot_cs, scales, xr, gmax, M, h, krot, flags, g,
+                                            threadIdx.x & 63);
 }
 
 template <int DT, int KP, bool MAT16>
