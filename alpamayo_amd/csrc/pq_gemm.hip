@@ -26,9 +26,12 @@
 //                v_mfma_i32_16x16x64_i8 per block (activation rows padded to
 //                16); the waves of a workgroup split K and add their partial
 //                sums in LDS in a fixed order.
-//   gemm_prefill M > 16: 192x128 (or 128x64) output tiles, 2x2 waves, operands
-//                staged through a 3-stage LDS ring fed by two register
-//                stages, v_mfma_i32_32x32x32_i8 tiles.
+//   gemm_prefill M > 16: 192x256 (or 128x128) output tiles, 8 (or 4) waves
+//                side by side along n, operands copied from global memory
+//                straight into a 3-stage LDS ring, v_mfma_i32_32x32x32_i8
+//                tiles, the output staged through LDS for 16-byte stores.
+#include <type_traits>
+
 #include "pq_device.h"
 #include "pq_internal.h"
 
@@ -283,7 +286,10 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
 // 1152-byte stride, which keeps the fragment reads free of bank conflicts.
 // B is unpacked to signed int8 (q - z) in registers at use.  After each
 // group the int32 tiles are scaled by the group's fp16 scales into fp32
-// accumulators.
+// accumulators.  The waves sit side by side along n (WM = 1): each B tile is
+// then unpacked by one wave only -- the unpack and the per-group scaling
+// are the kernel's VALU load, which bounds it (without packed fp32 the
+// scaling alone costs as many VALU cycles as the int8 MFMAs of the group).
 // ---------------------------------------------------------------------------
 constexpr int kPfStages = 3;
 constexpr int kPfGroupM = 4;   // tile rows walked together by one XCD's run of tiles
@@ -305,6 +311,15 @@ __device__ __forceinline__ void lds_copy16(const void* gsrc, uint32_t lds) {
 }
 __device__ __forceinline__ void lds_copy4(const void* gsrc, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(gsrc) : "memory", "m0");
+}
+
+// Barrier for LDS hand-offs only: the wave's LDS operations complete, then
+// s_barrier.  Unlike __syncthreads() it does not wait for the wave's global
+// stores (vmcnt), which may stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // s_waitcnt with vmcnt(n), any lgkmcnt/expcnt (gfx9 immediate encoding).
@@ -478,41 +493,56 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
 
   // Output, one 32-row slice per wave row at a time (WM*32 rows of the
   // tile): the waves write their values in the output type to LDS, then
-  // every lane stores 16 contiguous bytes along n.  The row pitch keeps the
-  // two half-waves' writes (rows 4 apart) in different banks.
-  const int esz = y_dtype == PQ_F32 ? 4 : 2;
-  const int pitch = BN * esz + 32;
-  const int cpr = BN * esz / 16;   // 16-byte chunks per staged row
+  // every lane stores 16 contiguous bytes along n, non-temporal (streamed
+  // out rather than left dirty in L2 for the end of the kernel to write
+  // back).  The row pitch keeps the
+  // two half-waves' writes (rows 4 apart) in different banks.  The bias
+  // values are loaded once and the output type is a template parameter:
+  // a global load or a dtype branch inside the element loop makes the
+  // compiler wait for the stores in flight (vmcnt(0)) at every join.
   static_assert(kPfStages * STAGE >= WM * 32 * (BN * 4 + 32), "output slice fits in the stage ring");
   const float* xs_tile = reinterpret_cast<const float*>(smem + kPfStages * STAGE);
+  const bool has_bias = bias != nullptr;
+  float bv[TN];
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm) {
-    __syncthreads();   // the stages (or the previous slice) are no longer read
+  for (int tn = 0; tn < TN; ++tn)
+    bv[tn] = has_bias ? pq_load_dyn(bias, bias_dtype, min(bn * BN + bcol[tn], N - 1)) : 0.0f;
+  auto emit = [&](auto out_dtype) {
+    constexpr int DT = decltype(out_dtype)::value;
+    constexpr int ESZ = DT == PQ_F32 ? 4 : 2;
+    constexpr int PITCH = BN * ESZ + 32;
+    constexpr int CPR = BN * ESZ / 16;   // 16-byte chunks per staged row
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int r = 8 * (v >> 2) + 4 * hj + (v & 3);
-      const int64_t m = static_cast<int64_t>(bm) * BM + wm * (BM / WM) + tm * 32 + r;
-      const float xsm = xs_tile[wm * (BM / WM) + tm * 32 + r];
+    for (int tm = 0; tm < TM; ++tm) {
+      lds_barrier();   // the stages (or the previous slice) are no longer read
 #pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const int n = min(bn * BN + bcol[tn], N - 1);
-        const float val = epilogue(acc[tm][tn][v], xsm, bias, bias_dtype, n);
-        uint8_t* dst = smem + (wm * 32 + r) * pitch + bcol[tn] * esz;
-        if (y_dtype == PQ_F32) *reinterpret_cast<float*>(dst) = val;
-        else if (y_dtype == PQ_F16) *reinterpret_cast<uint16_t*>(dst) = pq_f32_to_f16(val);
-        else *reinterpret_cast<uint16_t*>(dst) = pq_f32_to_bf16(val);
+      for (int v = 0; v < 16; ++v) {
+        const int r = 8 * (v >> 2) + 4 * hj + (v & 3);
+        const float xsm = xs_tile[wm * (BM / WM) + tm * 32 + r];
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+          float val = acc[tm][tn][v] * xsm;
+          if (has_bias) val = val + bv[tn];
+          uint8_t* dst = smem + (wm * 32 + r) * PITCH + bcol[tn] * ESZ;
+          if constexpr (DT == PQ_F32) *reinterpret_cast<float*>(dst) = val;
+          else if constexpr (DT == PQ_F16) *reinterpret_cast<uint16_t*>(dst) = pq_f32_to_f16(val);
+          else *reinterpret_cast<uint16_t*>(dst) = pq_f32_to_bf16(val);
+        }
+      }
+      lds_barrier();
+      for (int c = threadIdx.x; c < WM * 32 * CPR; c += NW * 64) {
+        const int sr = c / CPR, cc = c % CPR;
+        const int64_t m = static_cast<int64_t>(bm) * BM + (sr >> 5) * (BM / WM) + tm * 32 + (sr & 31);
+        const int n0 = bn * BN + cc * (16 / ESZ);
+        if (m < M && n0 < N)
+          __builtin_nontemporal_store(*reinterpret_cast<const v4i*>(smem + sr * PITCH + cc * 16),
+                                      reinterpret_cast<v4i*>(static_cast<uint8_t*>(y) + (m * N + n0) * ESZ));
       }
     }
-    __syncthreads();
-    for (int c = threadIdx.x; c < WM * 32 * cpr; c += NW * 64) {
-      const int sr = c / cpr, cc = c % cpr;
-      const int64_t m = static_cast<int64_t>(bm) * BM + (sr >> 5) * (BM / WM) + tm * 32 + (sr & 31);
-      const int n0 = bn * BN + cc * (16 / esz);
-      if (m < M && n0 < N)
-        *reinterpret_cast<uint4*>(static_cast<uint8_t*>(y) + (m * N + n0) * esz) =
-            *reinterpret_cast<const uint4*>(smem + sr * pitch + cc * 16);
-    }
-  }
+  };
+  if (y_dtype == PQ_F32) emit(std::integral_constant<int, PQ_F32>{});
+  else if (y_dtype == PQ_F16) emit(std::integral_constant<int, PQ_F16>{});
+  else emit(std::integral_constant<int, PQ_BF16>{});
 }
 
 template <int BM, int BN, int WM, int WN, bool PARTIALS>
@@ -533,10 +563,10 @@ void launch_prefill(const int8_t* xq, const float* xs, const uint8_t* wpack, con
                     hipStream_t stream) {
   const int64_t big = static_cast<int64_t>((M + 191) / 192) * ((N + 255) / 256);
   if (big >= 256)
-    launch_prefill_t<192, 256, 2, 4, PARTIALS>(xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype, partials, M, N, K,
+    launch_prefill_t<192, 256, 1, 8, PARTIALS>(xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype, partials, M, N, K,
                                                stream);
   else
-    launch_prefill_t<128, 128, 2, 2, PARTIALS>(xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype, partials, M, N, K,
+    launch_prefill_t<128, 128, 1, 4, PARTIALS>(xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype, partials, M, N, K,
                                                stream);
 }
 
