@@ -411,7 +411,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) bcol[tn] = wn * (BN / WN) + tn * 32 + r32;
 
-  auto compute = [&](int stage, int g) {
+  // Matrix work of group g from its stage.  The loads of group ig (= g + 2)
+  // are issued after the first two k-steps' MFMAs: issued at the top of the
+  // group, right after the barrier, all waves' copies queue up at once in
+  // the load path while no MFMA is in flight.
+  auto compute = [&](int stage, int g, int ig) {
     const uint8_t* As = smem + stage * STAGE;
     const uint8_t* Bs = As + A_BYTES;
     const uint32_t* Ms = reinterpret_cast<const uint32_t*>(Bs + B_BYTES);
@@ -447,6 +451,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn)
           T[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[tm], b[tn], T[tm][tn], 0, 0, 0);
+      if (i == 1 && ig < G) issue(ig, ig % kPfStages);
     }
     if constexpr (PARTIALS) {
 #pragma unroll
@@ -486,8 +491,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
     if (g + 1 < G) wait_vmcnt<LOADS>();
     else wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
-    if (g + 2 < G) issue(g + 2, (g + 2) % kPfStages);
-    compute(g % kPfStages, g);
+    compute(g % kPfStages, g, g + 2);
   }
   if constexpr (PARTIALS) return;
 
