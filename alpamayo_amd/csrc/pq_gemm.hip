@@ -55,6 +55,15 @@ namespace {
 // the int8 codes of all M rows into LDS (row stride K + 16 bytes, so the 16
 // rows of an A fragment hit distinct banks) and reads A from there.  The
 // first batch of weight loads is issued before that prologue.
+// Barrier for LDS hand-offs only: the wave's LDS operations complete, then
+// s_barrier.  Unlike __syncthreads() it does not wait for the wave's global
+// stores (vmcnt), which may stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 constexpr int kSkinnyRows = 16;
 
 template <int NT, int W, int U, bool PARTIALS, int AQ>
@@ -156,7 +165,7 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
       if (it == 0) {
         // Part 2: token scales, then the int8 image of A in LDS.
         if (threadIdx.x < kSkinnyRows) s_amax[threadIdx.x] = 0.0f;
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int q = 0; q < kPreMax; ++q) {   // absmax >= 0: unsigned order is float order
           const int i = threadIdx.x + q * nthr;
@@ -164,7 +173,7 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
         }
         for (int i = threadIdx.x + kPreMax * nthr; i < M * G; i += nthr)
           atomicMax(reinterpret_cast<unsigned*>(&s_amax[i / G]), __float_as_uint(gmax[i]));
-        __syncthreads();
+        lds_barrier();
         auto quant8 = [&](int e, const uint4* v) {
           const int r = e / k8;
           const int c8 = (e - r * k8) * 8;
@@ -210,7 +219,7 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
             quant8(e, v);
           }
         }
-        __syncthreads();
+        lds_barrier();
       }
     }
 #pragma unroll
@@ -311,15 +320,6 @@ __device__ __forceinline__ void lds_copy16(const void* gsrc, uint32_t lds) {
 }
 __device__ __forceinline__ void lds_copy4(const void* gsrc, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(gsrc) : "memory", "m0");
-}
-
-// Barrier for LDS hand-offs only: the wave's LDS operations complete, then
-// s_barrier.  Unlike __syncthreads() it does not wait for the wave's global
-// stores (vmcnt), which may stay in flight.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
 }
 
 // s_waitcnt with vmcnt(n), any lgkmcnt/expcnt (gfx9 immediate encoding).

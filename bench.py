@@ -5,9 +5,11 @@
 Workload of ``value`` (one "step"): one Qwen3-8B decoder layer's seven
 quantized linears (q/o 4096->4096, k/v 4096->1024, gate/up 4096->12288,
 down 12288->4096) at M = 1 decode token, bf16 in and out, each linear =
-fused rotate+quant kernel + W4A8 GEMM kernel, replayed as one HIP graph per
-layer.  Steps cycle through a pool of distinct layers (> 512 MB of weights)
-so the 256 MB Infinity Cache cannot serve them.  value = algorithmic bytes
+rotation kernel + W4A8 GEMM kernel.  A pool of distinct layers (8 by
+default, 772 MB of weights, so the 256 MB Infinity Cache cannot serve them)
+is captured as ONE HIP graph, the way a model's decode step is captured
+whole; a replay is as many steps as the pool has layers, and --steps is
+rounded up to a whole number of replays.  value = algorithmic bytes
 of the layer / time per step, in GB/s, where per linear
   B = N*K/2 + 2*N*K/128 + N*K/256 + 3*8*K + 2*K + 2*M*K + 2*M*N.
 Also reported: M = 4 and 16 decode, M = 3072 prefill in int8 TOPS and % of
@@ -53,7 +55,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--pool-layers", type=int, default=6)
+    ap.add_argument("--pool-layers", type=int, default=8)
     ap.add_argument("--prefill-steps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-prefill", action="store_true")
@@ -62,6 +64,8 @@ def main() -> int:
                     help="comma-separated decode token counts to time (M = 1 gives value)")
     args = ap.parse_args()
 
+    if args.steps % args.pool_layers:
+        args.steps += args.pool_layers - args.steps % args.pool_layers   # whole replays of the pool graph
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)",
               file=sys.stderr)
@@ -96,8 +100,9 @@ def main() -> int:
         return [[workloads.activations(M, K, g, device=dev) for (_, K) in shapes] for _ in pool]
 
     def capture_layers(M, seed):
+        """One HIP graph holding the whole pool of layers in sequence, as a
+        model's decode step is captured whole: a replay is len(pool) steps."""
         xs = make_inputs(M, seed)
-        graphs, outs = [], []
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -105,13 +110,10 @@ def main() -> int:
                 for m, x in zip(L, X):
                     m(x)
         torch.cuda.current_stream().wait_stream(s)
-        for L, X in zip(pool, xs):
-            gr = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(gr):
-                o = [m(x) for m, x in zip(L, X)]
-            graphs.append(gr)
-            outs.append(o)
-        return graphs, outs, xs
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            outs = [[m(x) for m, x in zip(L, X)] for L, X in zip(pool, xs)]
+        return gr, outs, xs
 
     def time_graphs(graphs, steps, warmup):
         for i in range(warmup):
@@ -130,13 +132,15 @@ def main() -> int:
     # ---- decode: M = 1 (value), 4, 16 -------------------------------------
     decode = {}
     decode_ms = sorted({int(v) for v in args.decode_m.split(",")} | {1})
+    P = len(pool)
     for M in decode_ms:
-        graphs, _, _ = capture_layers(M, 5000 + M)
-        ms = time_graphs(graphs, args.steps, args.warmup)
+        gr, _, _ = capture_layers(M, 5000 + M)
+        # K steps = K / P replays of the pool graph (steps is a multiple of P)
+        ms = time_graphs([gr], args.steps // P, -(-args.warmup // P)) / P
         b = sum(linear_bytes(M, N, K) for N, K in shapes)
         decode[M] = (ms, b / (ms * 1e-3) / 1e9)
         log(f"decode M={M}: {ms * 1e3:.1f} us/layer, {decode[M][1]:.0f} GB/s")
-        del graphs
+        del gr
     ms_per_step, value = decode[1]
 
     # ---- roofline of the dominant kernel: the decode GEMM at M = 1 --------
@@ -224,6 +228,7 @@ def main() -> int:
             "weight_pool_layers": args.pool_layers,
             "weight_pool_mb": round(pool_mb, 1),
             "graph_replay": True,
+            "layers_per_graph": args.pool_layers,
         },
         "roofline": {
             "bound": "hbm",
