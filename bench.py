@@ -32,6 +32,21 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+COPY_CAL_BYTES = 256 << 20
+# HBM bytes per decode-GEMM launch, measured with rocprofv3 FETCH_SIZE and
+# WRITE_SIZE passes and calibrated on a copy of known size; the summary
+# (with the commands that made it) holds it on a "traffic_bytes_per_launch:" line.
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "decode_gemm_m1_hbm_traffic.md")
+
+
+def measured_traffic():
+    try:
+        for line in open(TRAFFIC_SUMMARY):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 INT8_PEAK_TOPS = 5000.0
 KROT = 8
 
@@ -60,6 +75,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first copy 256 MiB device to device 3 times: the known-size kernel that calibrates "
+                         "the FETCH_SIZE / WRITE_SIZE counter passes")
     ap.add_argument("--decode-m", type=str, default="1,4,16",
                     help="comma-separated decode token counts to time (M = 1 gives value)")
     args = ap.parse_args()
@@ -80,6 +98,13 @@ def main() -> int:
     _lib.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        src = torch.ones(COPY_CAL_BYTES // 4, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     names = list(workloads.QWEN3_8B_LINEARS)
     shapes = [workloads.QWEN3_8B_LINEARS[n] for n in names]
 
@@ -237,7 +262,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "avg_launch_us": round(per_launch_us, 3),
         },
         "decode": {f"M{M}": {"us_per_layer": round(v[0] * 1e3, 2), "GBps": round(v[1], 1),
