@@ -31,6 +31,15 @@ _UINT = ctypes.c_uint
 _SZ = ctypes.c_size_t
 
 # name -> (restype, argtypes); mirrors include/paroquant_hip.h
+class LinearMember(ctypes.Structure):
+    """pq_linear_member: one linear of a group sharing its input (pq_w4a8_linear_group)."""
+    _fields_ = [("rot_idx", ctypes.c_void_p), ("rot_cs", ctypes.c_void_p), ("scales", ctypes.c_void_p),
+                ("wpack", ctypes.c_void_p), ("wmeta", ctypes.c_void_p), ("bias", ctypes.c_void_p),
+                ("y", ctypes.c_void_p), ("n", ctypes.c_int64)]
+
+
+MAX_GROUP = 4
+
 SIGNATURES = {
     "pq_abi_version": (_INT, []),
     "pq_last_error": (ctypes.c_char_p, []),
@@ -45,6 +54,9 @@ SIGNATURES = {
     "pq_w4a8_linear_workspace_size": (_SZ, [_I64, _I64, _I64, _INT]),
     "pq_w4a8_linear": (_INT, [_P, _INT, _P, _P, _P, _P, _P, _P, _INT, _P, _INT, _I64, _I64, _I64, _INT, _UINT, _P, _SZ,
                               _P]),
+    "pq_w4a8_linear_group_workspace_size": (_SZ, [_I64, _I64, _INT]),
+    "pq_w4a8_linear_group": (_INT, [_P, _INT, ctypes.POINTER(LinearMember), _INT, _INT, _INT, _I64, _I64, _INT, _UINT,
+                                    _P, _SZ, _P]),
 }
 
 _lock = threading.Lock()

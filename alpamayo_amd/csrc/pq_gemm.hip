@@ -66,15 +66,33 @@ __device__ __forceinline__ void lds_barrier() {
 
 constexpr int kSkinnyRows = 16;
 
+// The member of a group that owns workgroup tile `unit` (members own
+// contiguous runs of tiles; the lookup is wave-uniform).
+__device__ __forceinline__ int group_member(const pq::GemmGroup& grp, int unit) {
+  int mi = 0;
+#pragma unroll
+  for (int i = 1; i < pq::kMaxGroup; ++i)
+    if (i < grp.count && unit >= grp.first[i]) mi = i;
+  return mi;
+}
+
 template <int NT, int W, int U, bool PARTIALS, int AQ>
 __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) void gemm_skinny(
-    const int8_t* __restrict__ xq, const float* __restrict__ xs, const void* __restrict__ xr,
-    const float* __restrict__ gmax, const uint8_t* __restrict__ wpack, const uint32_t* __restrict__ wmeta,
-    const void* __restrict__ bias, int bias_dtype, void* __restrict__ y, int y_dtype, int32_t* __restrict__ partials,
-    int M, int N, int K) {
+    const pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* __restrict__ partials, int M, int K) {
   __shared__ float red[W][NT][4][64];
   __shared__ float s_amax[kSkinnyRows];
   extern __shared__ __attribute__((aligned(16))) int8_t aq[];
+  const int mi = group_member(grp, blockIdx.x);
+  const pq::GemmMember& mb = grp.mem[mi];
+  const int8_t* __restrict__ xq = mb.xq;
+  const float* __restrict__ xs = mb.xs;
+  const void* __restrict__ xr = mb.xr;
+  const float* __restrict__ gmax = mb.gmax;
+  const uint8_t* __restrict__ wpack = mb.wpack;
+  const uint32_t* __restrict__ wmeta = mb.wmeta;
+  const void* __restrict__ bias = mb.bias;
+  void* __restrict__ y = mb.y;
+  const int N = mb.n;
   const int G = K >> 7;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar branches
   const int lane = threadIdx.x & 63;
@@ -82,7 +100,7 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
   const int j = lane >> 4;
   const bool arow = c < M;
   const int astride = K + 16;
-  const int tile0 = blockIdx.x * NT;
+  const int tile0 = (blockIdx.x - grp.first[mi]) * NT;
 
   float acc[NT][4];
 #pragma unroll
@@ -331,9 +349,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 template <int BM, int BN, int WM, int WN, bool PARTIALS>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
-    const int8_t* __restrict__ xq, const float* __restrict__ xs, const uint8_t* __restrict__ wpack,
-    const uint32_t* __restrict__ wmeta, const void* __restrict__ bias, int bias_dtype, void* __restrict__ y,
-    int y_dtype, int32_t* __restrict__ partials, int M, int N, int K) {
+    const pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* __restrict__ partials, int M, int K) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
   constexpr int A_BYTES = BM * 128;                 // BM/8 blocks of 1 KB (8 rows each)
@@ -346,8 +362,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const int G = K >> 7;
-  const int ntiles16 = N >> 4;
-  const int nbn = (N + BN - 1) / BN;
+  const int nbn = grp.first[grp.count];   // BN-wide column tiles of all members
   // Tile order: workgroup b runs on XCD b % 8, so the grid is first cut
   // into 8 contiguous runs of tiles (one per XCD, when the count divides),
   // and each run walks kPfGroupM tile rows at a time, column by column:
@@ -358,7 +373,19 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
   const int first_bm = t / (kPfGroupM * nbn) * kPfGroupM;
   const int gm = min(nbm - first_bm, kPfGroupM);
   const int bm = first_bm + (t % (kPfGroupM * nbn)) % gm;
-  const int bn = (t % (kPfGroupM * nbn)) / gm;
+  const int bn_all = (t % (kPfGroupM * nbn)) / gm;
+  // The member owning this column tile (every member starts on a tile).
+  const int mi = group_member(grp, bn_all);
+  const pq::GemmMember& mb = grp.mem[mi];
+  const int8_t* __restrict__ xq = mb.xq;
+  const float* __restrict__ xs = mb.xs;
+  const uint8_t* __restrict__ wpack = mb.wpack;
+  const uint32_t* __restrict__ wmeta = mb.wmeta;
+  const void* __restrict__ bias = mb.bias;
+  void* __restrict__ y = mb.y;
+  const int N = mb.n;
+  const int ntiles16 = N >> 4;
+  const int bn = bn_all - grp.first[mi];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN;
@@ -550,28 +577,27 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
 }
 
 template <int BM, int BN, int WM, int WN, bool PARTIALS>
-void launch_prefill_t(const int8_t* xq, const float* xs, const uint8_t* wpack, const uint32_t* wmeta,
-                      const void* bias, int bias_dtype, void* y, int y_dtype, int32_t* partials, int M, int N, int K,
+void launch_prefill_t(pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* partials, int M, int K,
                       hipStream_t stream) {
   constexpr int STAGE = BM * 128 + (BN / 16) * kPfBStride + BN * 4;
-  const unsigned grid = static_cast<unsigned>(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
+  grp.first[0] = 0;
+  for (int i = 0; i < grp.count; ++i) grp.first[i + 1] = grp.first[i] + (grp.mem[i].n + BN - 1) / BN;
+  const unsigned grid = static_cast<unsigned>(((M + BM - 1) / BM) * grp.first[grp.count]);
   gemm_prefill<BM, BN, WM, WN, PARTIALS><<<grid, WM * WN * 64, kPfStages * STAGE + BM * 4, stream>>>(
-      xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype, partials, M, N, K);
+      grp, bias_dtype, y_dtype, partials, M, K);
 }
 
-// 192 x 256 tiles (8 waves of 96 x 64) when there are enough of them to fill
-// the chip, else 128 x 128 (4 waves, several workgroups per CU).
+// 192 x 256 tiles (8 waves of 192 x 32) when there are enough of them to
+// fill the chip, else 128 x 128 (4 waves, several workgroups per CU).
 template <bool PARTIALS>
-void launch_prefill(const int8_t* xq, const float* xs, const uint8_t* wpack, const uint32_t* wmeta, const void* bias,
-                    int bias_dtype, void* y, int y_dtype, int32_t* partials, int M, int N, int K,
+void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32_t* partials, int M, int K,
                     hipStream_t stream) {
-  const int64_t big = static_cast<int64_t>((M + 191) / 192) * ((N + 255) / 256);
-  if (big >= 256)
-    launch_prefill_t<192, 256, 1, 8, PARTIALS>(xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype, partials, M, N, K,
-                                               stream);
+  int64_t bn_tiles = 0;
+  for (int i = 0; i < grp.count; ++i) bn_tiles += (grp.mem[i].n + 255) / 256;
+  if (static_cast<int64_t>((M + 191) / 192) * bn_tiles >= 256)
+    launch_prefill_t<192, 256, 1, 8, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
   else
-    launch_prefill_t<128, 128, 1, 4, PARTIALS>(xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype, partials, M, N, K,
-                                               stream);
+    launch_prefill_t<128, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -599,28 +625,41 @@ SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k) {
 }
 
 template <int NT, int W, bool PARTIALS, int AQ>
-void launch_skinny_nw(const int8_t* xq, const float* xs, const void* xr, const float* gmax, const uint8_t* wpack,
-                      const uint32_t* wmeta, const void* bias, int bias_dtype, void* y, int y_dtype,
-                      int32_t* partials, int M, int N, int K, hipStream_t stream) {
+void launch_skinny_nw(pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* partials, int M, int K,
+                      hipStream_t stream) {
   constexpr int U = W >= 16 ? 4 : 8;
-  const unsigned grid = static_cast<unsigned>((N / 16) / NT);
+  grp.first[0] = 0;
+  for (int i = 0; i < grp.count; ++i) grp.first[i + 1] = grp.first[i] + grp.mem[i].n / 16 / NT;
+  const unsigned grid = static_cast<unsigned>(grp.first[grp.count]);
   const size_t lds = AQ != 0 ? static_cast<size_t>(M) * (K + 16) : 0;
-  gemm_skinny<NT, W, U, PARTIALS, AQ><<<grid, W * 64, lds, stream>>>(xq, xs, xr, gmax, wpack, wmeta, bias, bias_dtype,
-                                                                     y, y_dtype, partials, M, N, K);
+  gemm_skinny<NT, W, U, PARTIALS, AQ><<<grid, W * 64, lds, stream>>>(grp, bias_dtype, y_dtype, partials, M, K);
 }
 
 template <bool PARTIALS, int AQ>
-void launch_skinny(const SkinnyCfg& cfg, const int8_t* xq, const float* xs, const void* xr, const float* gmax,
-                   const uint8_t* wpack, const uint32_t* wmeta, const void* bias, int bias_dtype, void* y, int y_dtype,
-                   int32_t* partials, int M, int N, int K, hipStream_t stream) {
-#define PQ_SKINNY(NT_, W_)                                                                                      \
-  if (cfg.nt == NT_ && cfg.w == W_) {                                                                           \
-    launch_skinny_nw<NT_, W_, PARTIALS, AQ>(xq, xs, xr, gmax, wpack, wmeta, bias, bias_dtype, y, y_dtype, partials, \
-                                            M, N, K, stream);                                                   \
-    return;                                                                                                     \
+void launch_skinny(const SkinnyCfg& cfg, const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32_t* partials,
+                   int M, int K, hipStream_t stream) {
+#define PQ_SKINNY(NT_, W_)                                                                             \
+  if (cfg.nt == NT_ && cfg.w == W_) {                                                                  \
+    launch_skinny_nw<NT_, W_, PARTIALS, AQ>(grp, bias_dtype, y_dtype, partials, M, K, stream);         \
+    return;                                                                                            \
   }
   PQ_SKINNY(1, 4) PQ_SKINNY(1, 8) PQ_SKINNY(1, 16) PQ_SKINNY(2, 4) PQ_SKINNY(2, 8) PQ_SKINNY(2, 16)
 #undef PQ_SKINNY
+}
+
+// The decode GEMM's configuration for a group: the workgroup count is the
+// sum over members; two tiles per workgroup only when every member's tile
+// count is even.
+SkinnyCfg choose_skinny_group(const pq::GemmGroup& grp, int64_t m, int64_t k) {
+  int64_t n = 0;
+  bool even = true;
+  for (int i = 0; i < grp.count; ++i) {
+    n += grp.mem[i].n;
+    even = even && (grp.mem[i].n / 16) % 2 == 0;
+  }
+  SkinnyCfg cfg = choose_skinny(m, n, k);
+  if (!even) cfg.nt = 1;
+  return cfg;
 }
 
 int check_gemm_args(const char* who, int64_t m, int64_t n, int64_t k, int group_size) {
@@ -643,17 +682,19 @@ bool gemm_rotated_supported(int64_t m, int64_t k) {
   return m >= 1 && m <= kSkinnyRows && k % 128 == 0 && k <= 16384 && m * (k + 16) <= 80 * 1024;
 }
 
-void launch_gemm_rotated(const void* xr, bool xr_fp16, const float* gmax, const uint8_t* wpack, const uint32_t* wmeta,
-                         const void* bias, int bias_dtype, void* y, int y_dtype, int m, int n, int k,
-                         hipStream_t stream) {
-  SkinnyCfg cfg = choose_skinny(m, n, k);
+void launch_gemm_group(GemmGroup grp, int aq, int bias_dtype, int y_dtype, int m, int k, hipStream_t stream) {
+  if (aq == 0 && m > kSkinnyMaxM) {
+    launch_prefill<false>(grp, bias_dtype, y_dtype, nullptr, m, k, stream);
+    return;
+  }
+  SkinnyCfg cfg = choose_skinny_group(grp, m, k);
+  if (aq == 0) {
+    launch_skinny<false, 0>(cfg, grp, bias_dtype, y_dtype, nullptr, m, k, stream);
+    return;
+  }
   if (cfg.w == 16) cfg.nt = 1;   // two tiles x 16 waves would spill next to the prologue
-  if (xr_fp16)
-    launch_skinny<false, 1>(cfg, nullptr, nullptr, xr, gmax, wpack, wmeta, bias, bias_dtype, y, y_dtype, nullptr, m,
-                            n, k, stream);
-  else
-    launch_skinny<false, 2>(cfg, nullptr, nullptr, xr, gmax, wpack, wmeta, bias, bias_dtype, y, y_dtype, nullptr, m,
-                            n, k, stream);
+  if (aq == 1) launch_skinny<false, 1>(cfg, grp, bias_dtype, y_dtype, nullptr, m, k, stream);
+  else launch_skinny<false, 2>(cfg, grp, bias_dtype, y_dtype, nullptr, m, k, stream);
 }
 }  // namespace pq
 
@@ -677,15 +718,12 @@ extern "C" int pq_w4a8_gemm(const int8_t* xq, const float* xscale, const uint8_t
   PQ_REQUIRE(pq::aligned_to(xq, 16) && pq::aligned_to(wpack, 16) && pq::aligned_to(wmeta, 4) &&
                  pq::aligned_to(y, pq::dtype_size(y_dtype)),
              PQ_ERR_ARG, "pq_w4a8_gemm: xq and wpack must be 16-byte aligned");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int M = static_cast<int>(m), N = static_cast<int>(n), K = static_cast<int>(k);
-  if (m <= kSkinnyMaxM) {
-    (void)workspace, (void)workspace_bytes;
-    launch_skinny<false, 0>(choose_skinny(m, n, k), xq, xscale, nullptr, nullptr, wpack, wmeta, bias, bias_dtype, y, y_dtype, nullptr, M,
-                         N, K, s);
-  } else {
-    launch_prefill<false>(xq, xscale, wpack, wmeta, bias, bias_dtype, y, y_dtype, nullptr, M, N, K, s);
-  }
+  (void)workspace, (void)workspace_bytes;
+  pq::GemmGroup grp{};
+  grp.count = 1;
+  grp.mem[0] = {xq, xscale, nullptr, nullptr, wpack, wmeta, bias, y, static_cast<int>(n)};
+  pq::launch_gemm_group(grp, 0, bias_dtype, y_dtype, static_cast<int>(m), static_cast<int>(k),
+                        static_cast<hipStream_t>(stream));
   return pq::launch_status("pq_w4a8_gemm launch");
 }
 
@@ -700,12 +738,11 @@ extern "C" int pq_w4a8_gemm_partials(const int8_t* xq, const uint8_t* wpack, con
                  pq::aligned_to(partials, 4),
              PQ_ERR_ARG, "pq_w4a8_gemm_partials: misaligned pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int M = static_cast<int>(m), N = static_cast<int>(n), K = static_cast<int>(k);
-  if (m <= kSkinnyMaxM) {
-    launch_skinny<true, 0>(choose_skinny(m, n, k), xq, nullptr, nullptr, nullptr, wpack, wmeta, nullptr, 0, nullptr, 0, partials, M, N,
-                        K, s);
-  } else {
-    launch_prefill<true>(xq, nullptr, wpack, wmeta, nullptr, 0, nullptr, 0, partials, M, N, K, s);
-  }
+  const int M = static_cast<int>(m), K = static_cast<int>(k);
+  pq::GemmGroup grp{};
+  grp.count = 1;
+  grp.mem[0] = {xq, nullptr, nullptr, nullptr, wpack, wmeta, nullptr, nullptr, static_cast<int>(n)};
+  if (m <= kSkinnyMaxM) launch_skinny<true, 0>(choose_skinny(m, n, k), grp, 0, 0, partials, M, K, s);
+  else launch_prefill<true>(grp, 0, 0, partials, M, K, s);
   return pq::launch_status("pq_w4a8_gemm_partials launch");
 }

@@ -8,23 +8,69 @@
 
 namespace pq {
 
+// Linears that share one input run as a group: one rotation launch and one
+// GEMM launch over the members' concatenated output columns.
+constexpr int kMaxGroup = 4;
+
+// One member of a GEMM group: its A operand (int8 rows xq + token scales xs,
+// or rotated rows xr + per-group maxima gmax), its packed weights, its bias
+// and its output y [m][n].
+struct GemmMember {
+  const int8_t* xq;
+  const float* xs;
+  const void* xr;
+  const float* gmax;
+  const uint8_t* wpack;
+  const uint32_t* wmeta;
+  const void* bias;
+  void* y;
+  int n;
+};
+struct GemmGroup {
+  GemmMember mem[kMaxGroup];
+  int count;
+  int first[kMaxGroup + 1];   // first workgroup tile of each member; set by the launchers
+};
+
+// One member of a rotation group (grid.y = member): its rotation operands,
+// its outputs -- out / out_scale = xr / gmax for the split rotation, xq /
+// xscale for the row rotate+quant -- and an optional fp16 copy of the
+// rotated rows (xrot, row kernel only).
+struct RotMember {
+  const uint32_t* rot_idx;
+  const float* rot_cs;
+  const float* scales;
+  void* out;
+  float* out_scale;
+  void* xrot;
+};
+struct RotGroup {
+  RotMember mem[kMaxGroup];
+  int count;
+};
+
 // Rows per launch of the split rotation (and rows the rotated GEMM accepts).
 constexpr int kSplitMaxRows = 16;
 
-// Rotation of m <= kSplitMaxRows rows with one wave per 128-channel group:
-// xr [m][h] rotated values (fp16 when flags has PQ_RQ_MATERIALIZE_FP16, else
-// fp32) and gmax [m][h/128] the absmax of each row's group.
-PQ_HIDDEN void launch_rotate_split(const void* x, int x_dtype, const uint32_t* rot_idx, const float* rot_cs,
-                                   const float* scales, void* xr, float* gmax, int m, int h, int krot, unsigned flags,
-                                   hipStream_t stream);
+// Rotation of m <= kSplitMaxRows rows with one wave per 128-channel group,
+// for every member of the group: xr [m][h] rotated values (fp16 when flags
+// has PQ_RQ_MATERIALIZE_FP16, else fp32) and gmax [m][h/128] the absmax of
+// each row's group.
+PQ_HIDDEN void launch_rotate_split(const void* x, int x_dtype, const RotGroup& grp, int m, int h, int krot,
+                                   unsigned flags, hipStream_t stream);
+// Rotation + per-token int8 quant of whole rows for every member of the group.
+PQ_HIDDEN void launch_rotate_quant_group(const void* x, int x_dtype, const RotGroup& grp, int64_t rows, int h,
+                                         int krot, unsigned flags, hipStream_t stream);
 
 // Decode GEMM whose A operand is quantized in the kernel from launch_rotate_split's
 // output: token scale = max over the row's gmax / 127.  Returns false when m or
 // the LDS image of A (m x (k + 16) bytes) is out of range.
 PQ_HIDDEN bool gemm_rotated_supported(int64_t m, int64_t k);
-PQ_HIDDEN void launch_gemm_rotated(const void* xr, bool xr_fp16, const float* gmax, const uint8_t* wpack,
-                                   const uint32_t* wmeta, const void* bias, int bias_dtype, void* y, int y_dtype,
-                                   int m, int n, int k, hipStream_t stream);
+// The GEMM of a group (count >= 1 members, same m and k).  aq selects the A
+// operand: 0 = xq/xs (any m), 1 / 2 = fp16 / fp32 xr plus gmax quantized in
+// the kernel (gemm_rotated_supported(m, k)).
+PQ_HIDDEN void launch_gemm_group(GemmGroup grp, int aq, int bias_dtype, int y_dtype, int m, int k,
+                                 hipStream_t stream);
 
 }  // namespace pq
 

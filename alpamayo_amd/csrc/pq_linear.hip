@@ -33,58 +33,110 @@ bool use_split(int64_t m, int64_t k) { return m * k <= 12288 && pq::gemm_rotated
 
 size_t split_xr_bytes(int64_t m, int64_t k) { return align_up(static_cast<size_t>(m) * k * sizeof(float), 256); }
 
+// Workspace of a group of `count` linears: the members' per-row data back
+// to back -- decode: count x align256(4*m*k) of rotated rows, then count x
+// 4*m*(k/128) of group maxima; rows path: count x align256(m*k) of int8
+// activations, then count x 4*m of token scales.
+size_t group_workspace_size(int64_t m, int64_t k, int count) {
+  if (m <= 0 || k <= 0 || k % 128 || count < 1 || count > pq::kMaxGroup) return 0;
+  if (use_split(m, k)) return count * (split_xr_bytes(m, k) + static_cast<size_t>(m) * (k / 128) * sizeof(float));
+  return count * (align_up(static_cast<size_t>(m) * k, 256) + static_cast<size_t>(m) * sizeof(float));
+}
+
+int linear_group(const char* who, const void* x, int x_dtype, const pq_linear_member* members, int count,
+                 int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot, unsigned flags, void* workspace,
+                 size_t workspace_bytes, hipStream_t s) {
+  PQ_REQUIRE(count >= 1 && count <= pq::kMaxGroup, PQ_ERR_ARG, "%s: count=%d not in 1..%d", who, count,
+             pq::kMaxGroup);
+  PQ_REQUIRE(members != nullptr, PQ_ERR_ARG, "%s: null member table", who);
+  PQ_REQUIRE(m >= 0 && m <= 0x7fffffffLL, PQ_ERR_ARG, "%s: m=%lld", who, (long long)m);
+  PQ_REQUIRE(k > 0 && k % 128 == 0 && k <= 16384, PQ_ERR_ARG,
+             "%s: k=%lld must be a positive multiple of 128, at most 16384", who, (long long)k);
+  PQ_REQUIRE(krot >= 1 && krot <= 16, PQ_ERR_UNSUPPORTED, "%s: krot=%d not in 1..16", who, krot);
+  PQ_REQUIRE(x_dtype == PQ_F32 || x_dtype == PQ_F16 || x_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED,
+             "%s: x dtype code %d", who, x_dtype);
+  PQ_REQUIRE(y_dtype == PQ_F32 || y_dtype == PQ_F16 || y_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED,
+             "%s: y dtype code %d", who, y_dtype);
+  PQ_REQUIRE((flags & ~(PQ_RQ_INPUT_FP16 | PQ_RQ_MATERIALIZE_FP16)) == 0, PQ_ERR_ARG, "%s: unknown flags 0x%x",
+             who, flags);
+  bool any_bias = false;
+  for (int i = 0; i < count; ++i) {
+    const pq_linear_member& mb = members[i];
+    PQ_REQUIRE(mb.n > 0 && mb.n % 16 == 0 && mb.n <= (1 << 20), PQ_ERR_ARG,
+               "%s: member %d: n=%lld must be a positive multiple of 16", who, i, (long long)mb.n);
+    PQ_REQUIRE(mb.n * k / 2 < (int64_t(1) << 31), PQ_ERR_ARG, "%s: member %d: n*k/2 must stay below 2^31", who, i);
+    any_bias = any_bias || mb.bias != nullptr;
+  }
+  PQ_REQUIRE(!any_bias || bias_dtype == PQ_F32 || bias_dtype == PQ_F16 || bias_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED,
+             "%s: bias dtype code %d", who, bias_dtype);
+  if (m == 0) return PQ_OK;
+  PQ_REQUIRE(m * k < (int64_t(1) << 31), PQ_ERR_ARG, "%s: m*k=%lld must stay below 2^31", who, (long long)(m * k));
+  PQ_REQUIRE(x && pq::aligned_to(x, 16), PQ_ERR_ARG, "%s: x must be non-null and 16-byte aligned", who);
+  for (int i = 0; i < count; ++i) {
+    const pq_linear_member& mb = members[i];
+    PQ_REQUIRE(mb.rot_idx && mb.rot_cs && mb.wpack && mb.wmeta && mb.y, PQ_ERR_ARG, "%s: member %d: null pointer",
+               who, i);
+    PQ_REQUIRE(pq::aligned_to(mb.rot_idx, 16) && pq::aligned_to(mb.rot_cs, 16) && pq::aligned_to(mb.wpack, 16) &&
+                   pq::aligned_to(mb.wmeta, 4) && pq::aligned_to(mb.y, pq::dtype_size(y_dtype)),
+               PQ_ERR_ARG, "%s: member %d: misaligned pointer", who, i);
+  }
+  const size_t need = group_workspace_size(m, k, count);
+  PQ_REQUIRE(workspace != nullptr && workspace_bytes >= need && pq::aligned_to(workspace, 256), PQ_ERR_WORKSPACE,
+             "%s: a 256-byte aligned workspace of %zu bytes is needed for m=%lld k=%lld count=%d, got %zu", who,
+             need, (long long)m, (long long)k, count, workspace ? workspace_bytes : (size_t)0);
+
+  const int M = static_cast<int>(m), K = static_cast<int>(k);
+  char* ws = static_cast<char*>(workspace);
+  pq::RotGroup rg{};
+  pq::GemmGroup gg{};
+  rg.count = gg.count = count;
+  const bool split = use_split(m, k);
+  const size_t a_bytes = split ? split_xr_bytes(m, k) : align_up(static_cast<size_t>(m) * k, 256);
+  const size_t s_bytes = split ? static_cast<size_t>(m) * (k / 128) * sizeof(float) : static_cast<size_t>(m) * 4;
+  for (int i = 0; i < count; ++i) {
+    const pq_linear_member& mb = members[i];
+    void* a = ws + i * a_bytes;
+    float* sc = reinterpret_cast<float*>(ws + count * a_bytes + i * s_bytes);
+    rg.mem[i] = {mb.rot_idx, mb.rot_cs, mb.scales, a, sc, nullptr};
+    if (split)
+      gg.mem[i] = {nullptr, nullptr, a, sc, mb.wpack, mb.wmeta, mb.bias, mb.y, static_cast<int>(mb.n)};
+    else
+      gg.mem[i] = {static_cast<const int8_t*>(a), sc, nullptr, nullptr, mb.wpack, mb.wmeta, mb.bias, mb.y,
+                   static_cast<int>(mb.n)};
+  }
+  if (split) pq::launch_rotate_split(x, x_dtype, rg, M, K, krot, flags, s);
+  else pq::launch_rotate_quant_group(x, x_dtype, rg, m, K, krot, flags, s);
+  int st = pq::launch_status(split ? "linear rotation launch" : "linear rotate+quant launch");
+  if (st != PQ_OK) return st;
+  const int aq = split ? ((flags & PQ_RQ_MATERIALIZE_FP16) ? 1 : 2) : 0;
+  pq::launch_gemm_group(gg, aq, bias_dtype, y_dtype, M, K, s);
+  return pq::launch_status("linear GEMM launch");
+}
+
 }  // namespace
 
 extern "C" size_t pq_w4a8_linear_workspace_size(int64_t m, int64_t n, int64_t k, int krot) {
   (void)krot;
-  if (m <= 0 || n <= 0 || k <= 0 || k % 128 || n % 16) return 0;
-  if (use_split(m, k)) return split_xr_bytes(m, k) + static_cast<size_t>(m) * (k / 128) * sizeof(float);
-  return align_up(static_cast<size_t>(m) * k, 256) + static_cast<size_t>(m) * sizeof(float);
+  if (n <= 0 || n % 16) return 0;
+  return group_workspace_size(m, k, 1);
+}
+
+extern "C" size_t pq_w4a8_linear_group_workspace_size(int64_t m, int64_t k, int count) {
+  return group_workspace_size(m, k, count);
 }
 
 extern "C" int pq_w4a8_linear(const void* x, int x_dtype, const uint32_t* rot_idx, const float* rot_cs,
                               const float* scales, const uint8_t* wpack, const uint32_t* wmeta, const void* bias,
                               int bias_dtype, void* y, int y_dtype, int64_t m, int64_t n, int64_t k, int krot,
                               unsigned flags, void* workspace, size_t workspace_bytes, void* stream) {
-  PQ_REQUIRE(m >= 0 && m <= 0x7fffffffLL, PQ_ERR_ARG, "pq_w4a8_linear: m=%lld", (long long)m);
-  PQ_REQUIRE(n > 0 && n % 16 == 0 && n <= (1 << 20), PQ_ERR_ARG, "pq_w4a8_linear: n=%lld must be a positive multiple of 16",
-             (long long)n);
-  PQ_REQUIRE(k > 0 && k % 128 == 0 && k <= 16384, PQ_ERR_ARG,
-             "pq_w4a8_linear: k=%lld must be a positive multiple of 128, at most 16384", (long long)k);
-  PQ_REQUIRE(krot >= 1 && krot <= 16, PQ_ERR_UNSUPPORTED, "pq_w4a8_linear: krot=%d not in 1..16", krot);
-  PQ_REQUIRE(x_dtype == PQ_F32 || x_dtype == PQ_F16 || x_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED,
-             "pq_w4a8_linear: x dtype code %d", x_dtype);
-  PQ_REQUIRE(y_dtype == PQ_F32 || y_dtype == PQ_F16 || y_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED,
-             "pq_w4a8_linear: y dtype code %d", y_dtype);
-  PQ_REQUIRE(bias == nullptr || bias_dtype == PQ_F32 || bias_dtype == PQ_F16 || bias_dtype == PQ_BF16,
-             PQ_ERR_UNSUPPORTED, "pq_w4a8_linear: bias dtype code %d", bias_dtype);
-  PQ_REQUIRE((flags & ~(PQ_RQ_INPUT_FP16 | PQ_RQ_MATERIALIZE_FP16)) == 0, PQ_ERR_ARG,
-             "pq_w4a8_linear: unknown flags 0x%x", flags);
-  if (m == 0) return PQ_OK;
-  PQ_REQUIRE(x && rot_idx && rot_cs && wpack && wmeta && y, PQ_ERR_ARG, "pq_w4a8_linear: null pointer");
-  PQ_REQUIRE(pq::aligned_to(x, 16) && pq::aligned_to(rot_idx, 16) && pq::aligned_to(rot_cs, 16) && pq::aligned_to(wpack, 16) &&
-                 pq::aligned_to(wmeta, 4) && pq::aligned_to(y, pq::dtype_size(y_dtype)),
-             PQ_ERR_ARG, "pq_w4a8_linear: misaligned pointer");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool split = use_split(m, k);
-  const size_t need = pq_w4a8_linear_workspace_size(m, n, k, krot);
-  PQ_REQUIRE(workspace != nullptr && workspace_bytes >= need && pq::aligned_to(workspace, 256), PQ_ERR_WORKSPACE,
-             "pq_w4a8_linear: a 256-byte aligned workspace of %zu bytes is needed for m=%lld k=%lld, got %zu", need,
-             (long long)m, (long long)k, workspace ? workspace_bytes : (size_t)0);
-  if (split) {
-    const bool mat16 = (flags & PQ_RQ_MATERIALIZE_FP16) != 0;
-    void* xr = workspace;
-    float* gmax = reinterpret_cast<float*>(static_cast<char*>(workspace) + split_xr_bytes(m, k));
-    const int M = static_cast<int>(m), N = static_cast<int>(n), K = static_cast<int>(k);
-    pq::launch_rotate_split(x, x_dtype, rot_idx, rot_cs, scales, xr, gmax, M, K, krot, flags, s);
-    int st = pq::launch_status("pq_w4a8_linear rotation launch");
-    if (st != PQ_OK) return st;
-    pq::launch_gemm_rotated(xr, mat16, gmax, wpack, wmeta, bias, bias_dtype, y, y_dtype, M, N, K, s);
-    return pq::launch_status("pq_w4a8_linear GEMM launch");
-  }
-  int8_t* xq = static_cast<int8_t*>(workspace);
-  float* xs = reinterpret_cast<float*>(static_cast<char*>(workspace) + align_up(static_cast<size_t>(m) * k, 256));
-  int st = pq_rotate_quant_i8(x, x_dtype, rot_idx, rot_cs, scales, xq, xs, nullptr, m, k, krot, flags, stream);
-  if (st != PQ_OK) return st;
-  return pq_w4a8_gemm(xq, xs, wpack, wmeta, bias, bias_dtype, y, y_dtype, m, n, k, 128, nullptr, 0, stream);
+  const pq_linear_member one = {rot_idx, rot_cs, scales, wpack, wmeta, bias, y, n};
+  return linear_group("pq_w4a8_linear", x, x_dtype, &one, 1, bias_dtype, y_dtype, m, k, krot, flags, workspace,
+                      workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pq_w4a8_linear_group(const void* x, int x_dtype, const pq_linear_member* members, int count,
+                                    int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot, unsigned flags,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  return linear_group("pq_w4a8_linear_group", x, x_dtype, members, count, bias_dtype, y_dtype, m, k, krot, flags,
+                      workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }

@@ -147,10 +147,16 @@ __device__ __forceinline__ void load8(const void* base, int64_t elem, float f[8]
 constexpr int kRQWaves = 8;
 
 template <int DT, int KP, bool MAT16, int RB>
-__global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(
-    const void* __restrict__ x, const uint32_t* __restrict__ rot_idx, const float* __restrict__ rot_cs,
-    const float* __restrict__ scales, int8_t* __restrict__ xq, float* __restrict__ xscale,
-    uint16_t* __restrict__ xrot, int64_t row_begin, int h, int krot, unsigned flags) {
+__global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void* __restrict__ x,
+                                                                       const pq::RotGroup grp, int64_t row_begin,
+                                                                       int h, int krot, unsigned flags) {
+  const pq::RotMember& mb = grp.mem[blockIdx.y];
+  const uint32_t* __restrict__ rot_idx = mb.rot_idx;
+  const float* __restrict__ rot_cs = mb.rot_cs;
+  const float* __restrict__ scales = mb.scales;
+  int8_t* __restrict__ xq = static_cast<int8_t*>(mb.out);
+  float* __restrict__ xscale = mb.out_scale;
+  uint16_t* __restrict__ xrot = static_cast<uint16_t*>(mb.xrot);
   extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
   __shared__ float red[kRQWaves][RB];
   using RowT = typename std::conditional<MAT16, uint16_t, float>::type;
@@ -292,40 +298,39 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(
 constexpr int kSplitWaves = 4;
 
 template <int DT, int KP, bool MAT16, int MR>
-__global__ __launch_bounds__(kSplitWaves * 64) void rotate_split_kernel(
-    const void* __restrict__ x, const uint32_t* __restrict__ rot_idx, const float* __restrict__ rot_cs,
-    const float* __restrict__ scales, void* __restrict__ xr, float* __restrict__ gmax, int M, int h, int krot,
-    unsigned flags) {
+__global__ __launch_bounds__(kSplitWaves * 64) void rotate_split_kernel(const void* __restrict__ x,
+                                                                         const pq::RotGroup grp, int M, int h,
+                                                                         int krot, unsigned flags) {
   const int g = blockIdx.x * kSplitWaves + (threadIdx.x >> 6);
   if (g >= (h >> 7)) return;   // whole waves only; this kernel has no barrier
-  pqd::rotate_group_rows<DT, KP, MAT16, MR>(x, rot_idx, rot_cs, scales, xr, gmax, M, h, krot, flags, g,
-                                            threadIdx.x & 63);
+  const pq::RotMember& mb = grp.mem[blockIdx.y];
+  pqd::rotate_group_rows<DT, KP, MAT16, MR>(x, mb.rot_idx, mb.rot_cs, mb.scales, mb.out, mb.out_scale, M, h, krot,
+                                            flags, g, threadIdx.x & 63);
 }
 
 template <int DT, int KP, bool MAT16>
-void launch_split_kp(const void* x, const uint32_t* rot_idx, const float* rot_cs, const float* scales, void* xr,
-                     float* gmax, int M, int h, int krot, unsigned flags, hipStream_t stream) {
-  const unsigned grid = static_cast<unsigned>((h / 128 + kSplitWaves - 1) / kSplitWaves);
-#define PQ_SPLIT(MR_)                                                                                            \
-  if (M <= MR_) {                                                                                                \
-    rotate_split_kernel<DT, KP, MAT16, MR_><<<grid, kSplitWaves * 64, 0, stream>>>(x, rot_idx, rot_cs, scales, xr, \
-                                                                                   gmax, M, h, krot, flags);    \
-    return;                                                                                                      \
+void launch_split_kp(const void* x, const pq::RotGroup& grp, int M, int h, int krot, unsigned flags,
+                     hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>((h / 128 + kSplitWaves - 1) / kSplitWaves), static_cast<unsigned>(grp.count));
+#define PQ_SPLIT(MR_)                                                                                    \
+  if (M <= MR_) {                                                                                        \
+    rotate_split_kernel<DT, KP, MAT16, MR_><<<grid, kSplitWaves * 64, 0, stream>>>(x, grp, M, h, krot, flags); \
+    return;                                                                                              \
   }
   PQ_SPLIT(1) PQ_SPLIT(2) PQ_SPLIT(4) PQ_SPLIT(8) PQ_SPLIT(16)
 #undef PQ_SPLIT
 }
 
 template <int DT>
-void launch_split_dt(const void* x, const uint32_t* rot_idx, const float* rot_cs, const float* scales, void* xr,
-                     float* gmax, int M, int h, int krot, unsigned flags, hipStream_t stream) {
+void launch_split_dt(const void* x, const pq::RotGroup& grp, int M, int h, int krot, unsigned flags,
+                     hipStream_t stream) {
   const bool mat16 = (flags & PQ_RQ_MATERIALIZE_FP16) != 0;
   if (krot <= 8) {
-    if (mat16) launch_split_kp<DT, 8, true>(x, rot_idx, rot_cs, scales, xr, gmax, M, h, krot, flags, stream);
-    else launch_split_kp<DT, 8, false>(x, rot_idx, rot_cs, scales, xr, gmax, M, h, krot, flags, stream);
+    if (mat16) launch_split_kp<DT, 8, true>(x, grp, M, h, krot, flags, stream);
+    else launch_split_kp<DT, 8, false>(x, grp, M, h, krot, flags, stream);
   } else {
-    if (mat16) launch_split_kp<DT, 16, true>(x, rot_idx, rot_cs, scales, xr, gmax, M, h, krot, flags, stream);
-    else launch_split_kp<DT, 16, false>(x, rot_idx, rot_cs, scales, xr, gmax, M, h, krot, flags, stream);
+    if (mat16) launch_split_kp<DT, 16, true>(x, grp, M, h, krot, flags, stream);
+    else launch_split_kp<DT, 16, false>(x, grp, M, h, krot, flags, stream);
   }
 }
 
@@ -389,42 +394,39 @@ inline int rq_rows_per_block(int64_t rows, int h, bool mat16) {
 }
 
 template <int DT, int KP, bool MAT16, int RB>
-void launch_rq_rb(const void* x, const uint32_t* rot_idx, const float* rot_cs, const float* scales, int8_t* xq,
-                  float* xscale, void* xrot, int64_t row_begin, int64_t nblocks, int h, int krot, unsigned flags,
-                  hipStream_t stream) {
+void launch_rq_rb(const void* x, const pq::RotGroup& grp, int64_t row_begin, int64_t nblocks, int h, int krot,
+                  unsigned flags, hipStream_t stream) {
   if (nblocks <= 0) return;
   const size_t lds = static_cast<size_t>(RB) * h * (MAT16 ? 2 : 4);
-  rotate_quant_kernel<DT, KP, MAT16, RB><<<static_cast<unsigned>(nblocks), kRQWaves * 64, lds, stream>>>(
-      x, rot_idx, rot_cs, scales, xq, xscale, static_cast<uint16_t*>(xrot), row_begin, h, krot, flags);
+  const dim3 grid(static_cast<unsigned>(nblocks), static_cast<unsigned>(grp.count));
+  rotate_quant_kernel<DT, KP, MAT16, RB><<<grid, kRQWaves * 64, lds, stream>>>(x, grp, row_begin, h, krot, flags);
 }
 
 template <int DT, int KP, bool MAT16>
-void launch_rq(const void* x, const uint32_t* rot_idx, const float* rot_cs, const float* scales, int8_t* xq,
-               float* xscale, void* xrot, int64_t rows, int h, int krot, unsigned flags, hipStream_t stream) {
+void launch_rq(const void* x, const pq::RotGroup& grp, int64_t rows, int h, int krot, unsigned flags,
+               hipStream_t stream) {
   const int rb = rq_rows_per_block(rows, h, MAT16);
   const int64_t full = rows / rb;
   switch (rb) {
-    case 8: launch_rq_rb<DT, KP, MAT16, 8>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, 0, full, h, krot, flags, stream); break;
-    case 4: launch_rq_rb<DT, KP, MAT16, 4>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, 0, full, h, krot, flags, stream); break;
-    case 2: launch_rq_rb<DT, KP, MAT16, 2>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, 0, full, h, krot, flags, stream); break;
+    case 8: launch_rq_rb<DT, KP, MAT16, 8>(x, grp, 0, full, h, krot, flags, stream); break;
+    case 4: launch_rq_rb<DT, KP, MAT16, 4>(x, grp, 0, full, h, krot, flags, stream); break;
+    case 2: launch_rq_rb<DT, KP, MAT16, 2>(x, grp, 0, full, h, krot, flags, stream); break;
     default: break;
   }
   const int64_t done = rb > 1 ? full * rb : 0;   // the remaining rows, one block each
-  launch_rq_rb<DT, KP, MAT16, 1>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, done, rows - done, h, krot, flags,
-                                 stream);
+  launch_rq_rb<DT, KP, MAT16, 1>(x, grp, done, rows - done, h, krot, flags, stream);
 }
 
 template <int DT>
-void launch_rotate_quant(const void* x, const uint32_t* rot_idx, const float* rot_cs, const float* scales, int8_t* xq,
-                         float* xscale, void* xrot, int64_t rows, int h, int krot, unsigned flags,
+void launch_rotate_quant(const void* x, const pq::RotGroup& grp, int64_t rows, int h, int krot, unsigned flags,
                          hipStream_t stream) {
   const bool mat16 = (flags & PQ_RQ_MATERIALIZE_FP16) != 0;
   if (krot <= 8) {
-    if (mat16) launch_rq<DT, 8, true>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
-    else launch_rq<DT, 8, false>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
+    if (mat16) launch_rq<DT, 8, true>(x, grp, rows, h, krot, flags, stream);
+    else launch_rq<DT, 8, false>(x, grp, rows, h, krot, flags, stream);
   } else {
-    if (mat16) launch_rq<DT, 16, true>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
-    else launch_rq<DT, 16, false>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, rows, h, krot, flags, stream);
+    if (mat16) launch_rq<DT, 16, true>(x, grp, rows, h, krot, flags, stream);
+    else launch_rq<DT, 16, false>(x, grp, rows, h, krot, flags, stream);
   }
 }
 
@@ -437,13 +439,21 @@ void launch_quant(const void* x, int8_t* xq, float* xscale, int64_t rows, int h,
 }  // namespace
 
 namespace pq {
-void launch_rotate_split(const void* x, int x_dtype, const uint32_t* rot_idx, const float* rot_cs,
-                         const float* scales, void* xr, float* gmax, int m, int h, int krot, unsigned flags,
+void launch_rotate_split(const void* x, int x_dtype, const RotGroup& grp, int m, int h, int krot, unsigned flags,
                          hipStream_t stream) {
   switch (x_dtype) {
-    case PQ_F32: launch_split_dt<PQ_F32>(x, rot_idx, rot_cs, scales, xr, gmax, m, h, krot, flags, stream); break;
-    case PQ_F16: launch_split_dt<PQ_F16>(x, rot_idx, rot_cs, scales, xr, gmax, m, h, krot, flags, stream); break;
-    default: launch_split_dt<PQ_BF16>(x, rot_idx, rot_cs, scales, xr, gmax, m, h, krot, flags, stream); break;
+    case PQ_F32: launch_split_dt<PQ_F32>(x, grp, m, h, krot, flags, stream); break;
+    case PQ_F16: launch_split_dt<PQ_F16>(x, grp, m, h, krot, flags, stream); break;
+    default: launch_split_dt<PQ_BF16>(x, grp, m, h, krot, flags, stream); break;
+  }
+}
+
+void launch_rotate_quant_group(const void* x, int x_dtype, const RotGroup& grp, int64_t rows, int h, int krot,
+                               unsigned flags, hipStream_t stream) {
+  switch (x_dtype) {
+    case PQ_F32: launch_rotate_quant<PQ_F32>(x, grp, rows, h, krot, flags, stream); break;
+    case PQ_F16: launch_rotate_quant<PQ_F16>(x, grp, rows, h, krot, flags, stream); break;
+    default: launch_rotate_quant<PQ_BF16>(x, grp, rows, h, krot, flags, stream); break;
   }
 }
 }  // namespace pq
@@ -490,13 +500,11 @@ extern "C" int pq_rotate_quant_i8(const void* x, int x_dtype, const uint32_t* ro
                  pq::aligned_to(rot_cs, 16) && (xrot == nullptr || pq::aligned_to(xrot, 16)),
              PQ_ERR_ARG,
              "pq_rotate_quant_i8: x, rot_idx, rot_cs and xrot must be 16-byte aligned, xq 8-byte aligned");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int hh = static_cast<int>(h);
-  switch (x_dtype) {
-    case PQ_F32: launch_rotate_quant<PQ_F32>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
-    case PQ_F16: launch_rotate_quant<PQ_F16>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
-    default: launch_rotate_quant<PQ_BF16>(x, rot_idx, rot_cs, scales, xq, xscale, xrot, rows, hh, krot, flags, s); break;
-  }
+  pq::RotGroup grp{};
+  grp.count = 1;
+  grp.mem[0] = {rot_idx, rot_cs, scales, xq, xscale, xrot};
+  pq::launch_rotate_quant_group(x, x_dtype, grp, rows, static_cast<int>(h), krot, flags,
+                                static_cast<hipStream_t>(stream));
   return pq::launch_status("pq_rotate_quant_i8 launch");
 }
 

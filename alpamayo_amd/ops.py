@@ -13,6 +13,9 @@ the ``paroquant`` namespace:
   paroquant::w4a8_prepack(awq_qweight, awq_scales, awq_qzeros) -> (wpack, wmeta)
   paroquant::w4a8_linear(x, rot_idx, rot_cs, scales?, krot, wpack, wmeta, bias?, workspace?,
                          input_fp16, materialize_fp16, out_dtype) -> y
+  paroquant::w4a8_linear_group(x, rot_idx[], rot_cs[], scales?[], krot, wpack[], wmeta[], bias?[],
+                               workspace?, input_fp16, materialize_fp16, out_dtype) -> y[]
+      (1..4 linears sharing the input x, in two launches for the whole group)
 
 ``pack_rotation`` (host) turns Rotation's pairs/angles into rot_idx/rot_cs.
 
@@ -47,6 +50,9 @@ _pq_lib.define("w4a8_prepack(Tensor awq_qweight, Tensor awq_scales, Tensor awq_q
 _pq_lib.define("w4a8_linear(Tensor x, Tensor rot_idx, Tensor rot_cs, Tensor? scales, int krot, Tensor wpack, "
                "Tensor wmeta, Tensor? bias, Tensor? workspace, bool input_fp16, bool materialize_fp16, "
                "ScalarType out_dtype) -> Tensor")
+_pq_lib.define("w4a8_linear_group(Tensor x, Tensor[] rot_idx, Tensor[] rot_cs, Tensor?[] scales, int krot, "
+               "Tensor[] wpack, Tensor[] wmeta, Tensor?[] bias, Tensor? workspace, bool input_fp16, "
+               "bool materialize_fp16, ScalarType out_dtype) -> Tensor[]")
 
 
 # ---------------------------------------------------------------------------
@@ -426,6 +432,71 @@ def _linear_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace
 
 
 _pq_lib.impl("w4a8_linear", _linear_impl, "CUDA")
+
+
+def _linear_group_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16,
+                       materialize_fp16, out_dtype):
+    dev = x.device
+    count = len(wpack)
+    _require(1 <= count <= _lib.MAX_GROUP, f"a group holds 1..{_lib.MAX_GROUP} linears, got {count}")
+    _require(len(rot_idx) == len(rot_cs) == len(scales) == len(wmeta) == len(bias) == count,
+             "every per-member list must have one entry per linear")
+    _require(out_dtype in _DT, f"out_dtype must be float32/float16/bfloat16, got {out_dtype}")
+    xc = x.contiguous()
+    k = xc.size(-1)
+    m = xc.numel() // k
+    members = (_lib.LinearMember * count)()
+    keep, outs, bias_dt = [], [], 0
+    for i in range(count):
+        n, kw = _check_weights(wpack[i], wmeta[i], dev)
+        _require(kw == k, f"member {i}: the weights expect {kw} features, x has {k}")
+        _check_rot_params(x, rot_idx[i], rot_cs[i], scales[i], krot)
+        idx, cs = rot_idx[i].contiguous(), rot_cs[i].contiguous()
+        sc = scales[i].contiguous() if scales[i] is not None else None
+        b = bias[i]
+        if b is not None:
+            _require(b.dtype in _DT and b.numel() == n, f"member {i}: bias must hold {n} float values")
+            _same_device("bias", b, dev)
+            b = b.contiguous()
+            _require(bias_dt in (0, _DT[b.dtype]), "all biases of a group must share one dtype")
+            bias_dt = _DT[b.dtype]
+        y = torch.empty((m, n), dtype=out_dtype, device=dev)
+        keep += [idx, cs, sc, b]
+        outs.append(y)
+        members[i] = _lib.LinearMember(idx.data_ptr(), cs.data_ptr(), sc.data_ptr() if sc is not None else None,
+                                       wpack[i].data_ptr(), wmeta[i].data_ptr(),
+                                       b.data_ptr() if b is not None else None, y.data_ptr(), n)
+    lib = _lib.load()
+    need = int(lib.pq_w4a8_linear_group_workspace_size(m, k, count))
+    scratch = None
+    if need > 0:
+        if (workspace is not None and workspace.dtype == torch.uint8 and workspace.is_contiguous()
+                and workspace.numel() >= need and workspace.data_ptr() % 256 == 0):
+            _same_device("workspace", workspace, dev)
+            scratch = workspace
+        else:
+            scratch = torch.empty(need, dtype=torch.uint8, device=dev)
+    flags = (_lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0) | (_lib.PQ_RQ_MATERIALIZE_FP16 if materialize_fp16 else 0)
+    with _DeviceGuard(dev):
+        st = lib.pq_w4a8_linear_group(xc.data_ptr(), _DT[x.dtype], members, count, bias_dt, _DT[out_dtype], m, k,
+                                      krot, flags, scratch.data_ptr() if scratch is not None else None,
+                                      scratch.numel() if scratch is not None else 0, _stream(dev))
+    _lib.check(st, "paroquant::w4a8_linear_group")
+    return [y.view(*x.shape[:-1], y.size(1)) for y in outs]
+
+
+_pq_lib.impl("w4a8_linear_group", _linear_group_impl, "CUDA")
+
+
+@torch.library.register_fake("paroquant::w4a8_linear_group")
+def _linear_group_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16,
+                       materialize_fp16, out_dtype):
+    return [x.new_empty((*x.shape[:-1], w.size(0) * 16), dtype=out_dtype) for w in wpack]
+
+
+def linear_group_workspace_bytes(m: int, k: int, count: int) -> int:
+    """Workspace bytes paroquant::w4a8_linear_group needs for count linears over an [m, k] input."""
+    return int(_lib.load().pq_w4a8_linear_group_workspace_size(m, k, count))
 
 
 @torch.library.register_fake("paroquant::w4a8_linear")

@@ -8,6 +8,7 @@ from .paroquant_marlin_w4a8 import (  # noqa: F401
     AWQBuffers,
     BF16RotateLinearWrapper,
     MarlinW4A8Linear,
+    SharedInputRotateLinears,
     convert_model_to_marlin_w4a8,
     convert_wqlinear_layer,
     dequant_awq,

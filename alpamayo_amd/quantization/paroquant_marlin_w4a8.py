@@ -15,6 +15,10 @@ same public names and signatures:
   convert_model_to_marlin_w4a8      (513-529)
   load_paroquant_checkpoint         (the checkpoint part of load_paroquant_model, 462-510)
 
+Added here, with no counterpart in the reference: ``SharedInputRotateLinears``,
+which runs linears that read one activation (q/k/v, gate/up) as one group
+through ``paroquant::w4a8_linear_group``.
+
 What changes underneath: ``load_from_awq`` repacks into this project's
 kernel layout with ``paroquant::w4a8_prepack`` instead of vLLM's Marlin
 repack, and ``forward`` runs ``paroquant::quant_i8`` + ``paroquant::w4a8_gemm``
@@ -81,6 +85,60 @@ class BF16RotateLinearWrapper(nn.Module):
             return super().__getattr__(name)
         except AttributeError:
             return getattr(self.rotate_linear, name)
+
+
+class SharedInputRotateLinears(nn.Module):
+    """Linears that read the same activation -- q/k/v, or gate/up -- run as one group.
+
+    Each member keeps its own rotation and weights; forward(x) returns the
+    members' outputs, equal to calling each member on x.  The group runs
+    paroquant::w4a8_linear_group: one rotation (+ quant) launch for all
+    members and one GEMM launch over their concatenated output columns,
+    where separate calls take two launches per linear.  Members are
+    BF16RotateLinearWrapper or RotateLinearInt4 modules holding a
+    MarlinW4A8Linear, all of one kind, with one in_features and one number
+    of rotation layers.  The reference keeps these linears separate once
+    ParoQuant is loaded (paroquant_marlin_w4a8.py:455-460); its unquantised
+    counterparts are QKVLinear / MergedColumnLinear (patches.py:144-263).
+    """
+
+    def __init__(self, members):
+        super().__init__()
+        members = list(members)
+        if not 1 <= len(members) <= _ops._lib.MAX_GROUP:
+            raise ValueError(f"a group holds 1..{_ops._lib.MAX_GROUP} linears, got {len(members)}")
+        kinds = {type(m) for m in members}
+        if len(kinds) != 1 or not kinds <= {BF16RotateLinearWrapper, RotateLinearInt4}:
+            raise TypeError("members must all be BF16RotateLinearWrapper or all RotateLinearInt4")
+        rls = [m.rotate_linear if isinstance(m, BF16RotateLinearWrapper) else m for m in members]
+        for rl in rls:
+            if not isinstance(rl.qlinear, MarlinW4A8Linear):
+                raise TypeError("every member must hold a MarlinW4A8Linear (convert_model_to_marlin_w4a8)")
+        if len({rl.qlinear.in_features for rl in rls}) != 1 or len({rl.rotation.krot for rl in rls}) != 1:
+            raise ValueError("members must share in_features and the number of rotation layers")
+        self.members = nn.ModuleList(members)
+        self.bf16_inputs = isinstance(members[0], BF16RotateLinearWrapper)
+        self.register_buffer("workspace", torch.empty(0, dtype=torch.uint8), persistent=False)
+
+    def _rotate_linears(self):
+        return [m.rotate_linear if self.bf16_inputs else m for m in self.members]
+
+    def forward(self, x: torch.Tensor):
+        rls = self._rotate_linears()
+        for rl in rls:
+            rl.qlinear._check_loaded()
+            if not rl.rotation.prepared:
+                rl.rotation.prepare()
+        k = x.size(-1)
+        need = _ops.linear_group_workspace_bytes(x.numel() // k, k, len(rls))
+        if self.workspace.numel() < need or self.workspace.device != x.device:
+            self.workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+        outs = torch.ops.paroquant.w4a8_linear_group(
+            x, [rl.rotation.rot_idx for rl in rls], [rl.rotation.rot_cs for rl in rls],
+            [rl.rotation.scales_f32 for rl in rls], rls[0].rotation.krot, [rl.qlinear.qweight for rl in rls],
+            [rl.qlinear.scales for rl in rls], [rl.qlinear.bias for rl in rls], self.workspace, self.bf16_inputs,
+            True, x.dtype)
+        return tuple(outs)
 
 
 def _get_alpamayo_layers(model, target="vlm"):

@@ -155,6 +155,36 @@ int pq_w4a8_linear(const void* x, int x_dtype, const uint32_t* rot_idx, const fl
                    int y_dtype, int64_t m, int64_t n, int64_t k, int krot, unsigned flags, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* One linear of a group that shares its input x (pq_w4a8_linear_group). */
+typedef struct pq_linear_member {
+  const uint32_t* rot_idx; /* this linear's rotation operands (pq_rotation_pack) */
+  const float* rot_cs;
+  const float* scales;     /* channel scales [k] or NULL */
+  const uint8_t* wpack;    /* its weights (pq_w4a8_prepack) */
+  const uint32_t* wmeta;
+  const void* bias;        /* [n] in bias_dtype, or NULL */
+  void* y;                 /* [m, n] in y_dtype */
+  int64_t n;               /* output features, a positive multiple of 16 */
+} pq_linear_member;
+
+/* Bytes of workspace pq_w4a8_linear_group needs for count members sharing an
+ * [m, k] input: count times what pq_w4a8_linear needs for one (it does not
+ * depend on n). */
+size_t pq_w4a8_linear_group_workspace_size(int64_t m, int64_t k, int count);
+
+/* count (1..4) W4A8 linears over the same input x [m, k] (x_dtype), each with
+ * its own rotation and weights: member i writes its y [m, n_i].  Same results
+ * as pq_w4a8_linear per member, in two launches for the whole group -- one
+ * rotation (+ quant) launch and one GEMM over the concatenated columns.
+ * All members share k, krot, flags, bias_dtype and y_dtype.  No counterpart
+ * in the reference, whose ParoQuant loading runs q/k/v and gate/up as
+ * separate linears (paroquant_marlin_w4a8.py:455-460); it replaces, for one
+ * input, the calls BF16RotateLinearWrapper.forward makes per linear
+ * (paroquant_marlin_w4a8.py:59-65). */
+int pq_w4a8_linear_group(const void* x, int x_dtype, const pq_linear_member* members, int count, int bias_dtype,
+                         int y_dtype, int64_t m, int64_t k, int krot, unsigned flags, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

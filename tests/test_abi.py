@@ -85,6 +85,33 @@ def test_linear_argument_checks():
     assert lib.pq_w4a8_linear(*args(64, 4096, 8, 3, ctypes.c_void_p(272), need)) == 4   # not 256-aligned
 
 
+def test_linear_group_argument_checks():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    mem = (_lib.LinearMember * 5)()
+    for i in range(5):
+        mem[i] = _lib.LinearMember(256, 256, None, 256, 256, None, 256, 64)
+    call = lambda members, count, m=2, k=1024: lib.pq_w4a8_linear_group(  # noqa: E731
+        p, 2, members, count, 0, 2, m, k, 8, 3, p, 1 << 20, None)
+    assert call(mem, 0) == 1 and "count" in _err(lib)
+    assert call(mem, 5) == 1
+    assert call(None, 2) == 1 and "member table" in _err(lib)
+    mem[1].n = 40
+    assert call(mem, 2) == 1 and "member 1" in _err(lib)
+    mem[1].n = 64
+    assert call(mem, 2, k=1000) == 1
+    assert call(mem, 2, m=0) == 0                       # empty input: nothing to do
+    mem[0].rot_idx = None
+    assert call(mem, 2) == 1 and "member 0: null pointer" in _err(lib)
+    mem[0].rot_idx = 256
+    assert lib.pq_w4a8_linear_group(p, 2, mem, 2, 0, 2, 2, 1024, 8, 3, p, 16, None) == 4   # workspace too small
+    # the workspace of a group: count times one member's
+    for m, k in ((1, 4096), (3, 4096), (1, 12288), (4, 4096), (300, 2048)):
+        one = lib.pq_w4a8_linear_workspace_size(m, 64, k, 8)
+        assert lib.pq_w4a8_linear_group_workspace_size(m, k, 3) == 3 * one
+    assert lib.pq_w4a8_linear_group_workspace_size(1, 4096, 5) == 0
+
+
 def test_workspace_size_rules():
     lib = _lib.load()
     for m in (1, 4, 16, 3072):
