@@ -4,8 +4,12 @@
 
 Workload of ``value`` (one "step"): one Qwen3-8B decoder layer's seven
 quantized linears (q/o 4096->4096, k/v 4096->1024, gate/up 4096->12288,
-down 12288->4096) at M = 1 decode token, bf16 in and out, each linear =
-rotation kernel + W4A8 GEMM kernel.  A pool of distinct layers (8 by
+down 12288->4096) at M = 1 decode token, bf16 in and out.  As in a decoder
+layer, q/k/v read one input (the attention input) and gate/up another (the
+MLP input); each trio / pair runs as one group (paroquant::w4a8_linear_group:
+one rotation launch + one GEMM launch), o and down alone (two launches each).
+The same layer with all seven linears called separately is reported next to
+it.  A pool of distinct layers (8 by
 default, 772 MB of weights, so the 256 MB Infinity Cache cannot serve them)
 is captured as ONE HIP graph, the way a model's decode step is captured
 whole; a replay is as many steps as the pool has layers, and --steps is
@@ -117,27 +121,39 @@ def main() -> int:
                  for n, (N, K) in zip(names, shapes)]
         pool.append(layer)
     torch.cuda.synchronize()
+    from alpamayo_amd.quantization import SharedInputRotateLinears
+    # q/k/v read the attention input and gate/up the MLP input: each trio / pair runs as one group
+    groups = [(SharedInputRotateLinears(L[0:3]), SharedInputRotateLinears(L[4:6])) for L in pool]
     pool_mb = sum(m.rotate_linear.qlinear.qweight.numel() for L in pool for m in L) / 1e6
     log(f"pool: {args.pool_layers} layers, {pool_mb:.0f} MB of packed int4 weights ({time.time() - t0:.1f}s)")
 
     def make_inputs(M, seed):
+        """Per layer: the attention input (q, k, v), the attention output (o), the MLP input (gate, up) and
+        the activated MLP hidden state (down)."""
         g = workloads.generator(seed, device=dev)
-        return [[workloads.activations(M, K, g, device=dev) for (_, K) in shapes] for _ in pool]
+        return [tuple(workloads.activations(M, K, g, device=dev) for K in (4096, 4096, 4096, 12288)) for _ in pool]
 
-    def capture_layers(M, seed):
+    def run_layer(li, X, grouped):
+        L = pool[li]
+        xa, xo, xm, xd = X
+        if grouped:
+            qkv, gu = groups[li]
+            return [*qkv(xa), L[3](xo), *gu(xm), L[6](xd)]
+        return [L[0](xa), L[1](xa), L[2](xa), L[3](xo), L[4](xm), L[5](xm), L[6](xd)]
+
+    def capture_layers(M, seed, grouped):
         """One HIP graph holding the whole pool of layers in sequence, as a
         model's decode step is captured whole: a replay is len(pool) steps."""
         xs = make_inputs(M, seed)
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
-            for L, X in zip(pool, xs):
-                for m, x in zip(L, X):
-                    m(x)
+            for li, X in enumerate(xs):
+                run_layer(li, X, grouped)
         torch.cuda.current_stream().wait_stream(s)
         gr = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gr):
-            outs = [[m(x) for m, x in zip(L, X)] for L, X in zip(pool, xs)]
+            outs = [run_layer(li, X, grouped) for li, X in enumerate(xs)]
         return gr, outs, xs
 
     def time_graphs(graphs, steps, warmup):
@@ -155,24 +171,28 @@ def main() -> int:
     result = {}
 
     # ---- decode: M = 1 (value), 4, 16 -------------------------------------
-    decode = {}
+    # Each M twice: q/k/v and gate/up as groups over their shared inputs (value), and all seven
+    # linears as separate calls.
+    decode, decode_sep = {}, {}
     decode_ms = sorted({int(v) for v in args.decode_m.split(",")} | {1})
     P = len(pool)
     for M in decode_ms:
-        gr, _, _ = capture_layers(M, 5000 + M)
-        # K steps = K / P replays of the pool graph (steps is a multiple of P)
-        ms = time_graphs([gr], args.steps // P, -(-args.warmup // P)) / P
         b = sum(linear_bytes(M, N, K) for N, K in shapes)
-        decode[M] = (ms, b / (ms * 1e-3) / 1e9)
-        log(f"decode M={M}: {ms * 1e3:.1f} us/layer, {decode[M][1]:.0f} GB/s")
-        del gr
+        for grouped, table in ((True, decode), (False, decode_sep)):
+            gr, _, _ = capture_layers(M, 5000 + M, grouped)
+            # K steps = K / P replays of the pool graph (steps is a multiple of P)
+            ms = time_graphs([gr], args.steps // P, -(-args.warmup // P)) / P
+            table[M] = (ms, b / (ms * 1e-3) / 1e9)
+            log(f"decode M={M} {'grouped ' if grouped else 'separate'}: {ms * 1e3:.1f} us/layer, "
+                f"{table[M][1]:.0f} GB/s")
+            del gr
     ms_per_step, value = decode[1]
 
     # ---- roofline of the dominant kernel: the decode GEMM at M = 1 --------
     xq_all = []
-    for L, X in zip(pool, make_inputs(1, 7001)):
+    for L, (xa, xo, xm, xd) in zip(pool, make_inputs(1, 7001)):
         row = []
-        for m, x in zip(L, X):
+        for m, x in zip(L, (xa, xa, xa, xo, xm, xm, xd)):
             r = m.rotate_linear.rotation
             row.append(torch.ops.paroquant.rotate_quant_i8(x, r.rot_idx, r.rot_cs, r.scales_f32, r.krot, True, True))
         xq_all.append(row)
@@ -198,20 +218,24 @@ def main() -> int:
     prefill = None
     if not args.no_prefill:
         M = 3072
-        L = pool[0]
         g = workloads.generator(6000, device=dev)
-        X = [workloads.activations(M, K, g, device=dev) for (_, K) in shapes]
-        for m, x in zip(L, X):
-            m(x)
-        gr = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gr):
-            outs = [m(x) for m, x in zip(L, X)]
-        ms = time_graphs([gr], args.prefill_steps, 3)
+        X = tuple(workloads.activations(M, K, g, device=dev) for K in (4096, 4096, 4096, 12288))
         ops = sum(2 * M * N * K for N, K in shapes)
+        res = {}
+        for grouped in (True, False):
+            run_layer(0, X, grouped)
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                outs = run_layer(0, X, grouped)
+            res[grouped] = time_graphs([gr], args.prefill_steps, 3)
+            del gr, outs
+        ms = res[True]
         tops = ops / (ms * 1e-3) / 1e12
-        # GEMM kernels alone
+        tops_sep = ops / (res[False] * 1e-3) / 1e12
+        # GEMM kernels alone (each linear's GEMM on its own)
+        L = pool[0]
         xq = []
-        for m, x in zip(L, X):
+        for m, x in zip(L, (X[0], X[0], X[0], X[1], X[2], X[2], X[3])):
             r = m.rotate_linear.rotation
             xq.append(torch.ops.paroquant.rotate_quant_i8(x, r.rot_idx, r.rot_cs, r.scales_f32, r.krot, True, True))
         gg = torch.cuda.CUDAGraph()
@@ -223,10 +247,11 @@ def main() -> int:
         gtops = ops / (gms * 1e-3) / 1e12
         prefill = {"ms_per_layer": round(ms, 4), "tops": round(tops, 1),
                    "pct_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2),
+                   "separate_linears_ms_per_layer": round(res[False], 4), "separate_linears_tops": round(tops_sep, 1),
                    "gemm_only_tops": round(gtops, 1), "gemm_only_pct_int8_peak": round(100 * gtops / INT8_PEAK_TOPS, 2)}
-        log(f"prefill M=3072: {ms:.3f} ms/layer, {tops:.0f} TOPS ({prefill['pct_int8_peak']}%), "
-            f"GEMM only {gtops:.0f} TOPS")
-        del gr, gg, outs, xq, X
+        log(f"prefill M=3072: {ms:.3f} ms/layer grouped, {tops:.0f} TOPS ({prefill['pct_int8_peak']}%); "
+            f"separate {res[False]:.3f} ms/layer, {tops_sep:.0f} TOPS; GEMMs alone {gtops:.0f} TOPS")
+        del gg, xq, X
 
     # ---- CPU baseline: the oracle on the host ------------------------------
     cpu = None
@@ -248,7 +273,8 @@ def main() -> int:
         "data": "synthetic (seeded activations with 1% x20 outlier channels; random int4 weights, fp16 group scales)",
         "config": {
             "workload": "qwen3-8b decoder layer, 7 W4A8 linears (q,k,v,o 4096->4096/1024; gate,up 4096->12288; "
-                        "down 12288->4096), decode M=1, bf16 in/out, KROT=8, group 128",
+                        "down 12288->4096), decode M=1, bf16 in/out, KROT=8, group 128; q/k/v and gate/up each "
+                        "run as one group over their shared input",
             "tokens_per_step": 1,
             "weight_pool_layers": args.pool_layers,
             "weight_pool_mb": round(pool_mb, 1),
@@ -266,7 +292,9 @@ def main() -> int:
             "avg_launch_us": round(per_launch_us, 3),
         },
         "decode": {f"M{M}": {"us_per_layer": round(v[0] * 1e3, 2), "GBps": round(v[1], 1),
-                             "frac_hbm": round(v[1] / HBM_PEAK_GBS, 4)} for M, v in decode.items()},
+                             "frac_hbm": round(v[1] / HBM_PEAK_GBS, 4),
+                             "separate_linears_us_per_layer": round(decode_sep[M][0] * 1e3, 2),
+                             "separate_linears_GBps": round(decode_sep[M][1], 1)} for M, v in decode.items()},
         "prefill_M3072": prefill,
         "cpu_baseline": cpu,
     }
