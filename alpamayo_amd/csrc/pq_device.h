@@ -47,6 +47,25 @@ __device__ __forceinline__ v4i unpack16(uint32_t w0, uint32_t w1, uint32_t zb) {
   return r;
 }
 
+// 8 bytes of codes (16 consecutive k) -> 16 unsigned bytes q in k order (the
+// zero point is applied separately, see meta_neg_zero4).
+__device__ __forceinline__ v4i nibbles16(uint32_t w0, uint32_t w1) {
+  v4i r;
+  r.x = static_cast<int>(w0 & 0x0f0f0f0fu);
+  r.y = static_cast<int>((w0 >> 4) & 0x0f0f0f0fu);
+  r.z = static_cast<int>(w1 & 0x0f0f0f0fu);
+  r.w = static_cast<int>((w1 >> 4) & 0x0f0f0f0fu);
+  return r;
+}
+
+// Four bytes of -z (z = the zero point in meta bits 16..19): as an MFMA B
+// operand it adds -z * sum_k a[m, k] to a column's accumulator, which turns
+// sum_k a * q into sum_k a * (q - z) exactly.
+__device__ __forceinline__ uint32_t meta_neg_zero4(uint32_t meta) {
+  const uint32_t nz = 0u - ((meta >> 16) & 0xfu);   // byte 0 = (256 - z) mod 256
+  return __builtin_amdgcn_perm(0u, nz, 0u);          // replicate byte 0
+}
+
 __device__ __forceinline__ float meta_scale(uint32_t meta) {
   return pq_f16_to_f32(static_cast<uint16_t>(meta & 0xffffu));
 }

@@ -15,14 +15,16 @@
 //     low nibbles the first four, high nibbles the next four;
 //   wmeta [N/16][G][16] uint32: fp16 scale bits | zero << 16.
 //
-// Unpacking: a dword of 8 codes becomes two dwords of 4 signed bytes
-// (q - z) by  ((w & 0x0f0f0f0f) + (0x80808080 - z*0x01010101)) ^ 0x80808080
-// -- every byte stays in [113, 143] before the xor, so no carry crosses a
-// byte, and the xor maps 128 + d to the two's complement of d.
+// Unpacking, prefill kernel: a dword of 8 codes becomes two dwords of 4
+// signed bytes (q - z) by ((w & 0x0f0f0f0f) + (0x80808080 - z*0x01010101))
+// ^ 0x80808080 -- every byte stays in [113, 143] before the xor, so no carry
+// crosses a byte, and the xor maps 128 + d to the two's complement of d.
+// Decode kernel: the codes go in as plain nibbles q and the zero point as
+// two more MFMAs against bytes of -z, which adds -z * sum_k a exactly.
 //
 // Two kernels:
 //   gemm_skinny  M <= 16: each wave streams 1 KB weight blocks (one 16-column
-//                tile x one 128-group) with 16-byte loads, two
+//                tile x one 128-group) with 16-byte loads, four
 //                v_mfma_i32_16x16x64_i8 per block (activation rows padded to
 //                16); the waves of a workgroup split K and add their partial
 //                sums in LDS in a fixed order.
@@ -248,18 +250,25 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
           a0[u] = *reinterpret_cast<const v4i*>(al + g * 128);
           a1[u] = *reinterpret_cast<const v4i*>(al + g * 128 + 16);
         }
-        const v4i zero = {0, 0, 0, 0};
-        const v4i av0 = arow ? a0[u] : zero, av1 = arow ? a1[u] : zero;
+        // Rows past M hold a copy of a real row: MFMA rows are independent
+        // and those results are never stored, so they need no masking.
+        const v4i av0 = a0[u], av1 = a1[u];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const uint32_t meta = wm[u][nt];
-          const uint32_t zb = meta_zero_bias(meta);
           const v4i w = wb[u][nt];
-          const v4i b0 = unpack16(static_cast<uint32_t>(w.x), static_cast<uint32_t>(w.y), zb);
-          const v4i b1 = unpack16(static_cast<uint32_t>(w.z), static_cast<uint32_t>(w.w), zb);
+          // sum a * (q - z) = sum a * q + sum a * (-z): the codes go in as
+          // plain nibbles, the zero point as two more MFMAs on a constant
+          // -z operand (cheaper in VALU than biasing every byte).
+          const v4i b0 = nibbles16(static_cast<uint32_t>(w.x), static_cast<uint32_t>(w.y));
+          const v4i b1 = nibbles16(static_cast<uint32_t>(w.z), static_cast<uint32_t>(w.w));
+          const int nz = static_cast<int>(meta_neg_zero4(meta));
+          const v4i bz = {nz, nz, nz, nz};
           v4i p = {0, 0, 0, 0};
           p = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, b0, p, 0, 0, 0);
           p = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, b1, p, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, bz, p, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, bz, p, 0, 0, 0);
           if constexpr (PARTIALS) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
@@ -608,26 +617,31 @@ constexpr int kSkinnyMaxM = 16;
 struct SkinnyCfg {
   int nt;  // 16-column tiles per workgroup
   int w;   // waves per workgroup (split K)
+  int u;   // groups per wave per batch (loads in flight)
 };
 
-// Enough workgroups to cover the chip with every weight byte of a wave
-// requested up front (<= 8 groups per wave), and more waves per workgroup
-// when the column tiles are few.
+// About 4-6 waves per SIMD over the whole grid (more waves with fewer
+// groups each shorten every wave's serial load -> MFMA -> scale chain),
+// never more waves than K groups, and batches that divide the K groups
+// evenly where possible (an uneven last batch is masked by a scalar branch).
 SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k) {
   const int G = static_cast<int>(k / 128);
   const int tiles = static_cast<int>(n / 16);
   const int nt = (m > 4 && tiles % 2 == 0 && tiles / 2 >= 128) ? 2 : 1;
-  const int wgs = tiles / nt;
-  int w = 4;
-  if (wgs < 256 || G > 32) w = 8;
-  if (wgs < 128 || G > 64) w = 16;
-  return {nt, w};
+  const int64_t wgs = tiles / nt;
+  int w = wgs * 16 <= 6144 ? 16 : wgs * 8 <= 6144 ? 8 : 4;
+  while (w > 4 && w > G) w >>= 1;
+  int u = 4;
+  if (G <= w) u = 1;
+  else if (G % (w * 4) == 0) u = 4;
+  else if (G % (w * 3) == 0) u = 3;
+  else if (G % (w * 2) == 0) u = 2;
+  return {nt, w, u};
 }
 
-template <int NT, int W, bool PARTIALS, int AQ>
-void launch_skinny_nw(pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* partials, int M, int K,
-                      hipStream_t stream) {
-  constexpr int U = W >= 16 ? 4 : 8;
+template <int NT, int W, int U, bool PARTIALS, int AQ>
+void launch_skinny_nwu(pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* partials, int M, int K,
+                       hipStream_t stream) {
   grp.first[0] = 0;
   for (int i = 0; i < grp.count; ++i) grp.first[i + 1] = grp.first[i] + grp.mem[i].n / 16 / NT;
   const unsigned grid = static_cast<unsigned>(grp.first[grp.count]);
@@ -638,13 +652,23 @@ void launch_skinny_nw(pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* p
 template <bool PARTIALS, int AQ>
 void launch_skinny(const SkinnyCfg& cfg, const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32_t* partials,
                    int M, int K, hipStream_t stream) {
-#define PQ_SKINNY(NT_, W_)                                                                             \
-  if (cfg.nt == NT_ && cfg.w == W_) {                                                                  \
-    launch_skinny_nw<NT_, W_, PARTIALS, AQ>(grp, bias_dtype, y_dtype, partials, M, K, stream);         \
+#define PQ_SKINNY(NT_, W_, U_)                                                                         \
+  if (cfg.nt == NT_ && cfg.w == W_ && cfg.u == U_) {                                                   \
+    launch_skinny_nwu<NT_, W_, U_, PARTIALS, AQ>(grp, bias_dtype, y_dtype, partials, M, K, stream);    \
     return;                                                                                            \
   }
-  PQ_SKINNY(1, 4) PQ_SKINNY(1, 8) PQ_SKINNY(1, 16) PQ_SKINNY(2, 4) PQ_SKINNY(2, 8) PQ_SKINNY(2, 16)
+#define PQ_SKINNY_NT(NT_)                                                                              \
+  PQ_SKINNY(NT_, 4, 1) PQ_SKINNY(NT_, 4, 2) PQ_SKINNY(NT_, 4, 3) PQ_SKINNY(NT_, 4, 4)                  \
+  PQ_SKINNY(NT_, 8, 1) PQ_SKINNY(NT_, 8, 2) PQ_SKINNY(NT_, 8, 3) PQ_SKINNY(NT_, 8, 4)                  \
+  PQ_SKINNY(NT_, 16, 1) PQ_SKINNY(NT_, 16, 2) PQ_SKINNY(NT_, 16, 3) PQ_SKINNY(NT_, 16, 4)
+  PQ_SKINNY_NT(1)
+  PQ_SKINNY_NT(2)
+#undef PQ_SKINNY_NT
 #undef PQ_SKINNY
+  // every configuration choose_skinny makes is listed above; anything else
+  // runs the generic one (any G, masked batches)
+  if (cfg.nt == 2) launch_skinny_nwu<2, 4, 4, PARTIALS, AQ>(grp, bias_dtype, y_dtype, partials, M, K, stream);
+  else launch_skinny_nwu<1, 4, 4, PARTIALS, AQ>(grp, bias_dtype, y_dtype, partials, M, K, stream);
 }
 
 // The decode GEMM's configuration for a group: the workgroup count is the
