@@ -28,7 +28,9 @@ __device__ __forceinline__ float inv_scale(float absmax) { return absmax > 0.0f 
 // dwords of 4 signed bytes (q - z).  Every byte stays in [113, 143] before the
 // xor, so no carry crosses a byte; the xor maps 128 + d to two's complement d.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t zero_bias(uint32_t z) { return 0x80808080u - z * 0x01010101u; }
+__device__ __forceinline__ uint32_t zero_bias(uint32_t z) {
+  return __builtin_amdgcn_perm(0u, 0x80u - z, 0u);   // 0x80 - z in every byte (= 0x80808080 - z * 0x01010101)
+}
 
 __device__ __forceinline__ int unpack_lo(uint32_t w, uint32_t zb) {
   return static_cast<int>(((w & 0x0f0f0f0fu) + zb) ^ 0x80808080u);

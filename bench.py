@@ -17,8 +17,11 @@ rounded up to a whole number of replays.  value = algorithmic bytes
 of the layer / time per step, in GB/s, where per linear
   B = N*K/2 + 2*N*K/128 + N*K/256 + 3*8*K + 2*K + 2*M*K + 2*M*N.
 Also reported: M = 4 and 16 decode, M = 3072 prefill in int8 TOPS and % of
-the 5.0 POPS dense int8 peak, the roofline of the dominant kernel (the
-decode GEMM at M = 1) and the CPU oracle timed on the host.
+the 5.0 POPS dense int8 peak, a speculative-decoding verify block (36 chained
+layers at M = 16 with bf16 RMSNorm between the attention and MLP linears), a
+ragged packed batch (8 requests of U{1..512} tokens), the roofline of the
+dominant kernel (the decode GEMM at M = 1) and the CPU oracle timed on the
+host.
 
 Data are synthetic (seeded), weights random-init; one process, one GPU.
 """
@@ -78,6 +81,8 @@ def main() -> int:
     ap.add_argument("--prefill-steps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-verify", action="store_true", help="skip the 36-layer speculative verify block (M = 16)")
+    ap.add_argument("--no-ragged", action="store_true", help="skip the ragged packed batch")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first copy 256 MiB device to device 3 times: the known-size kernel that calibrates "
@@ -253,6 +258,82 @@ def main() -> int:
             f"separate {res[False]:.3f} ms/layer, {tops_sep:.0f} TOPS; GEMMs alone {gtops:.0f} TOPS")
         del gg, xq, X
 
+    # ---- speculative verify block: 36 chained layers at M = 16 -------------
+    # Per layer a -> (q, k, v) = L(a); o = L_o(q); h = RMSNorm_bf16(a + o) (eps 1e-6, weight U(0.8, 1.2));
+    # d = L_down(silu(L_gate(h)) * L_up(h)); next a = h + d.  Fresh random int4 weights per layer; the whole
+    # block is captured as one graph.  Reported: time per verified block, and the 252 quantized linears of the
+    # block alone (the same linears and inputs without the norms / activations in between).
+    verify = None
+    if not args.no_verify:
+        Mv, Lv, H = 16, 36, 4096
+        t0 = time.time()
+        vlayers = []
+        for li in range(Lv):
+            g = workloads.generator(3001 + li, device=dev)
+            L = [workloads.build_module(workloads.linear_spec(n, N, K, g, device=dev), dev)
+                 for n, (N, K) in zip(names, shapes)]
+            w_norm = (0.8 + 0.4 * torch.rand(H, generator=g, device=dev)).to(torch.bfloat16)
+            vlayers.append((L, SharedInputRotateLinears(L[0:3]), SharedInputRotateLinears(L[4:6]), w_norm))
+        torch.cuda.synchronize()
+        log(f"verify block: {Lv} layers built ({time.time() - t0:.1f}s)")
+        a0 = workloads.activations(Mv, H, workloads.generator(3000, device=dev), device=dev)
+
+        def run_block(a):
+            for L, qkv, gu, w_norm in vlayers:
+                q, _, _ = qkv(a)
+                o = L[3](q)
+                h = torch.nn.functional.rms_norm((a + o).float(), (H,), w_norm.float(), 1e-6).to(torch.bfloat16)
+                gt, up = gu(h)
+                d = L[6](torch.nn.functional.silu(gt) * up)
+                a = h + d
+            return a
+
+        lin_in = [(a0, a0, a0, torch.nn.functional.silu(a0[:, :1].repeat(1, 3 * H)))]   # fixed inputs per layer
+
+        def run_linears():
+            xa, _, _, xd = lin_in[0]
+            for L, qkv, gu, _ in vlayers:
+                q, _, _ = qkv(xa)
+                L[3](q)
+                gu(xa)
+                L[6](xd)
+
+        vres = {}
+        for key, fn in (("block", lambda: run_block(a0)), ("linears", run_linears)):
+            fn()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                fn()
+            vres[key] = time_graphs([gr], max(5, args.prefill_steps), 2)
+            del gr
+        vb = Lv * sum(linear_bytes(Mv, N, K) for N, K in shapes)
+        verify = {"layers": Lv, "tokens": Mv, "ms_per_block": round(vres["block"], 4),
+                  "linears_ms_per_block": round(vres["linears"], 4),
+                  "linears_GBps": round(vb / (vres["linears"] * 1e-3) / 1e9, 1),
+                  "linears_frac_hbm": round(vb / (vres["linears"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"verify block M=16 x 36 layers: {vres['block']:.3f} ms/block; quantized linears alone "
+            f"{vres['linears']:.3f} ms ({verify['linears_GBps']:.0f} GB/s)")
+        del vlayers
+
+    # ---- ragged packed batch: 8 requests of U{1..512} tokens ----------------
+    ragged = None
+    if not args.no_ragged:
+        lens = workloads.ragged_lengths(8, workloads.generator(1004))
+        Mr = sum(lens)
+        g = workloads.generator(6100, device=dev)
+        Xr = tuple(workloads.activations(Mr, K, g, device=dev) for K in (4096, 4096, 4096, 12288))
+        run_layer(0, Xr, True)
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            outs = run_layer(0, Xr, True)
+        rms = time_graphs([gr], args.prefill_steps, 3)
+        rops = sum(2 * Mr * N * K for N, K in shapes)
+        ragged = {"request_tokens": lens, "total_tokens": Mr, "ms_per_layer": round(rms, 4),
+                  "tops": round(rops / (rms * 1e-3) / 1e12, 1),
+                  "pct_int8_peak": round(100 * rops / (rms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 2)}
+        log(f"ragged batch {lens} (M={Mr}): {rms:.3f} ms/layer, {ragged['tops']:.0f} TOPS")
+        del gr, outs, Xr
+
     # ---- CPU baseline: the oracle on the host ------------------------------
     cpu = None
     if not args.no_cpu:
@@ -296,6 +377,8 @@ def main() -> int:
                              "separate_linears_us_per_layer": round(decode_sep[M][0] * 1e3, 2),
                              "separate_linears_GBps": round(decode_sep[M][1], 1)} for M, v in decode.items()},
         "prefill_M3072": prefill,
+        "verify_block_M16": verify,
+        "ragged_batch": ragged,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
