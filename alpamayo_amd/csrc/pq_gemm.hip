@@ -170,8 +170,11 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const int64_t blk = static_cast<int64_t>(tile0 + nt) * G + g;
-          wb[u][nt] = *reinterpret_cast<const v4i*>(wpack + blk * 1024 + lane * 16);
-          wm[u][nt] = wmeta[blk * 16 + c];
+          // Weights are read once per step: non-temporal loads keep them
+          // from evicting what is re-read (rotation operands, activations)
+          // from L2 and the Infinity Cache.
+          wb[u][nt] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wpack + blk * 1024 + lane * 16));
+          wm[u][nt] = __builtin_nontemporal_load(wmeta + blk * 16 + c);
         }
         if constexpr (AQ == 0) {
           // Unconditional (rows >= M read row 0 and are zeroed at use): a
