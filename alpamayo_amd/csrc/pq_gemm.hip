@@ -625,20 +625,29 @@ struct SkinnyCfg {
 
 // About 4-6 waves per SIMD over the whole grid (more waves with fewer
 // groups each shorten every wave's serial load -> MFMA -> scale chain),
-// never more waves than K groups, and batches that divide the K groups
-// evenly where possible (an uneven last batch is masked by a scalar branch).
-SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k) {
+// two column tiles per workgroup for wide outputs (768+ tiles, e.g. a
+// gate/up pair) when allowed, never more waves than K groups, and the
+// shallowest batch of at least two groups that divides the K groups (an
+// uneven last batch is masked by a scalar branch).  Measured on the
+// Qwen3-8B shapes at M = 1.  Two tiles are not allowed when a member of a
+// group has an odd tile count, nor with 16 waves behind the A-quantizing
+// prologue (that combination spills).
+SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k, bool two_tiles_ok = true, bool aq = false) {
   const int G = static_cast<int>(k / 128);
   const int tiles = static_cast<int>(n / 16);
-  const int nt = (m > 4 && tiles % 2 == 0 && tiles / 2 >= 128) ? 2 : 1;
-  const int64_t wgs = tiles / nt;
-  int w = wgs * 16 <= 6144 ? 16 : wgs * 8 <= 6144 ? 8 : 4;
+  auto waves_for = [](int64_t wgs) { return wgs * 16 <= 6144 ? 16 : wgs * 8 <= 6144 ? 8 : 4; };
+  int nt = (two_tiles_ok && tiles % 2 == 0 && (tiles >= 768 || (m > 4 && tiles / 2 >= 128))) ? 2 : 1;
+  int w = waves_for(tiles / nt);
+  if (aq && nt == 2 && w == 16) {
+    nt = 1;
+    w = waves_for(tiles);
+  }
   while (w > 4 && w > G) w >>= 1;
-  int u = 4;
+  int u = 2;
   if (G <= w) u = 1;
-  else if (G % (w * 4) == 0) u = 4;
-  else if (G % (w * 3) == 0) u = 3;
   else if (G % (w * 2) == 0) u = 2;
+  else if (G % (w * 3) == 0) u = 3;
+  else if (G % (w * 4) == 0) u = 4;
   return {nt, w, u};
 }
 
@@ -677,16 +686,14 @@ void launch_skinny(const SkinnyCfg& cfg, const pq::GemmGroup& grp, int bias_dtyp
 // The decode GEMM's configuration for a group: the workgroup count is the
 // sum over members; two tiles per workgroup only when every member's tile
 // count is even.
-SkinnyCfg choose_skinny_group(const pq::GemmGroup& grp, int64_t m, int64_t k) {
+SkinnyCfg choose_skinny_group(const pq::GemmGroup& grp, int64_t m, int64_t k, bool aq) {
   int64_t n = 0;
   bool even = true;
   for (int i = 0; i < grp.count; ++i) {
     n += grp.mem[i].n;
     even = even && (grp.mem[i].n / 16) % 2 == 0;
   }
-  SkinnyCfg cfg = choose_skinny(m, n, k);
-  if (!even) cfg.nt = 1;
-  return cfg;
+  return choose_skinny(m, n, k, even, aq);
 }
 
 int check_gemm_args(const char* who, int64_t m, int64_t n, int64_t k, int group_size) {
@@ -714,12 +721,11 @@ void launch_gemm_group(GemmGroup grp, int aq, int bias_dtype, int y_dtype, int m
     launch_prefill<false>(grp, bias_dtype, y_dtype, nullptr, m, k, stream);
     return;
   }
-  SkinnyCfg cfg = choose_skinny_group(grp, m, k);
+  const SkinnyCfg cfg = choose_skinny_group(grp, m, k, aq != 0);
   if (aq == 0) {
     launch_skinny<false, 0>(cfg, grp, bias_dtype, y_dtype, nullptr, m, k, stream);
     return;
   }
-  if (cfg.w == 16) cfg.nt = 1;   // two tiles x 16 waves would spill next to the prologue
   if (aq == 1) launch_skinny<false, 1>(cfg, grp, bias_dtype, y_dtype, nullptr, m, k, stream);
   else launch_skinny<false, 2>(cfg, grp, bias_dtype, y_dtype, nullptr, m, k, stream);
 }
