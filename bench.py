@@ -250,10 +250,27 @@ def main() -> int:
                 torch.ops.paroquant.w4a8_gemm(q8, s8, q.qweight, q.scales, None, q.workspace, torch.bfloat16)
         gms = time_graphs([gg], args.prefill_steps, 3)
         gtops = ops / (gms * 1e-3) / 1e12
+        # each shape's GEMM alone (q, k, gate, down; o, v, up repeat a shape)
+        per_shape = {}
+        for idx in (0, 1, 4, 6):
+            m = L[idx]
+            q = m.rotate_linear.qlinear
+            q8, s8 = xq[idx]
+            g1 = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g1):
+                torch.ops.paroquant.w4a8_gemm(q8, s8, q.qweight, q.scales, None, q.workspace, torch.bfloat16)
+            sms = time_graphs([g1], args.prefill_steps, 3)
+            sops = 2 * M * q.out_features * q.in_features
+            per_shape[f"{q.out_features}x{q.in_features}"] = {
+                "us": round(sms * 1e3, 1), "pct_int8_peak": round(100 * sops / (sms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 2)}
+            del g1
+        log("prefill GEMM per shape (N x K): " + ", ".join(f"{k} {v['us']} us ({v['pct_int8_peak']}%)"
+                                                           for k, v in per_shape.items()))
         prefill = {"ms_per_layer": round(ms, 4), "tops": round(tops, 1),
                    "pct_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2),
                    "separate_linears_ms_per_layer": round(res[False], 4), "separate_linears_tops": round(tops_sep, 1),
-                   "gemm_only_tops": round(gtops, 1), "gemm_only_pct_int8_peak": round(100 * gtops / INT8_PEAK_TOPS, 2)}
+                   "gemm_only_tops": round(gtops, 1), "gemm_only_pct_int8_peak": round(100 * gtops / INT8_PEAK_TOPS, 2),
+                   "gemm_per_shape": per_shape}
         log(f"prefill M=3072: {ms:.3f} ms/layer grouped, {tops:.0f} TOPS ({prefill['pct_int8_peak']}%); "
             f"separate {res[False]:.3f} ms/layer, {tops_sep:.0f} TOPS; GEMMs alone {gtops:.0f} TOPS")
         del gg, xq, X
