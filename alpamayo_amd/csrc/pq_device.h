@@ -157,17 +157,99 @@ __device__ __forceinline__ void rot_layer(const RotLane<KP>& p, int r, float (&a
   }
 }
 
+// ---------------------------------------------------------------------------
+// RMSNorm prologue (reference: Qwen3VLTextRMSNorm.forward,
+// src/alpamayo_r1/models/qwen3_vl/modeling_qwen3_vl.py:354-359):
+//   s = x (+ res), rounded to the activation dtype;
+//   h = round(w * round(s * rsqrt(mean(s^2) + eps))).
+// ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ float round_to_dt(float v) {
+  if constexpr (DT == PQ_F16) return pq_round_f16(v);
+  else if constexpr (DT == PQ_BF16) return pq_bf16_to_f32(pq_f32_to_bf16(v));
+  else return v;
+}
+
+template <int DT>
+__device__ __forceinline__ void load8_as_f32(const void* base, int64_t elem, float f[8]) {
+  if constexpr (DT == PQ_F32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + elem);
+    const float4 a = p[0], b = p[1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  } else {
+    const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + elem);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[2 * e] = pq_raw_to_f32<DT>(w[e] & 0xffffu);
+      f[2 * e + 1] = pq_raw_to_f32<DT>(w[e] >> 16);
+    }
+  }
+}
+
+// Wave64 sum through xor butterflies: every lane ends with the same value
+// (the same additions in the same association, only commuted).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// sum_k s[k]^2 of one row (h % 8 == 0), s = x (+ res) rounded to DT, by one
+// wave: lane l sums the 8-element chunks 8l, 8l + 512, ... in order (each
+// square rounded, then added), then the butterfly.  Every wave that calls it
+// on the same row gets the same bits.
+template <int DT>
+__device__ __forceinline__ float row_sumsq(const void* __restrict__ x, const void* __restrict__ res, int64_t row_off,
+                                           int h, int lane) {
+  float acc = 0.0f;
+  for (int c8 = lane * 8; c8 < h; c8 += 512) {
+    float f[8];
+    load8_as_f32<DT>(x, row_off + c8, f);
+    if (res != nullptr) {
+      float r[8];
+      load8_as_f32<DT>(res, row_off + c8, r);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = round_to_dt<DT>(f[e] + r[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = acc + f[e] * f[e];
+  }
+  return wave_sum(acc);
+}
+
+// rsqrt(mean + eps) as two correctly rounded float32 operations.
+__device__ __forceinline__ float rms_inv(float sumsq, int h, float eps) {
+  return 1.0f / __builtin_sqrtf(sumsq / static_cast<float>(h) + eps);
+}
+
+// The normalized value of one element (s already rounded to DT).
+template <int DT>
+__device__ __forceinline__ float rms_apply(float s, float r, float w) {
+  return round_to_dt<DT>(w * round_to_dt<DT>(s * r));
+}
+
 // One wave rotates 128-channel group g of the first min(M, MR) rows: channel
 // scale, the krot register-chain layers, then the rotated values go to xr
 // (fp16 when MAT16, else fp32; row stride h) and each row's absmax over the
 // group to gmax[m * (h / 128) + g].  With PQ_RQ_INPUT_FP16 the scaled input
 // is first rounded through fp16.  Rows past M repeat row M-1 and store
 // nothing.
-template <int DT, int KP, bool MAT16, int MR>
+//
+// With NORM the wave first computes each row's RMSNorm factor over the whole
+// row (every wave of the launch gets the same bits), then rotates the
+// normalized values of its group and, when h_out / s_out are set, writes
+// them and the residual sum s for the group's channels.
+template <int DT, int KP, bool MAT16, int MR, bool NORM = false>
 __device__ __forceinline__ void rotate_group_rows(const void* __restrict__ x, const uint32_t* __restrict__ rot_idx,
                                                   const float* __restrict__ rot_cs, const float* __restrict__ scales,
                                                   void* __restrict__ xr, float* __restrict__ gmax, int M, int h,
-                                                  int krot, unsigned flags, int g, int lane) {
+                                                  int krot, unsigned flags, int g, int lane,
+                                                  const void* __restrict__ nres = nullptr,
+                                                  const void* __restrict__ nw = nullptr,
+                                                  void* __restrict__ h_out = nullptr,
+                                                  void* __restrict__ s_out = nullptr, float eps = 0.0f) {
   const int G = h >> 7;
   const bool in16 = (flags & PQ_RQ_INPUT_FP16) != 0;
   const bool has_scales = scales != nullptr;
@@ -190,9 +272,38 @@ __device__ __forceinline__ void rotate_group_rows(const void* __restrict__ x, co
   const float s0 = has_scales ? s0r : 1.0f, s1 = has_scales ? s1r : 1.0f;
   const bool sw = rot_init_swapped(p);
   float a[MR], b[MR];
+  float xlo[MR], xhi[MR];
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
-    float lo = pq_raw_to_f32<DT>(xa[m]), hi = pq_raw_to_f32<DT>(xb[m]);
+    xlo[m] = pq_raw_to_f32<DT>(xa[m]);
+    xhi[m] = pq_raw_to_f32<DT>(xb[m]);
+  }
+  if constexpr (NORM) {
+    const float w0 = pq_load_as_f32<DT>(nw, g * 128 + lane), w1 = pq_load_as_f32<DT>(nw, g * 128 + 64 + lane);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const int mm = m < M ? m : M - 1;
+      const int64_t ro = static_cast<int64_t>(mm) * h;
+      const float r = rms_inv(row_sumsq<DT>(x, nres, ro, h, lane), h, eps);
+      if (nres != nullptr) {
+        xlo[m] = round_to_dt<DT>(xlo[m] + pq_load_as_f32<DT>(nres, ro + g * 128 + lane));
+        xhi[m] = round_to_dt<DT>(xhi[m] + pq_load_as_f32<DT>(nres, ro + g * 128 + 64 + lane));
+      }
+      if (m < M && s_out != nullptr) {
+        pq_store_from_f32<DT>(s_out, ro + g * 128 + lane, xlo[m]);
+        pq_store_from_f32<DT>(s_out, ro + g * 128 + 64 + lane, xhi[m]);
+      }
+      xlo[m] = rms_apply<DT>(xlo[m], r, w0);
+      xhi[m] = rms_apply<DT>(xhi[m], r, w1);
+      if (m < M && h_out != nullptr) {
+        pq_store_from_f32<DT>(h_out, ro + g * 128 + lane, xlo[m]);
+        pq_store_from_f32<DT>(h_out, ro + g * 128 + 64 + lane, xhi[m]);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    float lo = xlo[m], hi = xhi[m];
     lo = (in16 ? pq_round_f16(lo) : lo) * s0;
     hi = (in16 ? pq_round_f16(hi) : hi) * s1;
     a[m] = sw ? hi : lo;

@@ -52,15 +52,30 @@ struct RotGroup {
 // Rows per launch of the split rotation (and rows the rotated GEMM accepts).
 constexpr int kSplitMaxRows = 16;
 
+// Optional RMSNorm prologue of a group's rotation (a decoder layer's norm in
+// front of q/k/v or gate/up):  s = x + res (rounded to x's dtype; s = x when
+// res is null),  h = round(w * round(s * rsqrt(mean_k(s^2) + eps))), both
+// roundings to x's dtype, mean and rsqrt in float32.  The members rotate h;
+// h and s are also written when h_out / s_out are set ([m][k], x's dtype).
+// w: [k] in x's dtype.
+struct NormArgs {
+  const void* res;
+  const void* w;
+  void* h_out;
+  void* s_out;
+  float eps;
+};
+
 // Rotation of m <= kSplitMaxRows rows with one wave per 128-channel group,
 // for every member of the group: xr [m][h] rotated values (fp16 when flags
 // has PQ_RQ_MATERIALIZE_FP16, else fp32) and gmax [m][h/128] the absmax of
 // each row's group.
 PQ_HIDDEN void launch_rotate_split(const void* x, int x_dtype, const RotGroup& grp, int m, int h, int krot,
-                                   unsigned flags, hipStream_t stream);
+                                   unsigned flags, hipStream_t stream, const NormArgs* norm = nullptr);
 // Rotation + per-token int8 quant of whole rows for every member of the group.
 PQ_HIDDEN void launch_rotate_quant_group(const void* x, int x_dtype, const RotGroup& grp, int64_t rows, int h,
-                                         int krot, unsigned flags, hipStream_t stream);
+                                         int krot, unsigned flags, hipStream_t stream,
+                                         const NormArgs* norm = nullptr);
 
 // Decode GEMM whose A operand is quantized in the kernel from launch_rotate_split's
 // output: token scale = max over the row's gmax / 127.  Returns false when m or

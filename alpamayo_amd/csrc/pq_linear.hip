@@ -45,7 +45,7 @@ size_t group_workspace_size(int64_t m, int64_t k, int count) {
 
 int linear_group(const char* who, const void* x, int x_dtype, const pq_linear_member* members, int count,
                  int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot, unsigned flags, void* workspace,
-                 size_t workspace_bytes, hipStream_t s) {
+                 size_t workspace_bytes, hipStream_t s, const pq::NormArgs* norm = nullptr) {
   PQ_REQUIRE(count >= 1 && count <= pq::kMaxGroup, PQ_ERR_ARG, "%s: count=%d not in 1..%d", who, count,
              pq::kMaxGroup);
   PQ_REQUIRE(members != nullptr, PQ_ERR_ARG, "%s: null member table", who);
@@ -104,8 +104,8 @@ int linear_group(const char* who, const void* x, int x_dtype, const pq_linear_me
       gg.mem[i] = {static_cast<const int8_t*>(a), sc, nullptr, nullptr, mb.wpack, mb.wmeta, mb.bias, mb.y,
                    static_cast<int>(mb.n)};
   }
-  if (split) pq::launch_rotate_split(x, x_dtype, rg, M, K, krot, flags, s);
-  else pq::launch_rotate_quant_group(x, x_dtype, rg, m, K, krot, flags, s);
+  if (split) pq::launch_rotate_split(x, x_dtype, rg, M, K, krot, flags, s, norm);
+  else pq::launch_rotate_quant_group(x, x_dtype, rg, m, K, krot, flags, s, norm);
   int st = pq::launch_status(split ? "linear rotation launch" : "linear rotate+quant launch");
   if (st != PQ_OK) return st;
   const int aq = split ? ((flags & PQ_RQ_MATERIALIZE_FP16) ? 1 : 2) : 0;
@@ -139,4 +139,28 @@ extern "C" int pq_w4a8_linear_group(const void* x, int x_dtype, const pq_linear_
                                     void* workspace, size_t workspace_bytes, void* stream) {
   return linear_group("pq_w4a8_linear_group", x, x_dtype, members, count, bias_dtype, y_dtype, m, k, krot, flags,
                       workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pq_w4a8_linear_group_rmsnorm(const void* x, const void* residual, const void* norm_weight, float eps,
+                                            void* h_out, void* sum_out, int x_dtype,
+                                            const pq_linear_member* members, int count, int bias_dtype,
+                                            int y_dtype, int64_t m, int64_t k, int krot, unsigned flags,
+                                            void* workspace, size_t workspace_bytes, void* stream) {
+  const char* who = "pq_w4a8_linear_group_rmsnorm";
+  PQ_REQUIRE(x_dtype == PQ_F32 || x_dtype == PQ_F16 || x_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED, "%s: x dtype code %d",
+             who, x_dtype);
+  PQ_REQUIRE(eps >= 0.0f && eps < 1.0f, PQ_ERR_ARG, "%s: eps=%g must be in [0, 1)", who, static_cast<double>(eps));
+  if (m > 0) {
+    const size_t es = static_cast<size_t>(pq::dtype_size(x_dtype));
+    PQ_REQUIRE(norm_weight != nullptr && pq::aligned_to(norm_weight, es), PQ_ERR_ARG,
+               "%s: norm_weight must be non-null and aligned to its dtype", who);
+    PQ_REQUIRE(residual == nullptr || pq::aligned_to(residual, 16), PQ_ERR_ARG,
+               "%s: residual must be 16-byte aligned", who);
+    PQ_REQUIRE((h_out == nullptr || pq::aligned_to(h_out, es)) && (sum_out == nullptr || pq::aligned_to(sum_out, es)),
+               PQ_ERR_ARG, "%s: h_out and sum_out must be aligned to x's dtype", who);
+    PQ_REQUIRE(sum_out == nullptr || residual != nullptr, PQ_ERR_ARG, "%s: sum_out needs a residual", who);
+  }
+  const pq::NormArgs norm = {residual, norm_weight, h_out, sum_out, eps};
+  return linear_group(who, x, x_dtype, members, count, bias_dtype, y_dtype, m, k, krot, flags, workspace,
+                      workspace_bytes, static_cast<hipStream_t>(stream), &norm);
 }

@@ -146,10 +146,17 @@ __device__ __forceinline__ void load8(const void* base, int64_t elem, float f[8]
 // ---------------------------------------------------------------------------
 constexpr int kRQWaves = 8;
 
-template <int DT, int KP, bool MAT16, int RB>
+//
+// With NORM the block first computes the RMSNorm factor of each of its rows
+// (wave r takes row r, with the same per-row routine as the split rotation),
+// then rotates the normalized values; member 0's blocks also write the
+// normalized rows and the residual sum when asked.
+template <int DT, int KP, bool MAT16, int RB, bool NORM>
 __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void* __restrict__ x,
                                                                        const pq::RotGroup grp, int64_t row_begin,
-                                                                       int h, int krot, unsigned flags) {
+                                                                       int h, int krot, unsigned flags,
+                                                                       const pq::NormArgs nm) {
+  static_assert(RB <= kRQWaves, "one wave per row for the norm factors");
   const pq::RotMember& mb = grp.mem[blockIdx.y];
   const uint32_t* __restrict__ rot_idx = mb.rot_idx;
   const float* __restrict__ rot_cs = mb.rot_cs;
@@ -190,14 +197,42 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
     s1 = sp[(g * 128 + 64 + lane) & smask];
   };
 
+  // RMSNorm: residual rows and norm weights ride along with the inputs
+  // (unconditional loads; without a residual they re-read x and are unused).
+  __shared__ float s_rinv[RB];
+  const void* nres = NORM && nm.res != nullptr ? nm.res : x;
+  uint32_t ra[RB], rb[RB], ran[RB], rbn[RB];
+  uint32_t wa = 0, wb = 0, wan = 0, wbn = 0;
+  auto load_norm = [&](int g, uint32_t (&va)[RB], uint32_t (&vb)[RB], uint32_t& w0, uint32_t& w1) {
+    if constexpr (NORM) {
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        va[r] = pq_load_raw<DT>(nres, (row0 + r) * h + g * 128 + lane);
+        vb[r] = pq_load_raw<DT>(nres, (row0 + r) * h + g * 128 + 64 + lane);
+      }
+      w0 = pq_load_raw<DT>(nm.w, g * 128 + lane);
+      w1 = pq_load_raw<DT>(nm.w, g * 128 + 64 + lane);
+    }
+  };
+  if constexpr (NORM) {
+    if (w < RB) {
+      const float r = pqd::rms_inv(pqd::row_sumsq<DT>(x, nm.res, (row0 + w) * h, h, lane), h, nm.eps);
+      if (lane == 0) s_rinv[w] = r;
+    }
+    __syncthreads();
+  }
+  const bool write_norm = NORM && blockIdx.y == 0;   // the same for every member: member 0 writes
+
   if (w < G) {
     pqd::load_rot_lane<KP>(rot_idx, rot_cs, w, lane, cur);
     load_inputs(w, xa, xb, sa, sb);
+    load_norm(w, ra, rb, wa, wb);
   }
   for (int g = w; g < G; g += kRQWaves) {
     const int gn = (g + kRQWaves < G) ? g + kRQWaves : g;   // clamped: the loads stay unconditional
     pqd::load_rot_lane<KP>(rot_idx, rot_cs, gn, lane, nxt);
     load_inputs(gn, xan, xbn, san, sbn);
+    load_norm(gn, ran, rbn, wan, wbn);
 
     const bool sw = pqd::rot_init_swapped(cur);
     const float s0 = has_scales ? sa : 1.0f, s1 = has_scales ? sb : 1.0f;
@@ -205,6 +240,23 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
       float lo = pq_raw_to_f32<DT>(xa[r]), hi = pq_raw_to_f32<DT>(xb[r]);
+      if constexpr (NORM) {
+        const int64_t ro = (row0 + r) * h + g * 128 + lane;
+        if (nm.res != nullptr) {
+          lo = pqd::round_to_dt<DT>(lo + pq_raw_to_f32<DT>(ra[r]));
+          hi = pqd::round_to_dt<DT>(hi + pq_raw_to_f32<DT>(rb[r]));
+        }
+        if (write_norm && nm.s_out != nullptr) {
+          pq_store_from_f32<DT>(nm.s_out, ro, lo);
+          pq_store_from_f32<DT>(nm.s_out, ro + 64, hi);
+        }
+        lo = pqd::rms_apply<DT>(lo, s_rinv[r], pq_raw_to_f32<DT>(wa));
+        hi = pqd::rms_apply<DT>(hi, s_rinv[r], pq_raw_to_f32<DT>(wb));
+        if (write_norm && nm.h_out != nullptr) {
+          pq_store_from_f32<DT>(nm.h_out, ro, lo);
+          pq_store_from_f32<DT>(nm.h_out, ro + 64, hi);
+        }
+      }
       lo = (in16 ? pq_round_f16(lo) : lo) * s0;
       hi = (in16 ? pq_round_f16(hi) : hi) * s1;
       a[r] = sw ? hi : lo;
@@ -234,9 +286,13 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
     for (int r = 0; r < RB; ++r) {
       xa[r] = xan[r];
       xb[r] = xbn[r];
+      ra[r] = ran[r];
+      rb[r] = rbn[r];
     }
     sa = san;
     sb = sbn;
+    wa = wan;
+    wb = wbn;
   }
 
 #pragma unroll
@@ -297,41 +353,53 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
 // ---------------------------------------------------------------------------
 constexpr int kSplitWaves = 4;
 
-template <int DT, int KP, bool MAT16, int MR>
+template <int DT, int KP, bool MAT16, int MR, bool NORM>
 __global__ __launch_bounds__(kSplitWaves * 64) void rotate_split_kernel(const void* __restrict__ x,
                                                                          const pq::RotGroup grp, int M, int h,
-                                                                         int krot, unsigned flags) {
+                                                                         int krot, unsigned flags,
+                                                                         const pq::NormArgs nm) {
   const int g = blockIdx.x * kSplitWaves + (threadIdx.x >> 6);
   if (g >= (h >> 7)) return;   // whole waves only; this kernel has no barrier
   const pq::RotMember& mb = grp.mem[blockIdx.y];
-  pqd::rotate_group_rows<DT, KP, MAT16, MR>(x, mb.rot_idx, mb.rot_cs, mb.scales, mb.out, mb.out_scale, M, h, krot,
-                                            flags, g, threadIdx.x & 63);
+  // the normalized rows and the residual sum are the same for every member: member 0 writes them
+  const bool first = blockIdx.y == 0;
+  pqd::rotate_group_rows<DT, KP, MAT16, MR, NORM>(x, mb.rot_idx, mb.rot_cs, mb.scales, mb.out, mb.out_scale, M, h,
+                                                  krot, flags, g, threadIdx.x & 63, nm.res, nm.w,
+                                                  first ? nm.h_out : nullptr, first ? nm.s_out : nullptr, nm.eps);
 }
 
-template <int DT, int KP, bool MAT16>
+template <int DT, int KP, bool MAT16, bool NORM>
 void launch_split_kp(const void* x, const pq::RotGroup& grp, int M, int h, int krot, unsigned flags,
-                     hipStream_t stream) {
+                     const pq::NormArgs& nm, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>((h / 128 + kSplitWaves - 1) / kSplitWaves), static_cast<unsigned>(grp.count));
-#define PQ_SPLIT(MR_)                                                                                    \
-  if (M <= MR_) {                                                                                        \
-    rotate_split_kernel<DT, KP, MAT16, MR_><<<grid, kSplitWaves * 64, 0, stream>>>(x, grp, M, h, krot, flags); \
-    return;                                                                                              \
+#define PQ_SPLIT(MR_)                                                                                      \
+  if (M <= MR_) {                                                                                          \
+    rotate_split_kernel<DT, KP, MAT16, MR_, NORM><<<grid, kSplitWaves * 64, 0, stream>>>(x, grp, M, h, krot, \
+                                                                                        flags, nm);          \
+    return;                                                                                                \
   }
   PQ_SPLIT(1) PQ_SPLIT(2) PQ_SPLIT(4) PQ_SPLIT(8) PQ_SPLIT(16)
 #undef PQ_SPLIT
 }
 
-template <int DT>
-void launch_split_dt(const void* x, const pq::RotGroup& grp, int M, int h, int krot, unsigned flags,
-                     hipStream_t stream) {
+template <int DT, bool NORM>
+void launch_split_norm(const void* x, const pq::RotGroup& grp, int M, int h, int krot, unsigned flags,
+                       const pq::NormArgs& nm, hipStream_t stream) {
   const bool mat16 = (flags & PQ_RQ_MATERIALIZE_FP16) != 0;
   if (krot <= 8) {
-    if (mat16) launch_split_kp<DT, 8, true>(x, grp, M, h, krot, flags, stream);
-    else launch_split_kp<DT, 8, false>(x, grp, M, h, krot, flags, stream);
+    if (mat16) launch_split_kp<DT, 8, true, NORM>(x, grp, M, h, krot, flags, nm, stream);
+    else launch_split_kp<DT, 8, false, NORM>(x, grp, M, h, krot, flags, nm, stream);
   } else {
-    if (mat16) launch_split_kp<DT, 16, true>(x, grp, M, h, krot, flags, stream);
-    else launch_split_kp<DT, 16, false>(x, grp, M, h, krot, flags, stream);
+    if (mat16) launch_split_kp<DT, 16, true, NORM>(x, grp, M, h, krot, flags, nm, stream);
+    else launch_split_kp<DT, 16, false, NORM>(x, grp, M, h, krot, flags, nm, stream);
   }
+}
+
+template <int DT>
+void launch_split_dt(const void* x, const pq::RotGroup& grp, int M, int h, int krot, unsigned flags,
+                     const pq::NormArgs* norm, hipStream_t stream) {
+  if (norm != nullptr) launch_split_norm<DT, true>(x, grp, M, h, krot, flags, *norm, stream);
+  else launch_split_norm<DT, false>(x, grp, M, h, krot, flags, pq::NormArgs{}, stream);
 }
 
 // Per-token quant of an existing activation: absmax pass, then quant pass.
@@ -393,41 +461,49 @@ inline int rq_rows_per_block(int64_t rows, int h, bool mat16) {
   return rb;
 }
 
-template <int DT, int KP, bool MAT16, int RB>
+template <int DT, int KP, bool MAT16, int RB, bool NORM>
 void launch_rq_rb(const void* x, const pq::RotGroup& grp, int64_t row_begin, int64_t nblocks, int h, int krot,
-                  unsigned flags, hipStream_t stream) {
+                  unsigned flags, const pq::NormArgs& nm, hipStream_t stream) {
   if (nblocks <= 0) return;
   const size_t lds = static_cast<size_t>(RB) * h * (MAT16 ? 2 : 4);
   const dim3 grid(static_cast<unsigned>(nblocks), static_cast<unsigned>(grp.count));
-  rotate_quant_kernel<DT, KP, MAT16, RB><<<grid, kRQWaves * 64, lds, stream>>>(x, grp, row_begin, h, krot, flags);
+  rotate_quant_kernel<DT, KP, MAT16, RB, NORM><<<grid, kRQWaves * 64, lds, stream>>>(x, grp, row_begin, h, krot,
+                                                                                     flags, nm);
 }
 
-template <int DT, int KP, bool MAT16>
+template <int DT, int KP, bool MAT16, bool NORM>
 void launch_rq(const void* x, const pq::RotGroup& grp, int64_t rows, int h, int krot, unsigned flags,
-               hipStream_t stream) {
+               const pq::NormArgs& nm, hipStream_t stream) {
   const int rb = rq_rows_per_block(rows, h, MAT16);
   const int64_t full = rows / rb;
   switch (rb) {
-    case 8: launch_rq_rb<DT, KP, MAT16, 8>(x, grp, 0, full, h, krot, flags, stream); break;
-    case 4: launch_rq_rb<DT, KP, MAT16, 4>(x, grp, 0, full, h, krot, flags, stream); break;
-    case 2: launch_rq_rb<DT, KP, MAT16, 2>(x, grp, 0, full, h, krot, flags, stream); break;
+    case 8: launch_rq_rb<DT, KP, MAT16, 8, NORM>(x, grp, 0, full, h, krot, flags, nm, stream); break;
+    case 4: launch_rq_rb<DT, KP, MAT16, 4, NORM>(x, grp, 0, full, h, krot, flags, nm, stream); break;
+    case 2: launch_rq_rb<DT, KP, MAT16, 2, NORM>(x, grp, 0, full, h, krot, flags, nm, stream); break;
     default: break;
   }
   const int64_t done = rb > 1 ? full * rb : 0;   // the remaining rows, one block each
-  launch_rq_rb<DT, KP, MAT16, 1>(x, grp, done, rows - done, h, krot, flags, stream);
+  launch_rq_rb<DT, KP, MAT16, 1, NORM>(x, grp, done, rows - done, h, krot, flags, nm, stream);
+}
+
+template <int DT, bool NORM>
+void launch_rotate_quant_norm(const void* x, const pq::RotGroup& grp, int64_t rows, int h, int krot,
+                              unsigned flags, const pq::NormArgs& nm, hipStream_t stream) {
+  const bool mat16 = (flags & PQ_RQ_MATERIALIZE_FP16) != 0;
+  if (krot <= 8) {
+    if (mat16) launch_rq<DT, 8, true, NORM>(x, grp, rows, h, krot, flags, nm, stream);
+    else launch_rq<DT, 8, false, NORM>(x, grp, rows, h, krot, flags, nm, stream);
+  } else {
+    if (mat16) launch_rq<DT, 16, true, NORM>(x, grp, rows, h, krot, flags, nm, stream);
+    else launch_rq<DT, 16, false, NORM>(x, grp, rows, h, krot, flags, nm, stream);
+  }
 }
 
 template <int DT>
 void launch_rotate_quant(const void* x, const pq::RotGroup& grp, int64_t rows, int h, int krot, unsigned flags,
-                         hipStream_t stream) {
-  const bool mat16 = (flags & PQ_RQ_MATERIALIZE_FP16) != 0;
-  if (krot <= 8) {
-    if (mat16) launch_rq<DT, 8, true>(x, grp, rows, h, krot, flags, stream);
-    else launch_rq<DT, 8, false>(x, grp, rows, h, krot, flags, stream);
-  } else {
-    if (mat16) launch_rq<DT, 16, true>(x, grp, rows, h, krot, flags, stream);
-    else launch_rq<DT, 16, false>(x, grp, rows, h, krot, flags, stream);
-  }
+                         const pq::NormArgs* norm, hipStream_t stream) {
+  if (norm != nullptr) launch_rotate_quant_norm<DT, true>(x, grp, rows, h, krot, flags, *norm, stream);
+  else launch_rotate_quant_norm<DT, false>(x, grp, rows, h, krot, flags, pq::NormArgs{}, stream);
 }
 
 template <int DT>
@@ -440,20 +516,20 @@ void launch_quant(const void* x, int8_t* xq, float* xscale, int64_t rows, int h,
 
 namespace pq {
 void launch_rotate_split(const void* x, int x_dtype, const RotGroup& grp, int m, int h, int krot, unsigned flags,
-                         hipStream_t stream) {
+                         hipStream_t stream, const NormArgs* norm) {
   switch (x_dtype) {
-    case PQ_F32: launch_split_dt<PQ_F32>(x, grp, m, h, krot, flags, stream); break;
-    case PQ_F16: launch_split_dt<PQ_F16>(x, grp, m, h, krot, flags, stream); break;
-    default: launch_split_dt<PQ_BF16>(x, grp, m, h, krot, flags, stream); break;
+    case PQ_F32: launch_split_dt<PQ_F32>(x, grp, m, h, krot, flags, norm, stream); break;
+    case PQ_F16: launch_split_dt<PQ_F16>(x, grp, m, h, krot, flags, norm, stream); break;
+    default: launch_split_dt<PQ_BF16>(x, grp, m, h, krot, flags, norm, stream); break;
   }
 }
 
 void launch_rotate_quant_group(const void* x, int x_dtype, const RotGroup& grp, int64_t rows, int h, int krot,
-                               unsigned flags, hipStream_t stream) {
+                               unsigned flags, hipStream_t stream, const NormArgs* norm) {
   switch (x_dtype) {
-    case PQ_F32: launch_rotate_quant<PQ_F32>(x, grp, rows, h, krot, flags, stream); break;
-    case PQ_F16: launch_rotate_quant<PQ_F16>(x, grp, rows, h, krot, flags, stream); break;
-    default: launch_rotate_quant<PQ_BF16>(x, grp, rows, h, krot, flags, stream); break;
+    case PQ_F32: launch_rotate_quant<PQ_F32>(x, grp, rows, h, krot, flags, norm, stream); break;
+    case PQ_F16: launch_rotate_quant<PQ_F16>(x, grp, rows, h, krot, flags, norm, stream); break;
+    default: launch_rotate_quant<PQ_BF16>(x, grp, rows, h, krot, flags, norm, stream); break;
   }
 }
 }  // namespace pq

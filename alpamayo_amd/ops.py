@@ -16,6 +16,9 @@ the ``paroquant`` namespace:
   paroquant::w4a8_linear_group(x, rot_idx[], rot_cs[], scales?[], krot, wpack[], wmeta[], bias?[],
                                workspace?, input_fp16, materialize_fp16, out_dtype) -> y[]
       (1..4 linears sharing the input x, in two launches for the whole group)
+  paroquant::w4a8_linear_group_rmsnorm(x, residual?, norm_weight, eps, <the group's arguments>,
+                                       return_normed, return_sum) -> y[] (+ h) (+ x + residual)
+      (the same group behind a decoder layer's RMSNorm of x + residual, still two launches)
 
 ``pack_rotation`` (host) turns Rotation's pairs/angles into rot_idx/rot_cs.
 
@@ -53,6 +56,10 @@ _pq_lib.define("w4a8_linear(Tensor x, Tensor rot_idx, Tensor rot_cs, Tensor? sca
 _pq_lib.define("w4a8_linear_group(Tensor x, Tensor[] rot_idx, Tensor[] rot_cs, Tensor?[] scales, int krot, "
                "Tensor[] wpack, Tensor[] wmeta, Tensor?[] bias, Tensor? workspace, bool input_fp16, "
                "bool materialize_fp16, ScalarType out_dtype) -> Tensor[]")
+_pq_lib.define("w4a8_linear_group_rmsnorm(Tensor x, Tensor? residual, Tensor norm_weight, float eps, "
+               "Tensor[] rot_idx, Tensor[] rot_cs, Tensor?[] scales, int krot, Tensor[] wpack, Tensor[] wmeta, "
+               "Tensor?[] bias, Tensor? workspace, bool input_fp16, bool materialize_fp16, ScalarType out_dtype, "
+               "bool return_normed, bool return_sum) -> Tensor[]")
 
 
 # ---------------------------------------------------------------------------
@@ -434,17 +441,16 @@ def _linear_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace
 _pq_lib.impl("w4a8_linear", _linear_impl, "CUDA")
 
 
-def _linear_group_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16,
-                       materialize_fp16, out_dtype):
+def _group_members(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, out_dtype):
+    """The pq_linear_member table of a group over x [.., k], the outputs it writes, and what must stay alive."""
     dev = x.device
     count = len(wpack)
     _require(1 <= count <= _lib.MAX_GROUP, f"a group holds 1..{_lib.MAX_GROUP} linears, got {count}")
     _require(len(rot_idx) == len(rot_cs) == len(scales) == len(wmeta) == len(bias) == count,
              "every per-member list must have one entry per linear")
     _require(out_dtype in _DT, f"out_dtype must be float32/float16/bfloat16, got {out_dtype}")
-    xc = x.contiguous()
-    k = xc.size(-1)
-    m = xc.numel() // k
+    k = x.size(-1)
+    m = x.numel() // k
     members = (_lib.LinearMember * count)()
     keep, outs, bias_dt = [], [], 0
     for i in range(count):
@@ -466,23 +472,90 @@ def _linear_group_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, wor
         members[i] = _lib.LinearMember(idx.data_ptr(), cs.data_ptr(), sc.data_ptr() if sc is not None else None,
                                        wpack[i].data_ptr(), wmeta[i].data_ptr(),
                                        b.data_ptr() if b is not None else None, y.data_ptr(), n)
-    lib = _lib.load()
-    need = int(lib.pq_w4a8_linear_group_workspace_size(m, k, count))
-    scratch = None
-    if need > 0:
-        if (workspace is not None and workspace.dtype == torch.uint8 and workspace.is_contiguous()
-                and workspace.numel() >= need and workspace.data_ptr() % 256 == 0):
-            _same_device("workspace", workspace, dev)
-            scratch = workspace
-        else:
-            scratch = torch.empty(need, dtype=torch.uint8, device=dev)
+    return members, outs, keep, bias_dt, m, k
+
+
+def _group_scratch(workspace, m, k, count, dev):
+    need = int(_lib.load().pq_w4a8_linear_group_workspace_size(m, k, count))
+    if need <= 0:
+        return None
+    if (workspace is not None and workspace.dtype == torch.uint8 and workspace.is_contiguous()
+            and workspace.numel() >= need and workspace.data_ptr() % 256 == 0):
+        _same_device("workspace", workspace, dev)
+        return workspace
+    return torch.empty(need, dtype=torch.uint8, device=dev)
+
+
+def _linear_group_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16,
+                       materialize_fp16, out_dtype):
+    dev = x.device
+    xc = x.contiguous()
+    members, outs, keep, bias_dt, m, k = _group_members(xc, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
+                                                        out_dtype)
+    count = len(outs)
+    scratch = _group_scratch(workspace, m, k, count, dev)
     flags = (_lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0) | (_lib.PQ_RQ_MATERIALIZE_FP16 if materialize_fp16 else 0)
+    lib = _lib.load()
     with _DeviceGuard(dev):
         st = lib.pq_w4a8_linear_group(xc.data_ptr(), _DT[x.dtype], members, count, bias_dt, _DT[out_dtype], m, k,
                                       krot, flags, scratch.data_ptr() if scratch is not None else None,
                                       scratch.numel() if scratch is not None else 0, _stream(dev))
     _lib.check(st, "paroquant::w4a8_linear_group")
     return [y.view(*x.shape[:-1], y.size(1)) for y in outs]
+
+
+def _linear_group_rmsnorm_impl(x, residual, norm_weight, eps, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
+                               workspace, input_fp16, materialize_fp16, out_dtype, return_normed, return_sum):
+    dev = x.device
+    _require(x.dtype in _DT, f"x must be float32/float16/bfloat16, got {x.dtype}")
+    xc = x.contiguous()
+    k = xc.size(-1)
+    _require(norm_weight.dtype == x.dtype and norm_weight.numel() == k,
+             f"norm_weight must hold {k} values of x's dtype {x.dtype}")
+    _same_device("norm_weight", norm_weight, dev)
+    w = norm_weight.contiguous()
+    res = None
+    if residual is not None:
+        _require(residual.shape == x.shape and residual.dtype == x.dtype, "residual must match x's shape and dtype")
+        _same_device("residual", residual, dev)
+        res = residual.contiguous()
+    _require(not return_sum or res is not None, "return_sum needs a residual")
+    members, outs, keep, bias_dt, m, _ = _group_members(xc, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
+                                                        out_dtype)
+    count = len(outs)
+    h = torch.empty_like(xc) if return_normed else None
+    sm = torch.empty_like(xc) if return_sum else None
+    scratch = _group_scratch(workspace, m, k, count, dev)
+    flags = (_lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0) | (_lib.PQ_RQ_MATERIALIZE_FP16 if materialize_fp16 else 0)
+    lib = _lib.load()
+    with _DeviceGuard(dev):
+        st = lib.pq_w4a8_linear_group_rmsnorm(
+            xc.data_ptr(), res.data_ptr() if res is not None else None, w.data_ptr(), float(eps),
+            h.data_ptr() if h is not None else None, sm.data_ptr() if sm is not None else None, _DT[x.dtype],
+            members, count, bias_dt, _DT[out_dtype], m, k, krot, flags,
+            scratch.data_ptr() if scratch is not None else None, scratch.numel() if scratch is not None else 0,
+            _stream(dev))
+    _lib.check(st, "paroquant::w4a8_linear_group_rmsnorm")
+    res_out = [y.view(*x.shape[:-1], y.size(1)) for y in outs]
+    if h is not None:
+        res_out.append(h.view(x.shape))
+    if sm is not None:
+        res_out.append(sm.view(x.shape))
+    return res_out
+
+
+_pq_lib.impl("w4a8_linear_group_rmsnorm", _linear_group_rmsnorm_impl, "CUDA")
+
+
+@torch.library.register_fake("paroquant::w4a8_linear_group_rmsnorm")
+def _linear_group_rmsnorm_fake(x, residual, norm_weight, eps, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
+                               workspace, input_fp16, materialize_fp16, out_dtype, return_normed, return_sum):
+    outs = [x.new_empty((*x.shape[:-1], w.size(0) * 16), dtype=out_dtype) for w in wpack]
+    if return_normed:
+        outs.append(torch.empty_like(x))
+    if return_sum:
+        outs.append(torch.empty_like(x))
+    return outs
 
 
 _pq_lib.impl("w4a8_linear_group", _linear_group_impl, "CUDA")

@@ -123,7 +123,12 @@ class SharedInputRotateLinears(nn.Module):
     def _rotate_linears(self):
         return [m.rotate_linear if self.bf16_inputs else m for m in self.members]
 
-    def forward(self, x: torch.Tensor):
+    def forward(self, x: torch.Tensor, norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                residual: torch.Tensor | None = None, return_normed: bool = False, return_sum: bool = False):
+        """The members' outputs on x, or, with ``norm_weight``, on the decoder layer's RMSNorm of
+        x (+ residual): h = weight * (s * rsqrt(mean(s^2) + eps)) with s = x + residual, in x's dtype
+        (Qwen3VLTextRMSNorm.forward, modeling_qwen3_vl.py:354-359), computed inside the group's
+        rotation launch.  ``return_normed`` / ``return_sum`` append h / s to the outputs."""
         rls = self._rotate_linears()
         for rl in rls:
             rl.qlinear._check_loaded()
@@ -133,11 +138,16 @@ class SharedInputRotateLinears(nn.Module):
         need = _ops.linear_group_workspace_bytes(x.numel() // k, k, len(rls))
         if self.workspace.numel() < need or self.workspace.device != x.device:
             self.workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
-        outs = torch.ops.paroquant.w4a8_linear_group(
-            x, [rl.rotation.rot_idx for rl in rls], [rl.rotation.rot_cs for rl in rls],
-            [rl.rotation.scales_f32 for rl in rls], rls[0].rotation.krot, [rl.qlinear.qweight for rl in rls],
-            [rl.qlinear.scales for rl in rls], [rl.qlinear.bias for rl in rls], self.workspace, self.bf16_inputs,
-            True, x.dtype)
+        args = ([rl.rotation.rot_idx for rl in rls], [rl.rotation.rot_cs for rl in rls],
+                [rl.rotation.scales_f32 for rl in rls], rls[0].rotation.krot, [rl.qlinear.qweight for rl in rls],
+                [rl.qlinear.scales for rl in rls], [rl.qlinear.bias for rl in rls], self.workspace,
+                self.bf16_inputs, True, x.dtype)
+        if norm_weight is None:
+            if residual is not None or return_normed or return_sum:
+                raise ValueError("residual / return_normed / return_sum need norm_weight")
+            return tuple(torch.ops.paroquant.w4a8_linear_group(x, *args))
+        outs = torch.ops.paroquant.w4a8_linear_group_rmsnorm(x, residual, norm_weight.to(x.dtype), float(eps), *args,
+                                                             return_normed, return_sum)
         return tuple(outs)
 
 

@@ -185,6 +185,23 @@ int pq_w4a8_linear_group(const void* x, int x_dtype, const pq_linear_member* mem
                          int y_dtype, int64_t m, int64_t k, int krot, unsigned flags, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* pq_w4a8_linear_group behind a decoder layer's RMSNorm, in the same two
+ * launches: the members read h instead of x, where
+ *   s = x + residual (rounded to x's dtype; s = x when residual is NULL),
+ *   h = round(w * round(s * rsqrt(mean(s^2) + eps))),
+ * both roundings to x's dtype, mean and rsqrt in float32.  norm_weight: [k]
+ * in x's dtype.  When set, h_out and sum_out ([m, k], x's dtype) receive h
+ * and s (sum_out needs a residual).  residual must be 16-byte aligned.
+ * Reference: Qwen3VLTextRMSNorm.forward (src/alpamayo_r1/models/qwen3_vl/
+ * modeling_qwen3_vl.py:354-359) in front of the ParoQuant linears that read
+ * its output (q/k/v after input_layernorm, gate/up after
+ * post_attention_layernorm; paroquant_marlin_w4a8.py:59-65 per linear).
+ * No counterpart of the fusion itself in the reference. */
+int pq_w4a8_linear_group_rmsnorm(const void* x, const void* residual, const void* norm_weight, float eps,
+                                 void* h_out, void* sum_out, int x_dtype, const pq_linear_member* members,
+                                 int count, int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot,
+                                 unsigned flags, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,6 +17,8 @@ the path so that the HIP kernels can be checked against it:
                (paroquant_marlin_w4a8.py:59-65, rotation_linear.py:120-124)
   weightquant.py  offline asymmetric uint4 weight quantizer
                (quantization_utils.py:18-73)
+  rmsnorm.py   the decoder layer's RMSNorm (+ residual add) in front of a
+               shared-input group (modeling_qwen3_vl.py:354-359)
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import this package, and only as the checker: the product
@@ -33,6 +35,9 @@ Pinning status of each function (how each is checked, see tests/test_oracle_*.py
               vLLM is not installed and no reference test pins it.
   gemm        exact int64 brute force of the per-group partials, and a
               float64 dequant_awq matmul for the epilogue.
+  rmsnorm     torch.nn.functional.rms_norm (the library routine of the same
+              formula) on float32 inputs, scale invariance, unit-weight
+              mean(h^2) = 1, eps dominance on tiny rows.
   packing     pack_intweight / pseudo_quantize_tensor against golden vectors
               written by importing the reference's own functions in the
               build container (tests/golden/make_golden.py); AWQ order

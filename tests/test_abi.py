@@ -134,3 +134,24 @@ def test_status_names_and_error_type():
     with pytest.raises(_lib.PQError, match="PQ_ERR_ARG"):
         _lib.check(1, "x")
     _lib.check(0, "x")
+
+
+def test_linear_group_rmsnorm_argument_checks():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    mem = (_lib.LinearMember * 1)()
+    mem[0] = _lib.LinearMember(256, 256, None, 256, 256, None, 256, 64)
+    args = dict(count=1, bias_dtype=0, y_dtype=2, m=1, k=4096, krot=8, flags=3, ws=p, wsb=1 << 20, stream=None)
+
+    def call(x=p, res=None, w=p, eps=1e-6, h=None, s=None, dt=2, **kw):
+        a = dict(args, **kw)
+        return lib.pq_w4a8_linear_group_rmsnorm(x, res, w, eps, h, s, dt, mem, a["count"], a["bias_dtype"],
+                                                a["y_dtype"], a["m"], a["k"], a["krot"], a["flags"], a["ws"],
+                                                a["wsb"], a["stream"])
+
+    assert call(eps=-1.0) == 1 and "eps" in _err(lib)
+    assert call(w=None) == 1 and "norm_weight" in _err(lib)
+    assert call(res=ctypes.c_void_p(258)) == 1 and "residual" in _err(lib)
+    assert call(s=p) == 1 and "sum_out" in _err(lib)
+    assert call(dt=7) == 2
+    assert call(m=0) == 0   # empty input: no-op
