@@ -57,15 +57,6 @@ namespace {
 // the int8 codes of all M rows into LDS (row stride K + 16 bytes, so the 16
 // rows of an A fragment hit distinct banks) and reads A from there.  The
 // first batch of weight loads is issued before that prologue.
-// Barrier for LDS hand-offs only: the wave's LDS operations complete, then
-// s_barrier.  Unlike __syncthreads() it does not wait for the wave's global
-// stores (vmcnt), which may stay in flight.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 constexpr int kSkinnyRows = 16;
 
 // The member of a group that owns workgroup tile `unit` (members own
@@ -333,31 +324,6 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
 constexpr int kPfStages = 3;
 constexpr int kPfGroupM = 4;   // tile rows walked together by one XCD's run of tiles
 constexpr int kPfBStride = 1024 + 128;
-
-__device__ __forceinline__ int pf_swz(int line) { return (line >> 1) & 7; }
-
-// Global -> LDS copies of 16 (4) bytes per lane: lane l's bytes land at LDS
-// address lds + 16*l (4*l).  Written as inline asm on purpose: the compiler
-// would otherwise treat every later LDS read as possibly aliasing the copy
-// and wait for all outstanding loads (vmcnt(0)) before it, which serializes
-// the stage ring.  The kernels wait for these loads explicitly (wait_vmcnt).
-// M0 is used only here.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
-}
-__device__ __forceinline__ void lds_copy16(const void* gsrc, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(gsrc) : "memory", "m0");
-}
-__device__ __forceinline__ void lds_copy4(const void* gsrc, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(gsrc) : "memory", "m0");
-}
-
-// s_waitcnt with vmcnt(n), any lgkmcnt/expcnt (gfx9 immediate encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 template <int BM, int BN, int WM, int WN, bool PARTIALS>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(

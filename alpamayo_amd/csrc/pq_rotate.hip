@@ -335,11 +335,13 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
         *reinterpret_cast<uint4*>(xrot + (row0 + r) * h + c8) = o;
       }
     }
-    uint2 o;
-    o.x = quant4(f[0], f[1], f[2], f[3], inv);
-    o.y = quant4(f[4], f[5], f[6], f[7], inv);
-    *reinterpret_cast<uint2*>(xq + (row0 + r) * h + c8) = o;
-    if (c8 == 0) xscale[row0 + r] = am / 127.0f;
+    if (xq != nullptr) {   // null: only the fp16 rows are wanted (the W4A16 linear)
+      uint2 o;
+      o.x = quant4(f[0], f[1], f[2], f[3], inv);
+      o.y = quant4(f[4], f[5], f[6], f[7], inv);
+      *reinterpret_cast<uint2*>(xq + (row0 + r) * h + c8) = o;
+      if (c8 == 0) xscale[row0 + r] = am / 127.0f;
+    }
   }
 }
 

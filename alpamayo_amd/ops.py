@@ -60,6 +60,10 @@ _pq_lib.define("w4a8_linear_group_rmsnorm(Tensor x, Tensor? residual, Tensor nor
                "Tensor[] rot_idx, Tensor[] rot_cs, Tensor?[] scales, int krot, Tensor[] wpack, Tensor[] wmeta, "
                "Tensor?[] bias, Tensor? workspace, bool input_fp16, bool materialize_fp16, ScalarType out_dtype, "
                "bool return_normed, bool return_sum) -> Tensor[]")
+_pq_lib.define("w4a16_prepack(Tensor awq_qweight, Tensor scales, Tensor scaled_zeros) -> (Tensor, Tensor)")
+_pq_lib.define("w4a16_gemm(Tensor x, Tensor wpack, Tensor wmeta, Tensor? bias, ScalarType out_dtype) -> Tensor")
+_pq_lib.define("w4a16_linear(Tensor x, Tensor rot_idx, Tensor rot_cs, Tensor? scales, int krot, Tensor wpack, "
+               "Tensor wmeta, Tensor? bias, Tensor? workspace, bool input_fp16, ScalarType out_dtype) -> Tensor")
 
 
 # ---------------------------------------------------------------------------
@@ -575,4 +579,121 @@ def linear_group_workspace_bytes(m: int, k: int, count: int) -> int:
 @torch.library.register_fake("paroquant::w4a8_linear")
 def _linear_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16, materialize_fp16,
                  out_dtype):
+    return x.new_empty((*x.shape[:-1], wpack.size(0) * 16), dtype=out_dtype)
+
+
+# ---------------------------------------------------------------------------
+# paroquant::w4a16_prepack / w4a16_gemm / w4a16_linear (WQLinear's W4A16 path)
+# ---------------------------------------------------------------------------
+
+def _w16_bias(bias, n, dev):
+    if bias is None:
+        return None
+    _require(bias.dtype in _DT and bias.numel() == n, f"bias must hold {n} float values")
+    _same_device("bias", bias, dev)
+    return bias.contiguous()
+
+
+def _w16_prepack_impl(awq_qweight, scales, scaled_zeros):
+    dev = awq_qweight.device
+    _require(awq_qweight.dtype == torch.int32 and awq_qweight.dim() == 2, "awq_qweight must be int32 [K, N/8]")
+    k, n = awq_qweight.size(0), awq_qweight.size(1) * 8
+    _require(k % 128 == 0 and n % 16 == 0, f"K={k} must be a multiple of 128 and N={n} of 16")
+    g = k // 128
+    for name, t in (("scales", scales), ("scaled_zeros", scaled_zeros)):
+        _require(t.dtype == torch.float16 and tuple(t.shape) == (g, n),
+                 f"{name} must be float16 [{g}, {n}], got {t.dtype} {tuple(t.shape)}")
+        _same_device(name, t, dev)
+    qw, sc, sz = awq_qweight.contiguous(), scales.contiguous(), scaled_zeros.contiguous()
+    wpack = torch.empty((n // 16, g, 64, 16), dtype=torch.uint8, device=dev)
+    wmeta = torch.empty((n // 16, g, 16), dtype=torch.int32, device=dev)
+    lib = _lib.load()
+    with _DeviceGuard(dev):
+        st = lib.pq_w4a16_prepack(qw.data_ptr(), sc.data_ptr(), sz.data_ptr(), wpack.data_ptr(), wmeta.data_ptr(), k,
+                                  n, 128, _stream(dev))
+    _lib.check(st, "paroquant::w4a16_prepack")
+    return wpack, wmeta
+
+
+_pq_lib.impl("w4a16_prepack", _w16_prepack_impl, "CUDA")
+
+
+@torch.library.register_fake("paroquant::w4a16_prepack")
+def _w16_prepack_fake(awq_qweight, scales, scaled_zeros):
+    k, n = awq_qweight.size(0), awq_qweight.size(1) * 8
+    return (awq_qweight.new_empty((n // 16, k // 128, 64, 16), dtype=torch.uint8),
+            awq_qweight.new_empty((n // 16, k // 128, 16), dtype=torch.int32))
+
+
+def _w16_gemm_impl(x, wpack, wmeta, bias, out_dtype):
+    dev = x.device
+    n, k = _check_weights(wpack, wmeta, dev)
+    _require(x.dtype == torch.float16, f"x must be float16 (the W4A16 kernels take fp16 activations), got {x.dtype}")
+    _require(x.size(-1) == k, f"x has {x.size(-1)} features, the weights expect {k}")
+    _require(out_dtype in _DT, f"out_dtype must be float32/float16/bfloat16, got {out_dtype}")
+    xc = x.contiguous()
+    m = xc.numel() // k
+    y = torch.empty((m, n), dtype=out_dtype, device=dev)
+    bias = _w16_bias(bias, n, dev)
+    lib = _lib.load()
+    with _DeviceGuard(dev):
+        st = lib.pq_w4a16_gemm(xc.data_ptr(), wpack.data_ptr(), wmeta.data_ptr(),
+                               bias.data_ptr() if bias is not None else None,
+                               _DT[bias.dtype] if bias is not None else 0, y.data_ptr(), _DT[out_dtype], m, n, k, 128,
+                               _stream(dev))
+    _lib.check(st, "paroquant::w4a16_gemm")
+    return y.view(*x.shape[:-1], n)
+
+
+_pq_lib.impl("w4a16_gemm", _w16_gemm_impl, "CUDA")
+
+
+@torch.library.register_fake("paroquant::w4a16_gemm")
+def _w16_gemm_fake(x, wpack, wmeta, bias, out_dtype):
+    return x.new_empty((*x.shape[:-1], wpack.size(0) * 16), dtype=out_dtype)
+
+
+def w4a16_linear_workspace_bytes(m: int, k: int) -> int:
+    return int(_lib.load().pq_w4a16_linear_workspace_size(m, k))
+
+
+def _w16_linear_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16, out_dtype):
+    dev = x.device
+    n, k = _check_weights(wpack, wmeta, dev)
+    _require(x.size(-1) == k, f"x has {x.size(-1)} features, the weights expect {k}")
+    _check_rot_params(x, rot_idx, rot_cs, scales, krot)
+    _require(out_dtype in _DT, f"out_dtype must be float32/float16/bfloat16, got {out_dtype}")
+    xc = x.contiguous()
+    m = xc.numel() // k
+    y = torch.empty((m, n), dtype=out_dtype, device=dev)
+    bias = _w16_bias(bias, n, dev)
+    lib = _lib.load()
+    need = int(lib.pq_w4a16_linear_workspace_size(m, k))
+    scratch = None
+    if need > 0:
+        if (workspace is not None and workspace.dtype == torch.uint8 and workspace.is_contiguous()
+                and workspace.numel() >= need and workspace.data_ptr() % 256 == 0):
+            _same_device("workspace", workspace, dev)
+            scratch = workspace
+        else:
+            scratch = torch.empty(need, dtype=torch.uint8, device=dev)
+    flags = _lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0
+    idx, cs = rot_idx.contiguous(), rot_cs.contiguous()
+    sc = scales.contiguous() if scales is not None else None
+    with _DeviceGuard(dev):
+        st = lib.pq_w4a16_linear(xc.data_ptr(), _DT[x.dtype], idx.data_ptr(), cs.data_ptr(),
+                                 sc.data_ptr() if sc is not None else None, wpack.data_ptr(), wmeta.data_ptr(),
+                                 bias.data_ptr() if bias is not None else None,
+                                 _DT[bias.dtype] if bias is not None else 0, y.data_ptr(), _DT[out_dtype], m, n, k,
+                                 krot, flags, scratch.data_ptr() if scratch is not None else None,
+                                 scratch.numel() if scratch is not None else 0, _stream(dev))
+    _lib.check(st, "paroquant::w4a16_linear")
+    return y.view(*x.shape[:-1], n)
+
+
+_pq_lib.impl("w4a16_linear", _w16_linear_impl, "CUDA")
+
+
+@torch.library.register_fake("paroquant::w4a16_linear")
+def _w16_linear_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16, out_dtype):
     return x.new_empty((*x.shape[:-1], wpack.size(0) * 16), dtype=out_dtype)

@@ -5,10 +5,14 @@ names, shapes and dtypes (``qweight`` int16 [N/4, K], ``scales`` and
 ``scaled_zeros`` [calculate_zeros_width(K)*8, N], optional ``bias``), so
 ParoQuant state dicts load unchanged.
 
-``WQLinear.forward`` is the reference's W4A16 AWQ gemv/gemm path
-(qmodule.py:207-232), which calls the un-vendored ``torch.ops.awq`` kernels;
-this build converts WQLinear layers to ``MarlinW4A8Linear`` before inference
-(``convert_model_to_marlin_w4a8``) and does not implement W4A16.
+``WQLinear.forward`` is the reference's W4A16 path (qmodule.py:207-232),
+there the un-vendored ``torch.ops.awq.gemv`` / ``gemm`` kernels; here
+``paroquant::w4a16_gemm``: fp16 activations times the weights
+fp16(q * scales + scaled_zeros) (one rounding), float32 accumulation, plus
+bias.  ``prepare()`` derives the kernel's packed weights (non-persistent
+buffers ``w16_pack`` / ``w16_meta``, so state-dict keys are unchanged); the
+first forward after the checkpoint buffers change re-derives them (call
+``prepare()`` ahead of a graph capture).
 """
 
 from __future__ import annotations
@@ -102,6 +106,9 @@ class WQLinear(nn.Module):
             self.register_buffer("bias", torch.zeros((out_features), dtype=dtype))
         else:
             self.bias = None
+        self.register_buffer("w16_pack", torch.empty(0, dtype=torch.uint8), persistent=False)
+        self.register_buffer("w16_meta", torch.empty(0, dtype=torch.int32), persistent=False)
+        self._w16_src = None
 
     @classmethod
     def from_linear(cls, linear, w_bit, group_size, init_only=False, scales=None, zeros=None):
@@ -129,11 +136,34 @@ class WQLinear(nn.Module):
         q.scaled_zeros = scaled_zeros.transpose(1, 0).contiguous()
         return q
 
+    def _w16_source(self):
+        return tuple((t.data_ptr(), t._version, t.device) for t in (self.qweight, self.scales, self.scaled_zeros))
+
+    @property
+    def prepared(self) -> bool:
+        return self.w16_pack.numel() > 0 and self._w16_src == self._w16_source()
+
+    @torch.no_grad()
+    def prepare(self) -> None:
+        """(Re)derive the W4A16 kernel's packed weights from qweight / scales / scaled_zeros."""
+        from .paroquant_marlin_w4a8 import pack_awq_int32
+
+        if self.group_size != 128:
+            raise NotImplementedError(f"the W4A16 kernels take group_size 128, not {self.group_size}")
+        n, k = self.out_features, self.in_features
+        g = k // self.group_size
+        codes = unpack_intweight(self.qweight, n, k)
+        awq = pack_awq_int32(codes.t().contiguous())
+        self.w16_pack, self.w16_meta = torch.ops.paroquant.w4a16_prepack(
+            awq, self.scales[:g].to(torch.float16).contiguous(), self.scaled_zeros[:g].to(torch.float16).contiguous())
+        self._w16_src = self._w16_source()
+
     @torch.no_grad()
     def forward(self, inputs):
-        raise NotImplementedError(
-            "WQLinear.forward is the W4A16 AWQ path (external torch.ops.awq kernels), which this build does not "
-            "provide; convert the layer with convert_wqlinear_layer / convert_model_to_marlin_w4a8")
+        """inputs: fp16 [..., K] -> fp16 [..., N] (qmodule.py:207-232)."""
+        if not self.prepared:
+            self.prepare()
+        return torch.ops.paroquant.w4a16_gemm(inputs, self.w16_pack, self.w16_meta, self.bias, inputs.dtype)
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, bias={self.bias is not None}, "

@@ -16,7 +16,9 @@ rotate+quant kernels (non-persistent, so state-dict keys are unchanged):
                                       in float64 on the host and rounded once
   scales_f32 float32 [K]              channel scales
 and ``RotateLinearInt4.forward`` runs rotation + int8 quant + GEMM through
-``paroquant::w4a8_linear`` when its qlinear is a ``MarlinW4A8Linear``.
+``paroquant::w4a8_linear`` when its qlinear is a ``MarlinW4A8Linear``, and
+rotation + W4A16 GEMM through ``paroquant::w4a16_linear`` when it is a
+``WQLinear``.
 """
 
 from __future__ import annotations
@@ -139,6 +141,15 @@ class RotateLinearInt4(nn.Module):
         if isinstance(self.qlinear, MarlinW4A8Linear):
             # rotation (fp16 result) -> per-token int8 -> W4A8 GEMM, fused.
             return self.qlinear.forward_rotated(x, self.rotation, input_fp16=False, out_dtype=x.dtype)
+        if isinstance(self.qlinear, WQLinear):
+            # rotation (fp16 result) -> W4A16 GEMM behind one entry point.
+            q, rot = self.qlinear, self.rotation
+            if not q.prepared:
+                q.prepare()
+            if not rot.prepared:
+                rot.prepare()
+            return torch.ops.paroquant.w4a16_linear(x, rot.rot_idx, rot.rot_cs, rot.scales_f32, rot.krot, q.w16_pack,
+                                                    q.w16_meta, q.bias, None, False, x.dtype)
         x = self.rotation(x)
         return self.qlinear(x)
 

@@ -89,6 +89,13 @@ def weights(N: int, K: int, gen: torch.Generator, device="cpu", keep_codes=False
     return Weights(qw, scales, qz, codes.to(torch.uint8) if keep_codes else None, zeros)
 
 
+def w16_scales(w: Weights) -> tuple[torch.Tensor, torch.Tensor]:
+    """WQLinear's fp16 (scales, scaled_zeros) [G, N] for the same weights: scaled_zeros = -(s * z),
+    rounded to fp16 as WQLinear.from_linear stores it (qmodule.py:199-203)."""
+    sz = (-(w.awq_scales.float() * w.zeros.float())).to(torch.float16)
+    return w.awq_scales, sz
+
+
 @dataclass
 class LinearSpec:
     name: str
@@ -122,3 +129,25 @@ def build_module(spec: LinearSpec, device="cuda"):
 
 def ragged_lengths(n_requests: int, gen: torch.Generator, lo: int = 1, hi: int = 512) -> list[int]:
     return [int(v) for v in torch.randint(lo, hi + 1, (n_requests,), generator=gen)]
+
+
+def build_w16_module(spec: LinearSpec, device="cuda"):
+    """RotateLinearInt4(..., qlinear=WQLinear) on `device`, the W4A16 form of the same layer (needs the codes)."""
+    from .quantization import RotateLinearInt4
+    from .quantization.qmodule import pack_intweight
+
+    if spec.w.codes is None:
+        raise ValueError("build_w16_module needs a spec made with keep_codes=True")
+    rl = RotateLinearInt4(spec.K, spec.N, bias=False, dtype=torch.float16,
+                          rotation_angles=spec.theta.to(device), rotation_pairs=spec.pairs.to(device),
+                          channel_scales=spec.channel_scales.to(device))
+    rl = rl.to(device)
+    q = rl.qlinear
+    G = spec.K // GROUP
+    s, sz = w16_scales(spec.w)
+    q.qweight.copy_(pack_intweight(spec.w.codes.to(torch.int32)).to(device))
+    q.scales[:G].copy_(s.to(device))
+    q.scaled_zeros[:G].copy_(sz.to(device))
+    q.prepare()
+    rl.rotation.prepare()
+    return rl

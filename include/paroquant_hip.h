@@ -29,6 +29,12 @@
  *                        rotation::rotate -> MarlinW4A8Linear.forward
  *                        (paroquant_marlin_w4a8.py:59-65, 314-333;
  *                        rotation_linear.py:120-124)
+ *   pq_w4a16_gemm        torch.ops.awq.gemv / torch.ops.awq.gemm behind
+ *                        WQLinear.forward (qmodule.py:207-232)
+ *   pq_w4a16_prepack     the weight preparation those kernels need
+ *   pq_w4a16_linear      RotateLinearInt4.forward with a WQLinear:
+ *                        rotation::rotate -> WQLinear.forward
+ *                        (rotation_linear.py:136-139)
  */
 #ifndef PAROQUANT_HIP_H
 #define PAROQUANT_HIP_H
@@ -201,6 +207,44 @@ int pq_w4a8_linear_group_rmsnorm(const void* x, const void* residual, const void
                                  void* h_out, void* sum_out, int x_dtype, const pq_linear_member* members,
                                  int count, int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot,
                                  unsigned flags, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- W4A16 (fp16 activations, no activation quant) ---- */
+
+/* Repack WQLinear weights for pq_w4a16_gemm: awq_qweight int32 [k, n/8] (the
+ * codes in AWQ order, as unpack_wqlinear_qweight + pack_awq_int32 give them,
+ * paroquant_marlin_w4a8.py:95-164), scales and scaled_zeros fp16 [k/128, n]
+ * (the first k/128 rows of WQLinear's buffers).  wpack: the same layout as
+ * pq_w4a8_prepack's; wmeta: uint32 [n/16, k/128, 16] = s | sz << 16.
+ * Reference: the WQLinear buffers read by torch.ops.awq.gemv / gemm
+ * (qmodule.py:113-147, 207-232). */
+int pq_w4a16_prepack(const int32_t* awq_qweight, const uint16_t* scales, const uint16_t* scaled_zeros,
+                     uint8_t* wpack, uint32_t* wmeta, int64_t k, int64_t n, int group_size, void* stream);
+
+/* y[m, n] = sum_k x[m, k] * w[k, n] (+ bias[n]), written as y_dtype, with
+ * w = fp16(q * s + sz) (one rounding) and float32 accumulation.  x: fp16
+ * [m, k], 16-byte aligned; wpack/wmeta from pq_w4a16_prepack; bias: [n] of
+ * bias_dtype or NULL.  group_size == 128, k % 128 == 0, n % 16 == 0.
+ * Reference: WQLinear.forward (qmodule.py:207-232): torch.ops.awq.gemv for
+ * fewer than 8 rows, torch.ops.awq.gemm otherwise, then + bias; weight
+ * semantics of dequant_wqlinear (paroquant_marlin_w4a8.py:216-224). */
+int pq_w4a16_gemm(const void* x, const uint8_t* wpack, const uint32_t* wmeta, const void* bias, int bias_dtype,
+                  void* y, int y_dtype, int64_t m, int64_t n, int64_t k, int group_size, void* stream);
+
+/* Bytes of scratch pq_w4a16_linear needs between its two kernels: the
+ * rotated fp16 rows, 2*m*k rounded up to 256, plus 4*m*(k/128) bytes when
+ * m <= 16.  Its content does not matter. */
+size_t pq_w4a16_linear_workspace_size(int64_t m, int64_t k);
+
+/* y = pq_w4a16_gemm of the rotation of x, rounded to fp16: x [m, k]
+ * (x_dtype f32/f16/bf16), rotation operands as for pq_w4a8_linear,
+ * flags 0 or PQ_RQ_INPUT_FP16 (round x to fp16 first).  Two launches.
+ * Reference: RotateLinearInt4.forward with a WQLinear qlinear
+ * (rotation_linear.py:136-139): rotation::rotate (rotation.cu:456-493),
+ * then WQLinear.forward (qmodule.py:207-232). */
+int pq_w4a16_linear(const void* x, int x_dtype, const uint32_t* rot_idx, const float* rot_cs, const float* scales,
+                    const uint8_t* wpack, const uint32_t* wmeta, const void* bias, int bias_dtype, void* y,
+                    int y_dtype, int64_t m, int64_t n, int64_t k, int krot, unsigned flags, void* workspace,
+                    size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -19,6 +19,8 @@ the path so that the HIP kernels can be checked against it:
                (quantization_utils.py:18-73)
   rmsnorm.py   the decoder layer's RMSNorm (+ residual add) in front of a
                shared-input group (modeling_qwen3_vl.py:354-359)
+  w4a16.py     the W4A16 linear: WQLinear.forward (qmodule.py:207-232) and
+               RotateLinearInt4 over it (rotation_linear.py:136-139)
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import this package, and only as the checker: the product
@@ -38,6 +40,11 @@ Pinning status of each function (how each is checked, see tests/test_oracle_*.py
   rmsnorm     torch.nn.functional.rms_norm (the library routine of the same
               formula) on float32 inputs, scale invariance, unit-weight
               mean(h^2) = 1, eps dominance on tiny rows.
+  w4a16       the fp16 weights against the reference's dequant_wqlinear
+              formula (float32, exact) rounded once, against dequant_awq
+              when sz = -s*z is representable, and a brute-force loop for
+              the GEMM.  The external kernels' accumulation order and
+              rounding are parity unpinned (not in the reference tree).
   packing     pack_intweight / pseudo_quantize_tensor against golden vectors
               written by importing the reference's own functions in the
               build container (tests/golden/make_golden.py); AWQ order

@@ -155,3 +155,40 @@ def test_linear_group_rmsnorm_argument_checks():
     assert call(s=p) == 1 and "sum_out" in _err(lib)
     assert call(dt=7) == 2
     assert call(m=0) == 0   # empty input: no-op
+
+
+def test_w4a16_argument_checks():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+
+    def gemm(x=p, m=4, n=64, k=256, gs=128, yd=2):
+        return lib.pq_w4a16_gemm(x, p, p, None, 0, p, yd, m, n, k, gs, None)
+
+    assert gemm(gs=64) == 2 and "group_size" in _err(lib)
+    assert gemm(n=60) == 1
+    assert gemm(k=200) == 1
+    assert gemm(yd=9) == 2
+    assert gemm(x=ctypes.c_void_p(258)) == 1 and "aligned" in _err(lib)
+    assert gemm(x=None) == 1 and "null" in _err(lib)
+    assert gemm(m=1 << 20, k=1 << 11) == 1   # 2*m*k reaches 2^31
+    assert gemm(m=0) == 0                     # empty input: no-op
+    assert lib.pq_w4a16_prepack(p, p, p, p, p, 256, 64, 64, None) == 2
+    assert lib.pq_w4a16_prepack(p, p, p, p, p, 100, 64, 128, None) == 1
+    assert lib.pq_w4a16_prepack(p, None, p, p, p, 256, 64, 128, None) == 1
+
+    def linear(m=1, k=4096, krot=8, flags=0, ws=None, wsb=0, xd=1):
+        return lib.pq_w4a16_linear(p, xd, p, p, None, p, p, None, 0, p, 1, m, 4096, k, krot, flags, ws, wsb, None)
+
+    assert linear(krot=0) == 2
+    assert linear(flags=2) == 1 and "flags" in _err(lib)   # the fp16 rounding of the rotation is implied
+    assert linear(xd=5) == 2
+    assert linear(k=32768) == 1
+    assert linear(m=0) == 0
+    need1 = lib.pq_w4a16_linear_workspace_size(1, 4096)
+    assert need1 == 2 * 4096 + 4 * 32                       # fp16 row + the split rotation's group maxima
+    need64 = lib.pq_w4a16_linear_workspace_size(64, 4096)
+    assert need64 == 64 * 4096 * 2
+    assert lib.pq_w4a16_linear_workspace_size(0, 4096) == 0
+    assert linear(m=64) == 4 and "workspace" in _err(lib)
+    assert linear(m=64, ws=p, wsb=need64 - 1) == 4
+    assert linear(m=64, ws=ctypes.c_void_p(272), wsb=need64) == 4
