@@ -372,4 +372,32 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// ---------------------------------------------------------------------------
+// OCP MX (v1.0) MXFP4: blocks of 32 elements share an E8M0 scale 2^e with
+// e = floor(log2(amax)) - 2 (2 = the largest exponent of E2M1), clamped to
+// [-127, 127]; each element v / 2^e goes to the E2M1 grid {0, 0.5, 1, 1.5,
+// 2, 3, 4, 6} by round-to-nearest-even, saturating at 6, sign kept (NaN
+// elements: code 0; their block's scale byte is 0xFF).
+// ---------------------------------------------------------------------------
+// Shared exponent of a block from its absmax (0, subnormal: -127; Inf: 126).
+__device__ __forceinline__ int mx_shared_exp(float amax) {
+  const int ef = static_cast<int>((__float_as_uint(amax) >> 23) & 0xffu);   // biased exponent
+  const int e = ef - 127 - 2;                                               // ef = 0 gives e < -127
+  return e < -127 ? -127 : e;
+}
+// 2^-e as a float (e in [-127, 126]).
+__device__ __forceinline__ float mx_inv_scale(int e) { return __uint_as_float(static_cast<uint32_t>(127 - e) << 23); }
+// E2M1 code of y = v / 2^e: magnitude index = number of grid midpoints below
+// |y|, a midpoint counting when passed (>) or, for the ties that round up to
+// an even code (0.75, 1.75, 3.5), when reached (>=).
+__device__ __forceinline__ uint32_t mx_e2m1(float y) {
+  const float a = fabsf(y);
+  const uint32_t c = static_cast<uint32_t>(a > 0.25f) + static_cast<uint32_t>(a >= 0.75f) +
+                     static_cast<uint32_t>(a > 1.25f) + static_cast<uint32_t>(a >= 1.75f) +
+                     static_cast<uint32_t>(a > 2.5f) + static_cast<uint32_t>(a >= 3.5f) +
+                     static_cast<uint32_t>(a > 5.0f);
+  const uint32_t sign = (__float_as_uint(y) >> 28) & 8u;
+  return c | (y == y ? sign : 0u);   // a NaN element is code 0 (its block's scale is NaN)
+}
+
 }  // namespace pqd

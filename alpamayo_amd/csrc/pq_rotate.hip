@@ -31,9 +31,15 @@ constexpr int kRotRows = 4;   // rows per workgroup of the plain rotation kernel
 // tile lives in LDS; pairs are read per layer and masked to the group so a
 // bad index can never address outside the tile.
 // ---------------------------------------------------------------------------
-template <int DT, int G, bool SCALE>
+//
+// MX: instead of the rotated values, their OCP MXFP4 quantization (fused
+// rotate + quant): y receives the E2M1 codes [rows][h/2] (element 2i in the
+// low nibble of byte i) and sc the E8M0 scales [rows][h/32] (0xFF when the
+// block holds a NaN).  Thread t quantizes 8 channels of tile row t/16; the
+// 4 threads of a 32-channel block exchange their absmax by lane shuffles.
+template <int DT, int G, bool SCALE, bool MX>
 __global__ __launch_bounds__(64) void rotate_kernel(const void* __restrict__ x, void* __restrict__ y,
-                                                    const int16_t* __restrict__ idx,
+                                                    uint8_t* __restrict__ sc, const int16_t* __restrict__ idx,
                                                     const void* __restrict__ theta,
                                                     const void* __restrict__ scales, int64_t rows,
                                                     int h, int krot) {
@@ -83,14 +89,45 @@ __global__ __launch_bounds__(64) void rotate_kernel(const void* __restrict__ x, 
     __syncthreads();
   }
 
+  if constexpr (MX) {
+    static_assert(kRotRows * 128 == 64 * 8, "8 channels per thread");
+    const int r = t >> 4;
+    const int c8 = (t & 15) * 8;
+    float v[8];
+    float am = 0.0f;
+    bool nan = false;
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    const int local = t + 64 * half;
-    const int ch = ch0 + local;
+    for (int e = 0; e < 8; ++e) {
+      v[e] = tile[r][c8 + e];
+      am = fmaxf(am, fabsf(v[e]));
+      nan = nan || (v[e] != v[e]);
+    }
+    am = fmaxf(am, __shfl_xor(am, 1));
+    am = fmaxf(am, __shfl_xor(am, 2));
+    int nn = nan ? 1 : 0;
+    nn |= __shfl_xor(nn, 1);
+    nn |= __shfl_xor(nn, 2);
+    const int ex = pqd::mx_shared_exp(am);
+    const float inv = pqd::mx_inv_scale(ex);
+    uint32_t w = 0;
 #pragma unroll
-    for (int r = 0; r < kRotRows; ++r) {
-      const int64_t row = row0 + r;
-      if (row < rows && ch < h) pq_store_from_f32<DT>(y, row * h + ch, tile[r][local]);
+    for (int e = 0; e < 8; ++e) w |= pqd::mx_e2m1(v[e] * inv) << (4 * e);
+    const int64_t row = row0 + r;
+    const int ch = ch0 + c8;
+    if (row < rows && ch < h) {
+      *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(y) + row * (h >> 1) + (ch >> 1)) = w;
+      if ((t & 3) == 0) sc[row * (h >> 5) + (ch >> 5)] = nn ? 0xFFu : static_cast<uint8_t>(ex + 127);
+    }
+  } else {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int local = t + 64 * half;
+      const int ch = ch0 + local;
+#pragma unroll
+      for (int r = 0; r < kRotRows; ++r) {
+        const int64_t row = row0 + r;
+        if (row < rows && ch < h) pq_store_from_f32<DT>(y, row * h + ch, tile[r][local]);
+      }
     }
   }
 }
@@ -435,21 +472,23 @@ __global__ __launch_bounds__(NT) void quant_kernel(const void* __restrict__ x, i
 }
 
 template <int DT, int G, bool SCALE>
-void launch_rotate(const void* x, void* y, const int16_t* idx, const void* theta, const void* scales,
+void launch_rotate(const void* x, void* y, uint8_t* sc, const int16_t* idx, const void* theta, const void* scales,
                    int64_t rows, int h, int krot, hipStream_t stream) {
   dim3 grid(static_cast<unsigned>((rows + kRotRows - 1) / kRotRows), static_cast<unsigned>((h + 127) / 128));
-  rotate_kernel<DT, G, SCALE><<<grid, 64, 0, stream>>>(x, y, idx, theta, scales, rows, h, krot);
+  if (sc != nullptr) rotate_kernel<DT, G, SCALE, true><<<grid, 64, 0, stream>>>(x, y, sc, idx, theta, scales, rows, h, krot);
+  else rotate_kernel<DT, G, SCALE, false><<<grid, 64, 0, stream>>>(x, y, sc, idx, theta, scales, rows, h, krot);
 }
 
+// sc == nullptr: rotated values into y; else MXFP4 codes into y, scales into sc.
 template <int DT>
-void launch_rotate_dt(const void* x, void* y, const int16_t* idx, const void* theta, const void* scales,
-                      int64_t rows, int h, int krot, int group, hipStream_t stream) {
+void launch_rotate_dt(const void* x, void* y, uint8_t* sc, const int16_t* idx, const void* theta,
+                      const void* scales, int64_t rows, int h, int krot, int group, hipStream_t stream) {
   if (group == 128) {
-    if (scales) launch_rotate<DT, 128, true>(x, y, idx, theta, scales, rows, h, krot, stream);
-    else launch_rotate<DT, 128, false>(x, y, idx, theta, scales, rows, h, krot, stream);
+    if (scales) launch_rotate<DT, 128, true>(x, y, sc, idx, theta, scales, rows, h, krot, stream);
+    else launch_rotate<DT, 128, false>(x, y, sc, idx, theta, scales, rows, h, krot, stream);
   } else {
-    if (scales) launch_rotate<DT, 64, true>(x, y, idx, theta, scales, rows, h, krot, stream);
-    else launch_rotate<DT, 64, false>(x, y, idx, theta, scales, rows, h, krot, stream);
+    if (scales) launch_rotate<DT, 64, true>(x, y, sc, idx, theta, scales, rows, h, krot, stream);
+    else launch_rotate<DT, 64, false>(x, y, sc, idx, theta, scales, rows, h, krot, stream);
   }
 }
 
@@ -554,11 +593,49 @@ extern "C" int pq_rotate(const void* x, void* y, const int16_t* idx_ij, const vo
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int hh = static_cast<int>(h);
   switch (dtype) {
-    case PQ_F32: launch_rotate_dt<PQ_F32>(x, y, idx_ij, theta, scales, rows, hh, krot, group_size, s); break;
-    case PQ_F16: launch_rotate_dt<PQ_F16>(x, y, idx_ij, theta, scales, rows, hh, krot, group_size, s); break;
-    default: launch_rotate_dt<PQ_BF16>(x, y, idx_ij, theta, scales, rows, hh, krot, group_size, s); break;
+    case PQ_F32: launch_rotate_dt<PQ_F32>(x, y, nullptr, idx_ij, theta, scales, rows, hh, krot, group_size, s); break;
+    case PQ_F16: launch_rotate_dt<PQ_F16>(x, y, nullptr, idx_ij, theta, scales, rows, hh, krot, group_size, s); break;
+    default: launch_rotate_dt<PQ_BF16>(x, y, nullptr, idx_ij, theta, scales, rows, hh, krot, group_size, s); break;
   }
   return pq::launch_status("pq_rotate launch");
+}
+
+// rotation::rotate followed by OCP MXFP4 quantization of the float32 result,
+// in one pass.  The CDNA4 counterpart of the reference's NVFP4
+// rotation::rotate_and_quant (kernels/paroquant_kernels/src/rotation.cu:62-111,
+// 230-315): the same rotation, a different block format (32-element blocks,
+// E8M0 scales, no second-level scale).
+extern "C" int pq_rotate_mxfp4(const void* x, uint8_t* q_out, uint8_t* scale_out, const int16_t* idx_ij,
+                               const void* theta, const void* scales, int64_t rows, int64_t h, int krot,
+                               int group_size, int dtype, void* stream) {
+  PQ_REQUIRE(rows >= 0 && h > 0, PQ_ERR_ARG, "pq_rotate_mxfp4: rows=%lld h=%lld", (long long)rows, (long long)h);
+  PQ_REQUIRE(group_size == 64 || group_size == 128, PQ_ERR_UNSUPPORTED,
+             "pq_rotate_mxfp4: Unexpected group_size: %d (supported: 64, 128)", group_size);
+  PQ_REQUIRE(krot == 1 || krot == 2 || krot == 4 || krot == 8 || krot == 16, PQ_ERR_UNSUPPORTED,
+             "pq_rotate_mxfp4: Unsupported KROT = %d; compiled variants: 1/2/4/8/16", krot);
+  PQ_REQUIRE(h % group_size == 0, PQ_ERR_ARG, "pq_rotate_mxfp4: h must be divisible by GROUP_SIZE (h=%lld, G=%d)",
+             (long long)h, group_size);
+  PQ_REQUIRE(h <= (1 << 24), PQ_ERR_ARG, "pq_rotate_mxfp4: h=%lld too large", (long long)h);
+  PQ_REQUIRE(dtype == PQ_F32 || dtype == PQ_F16 || dtype == PQ_BF16, PQ_ERR_UNSUPPORTED,
+             "pq_rotate_mxfp4: dtype code %d (Float, Half or BFloat16)", dtype);
+  if (rows == 0) return PQ_OK;
+  PQ_REQUIRE(x && q_out && scale_out && idx_ij && theta, PQ_ERR_ARG, "pq_rotate_mxfp4: null pointer");
+  PQ_REQUIRE(pq::aligned_to(q_out, 4), PQ_ERR_ARG, "pq_rotate_mxfp4: q_out must be 4-byte aligned");
+  PQ_REQUIRE((rows + kRotRows - 1) / kRotRows <= 0x7fffffffLL, PQ_ERR_ARG, "pq_rotate_mxfp4: too many rows");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int hh = static_cast<int>(h);
+  switch (dtype) {
+    case PQ_F32:
+      launch_rotate_dt<PQ_F32>(x, q_out, scale_out, idx_ij, theta, scales, rows, hh, krot, group_size, s);
+      break;
+    case PQ_F16:
+      launch_rotate_dt<PQ_F16>(x, q_out, scale_out, idx_ij, theta, scales, rows, hh, krot, group_size, s);
+      break;
+    default:
+      launch_rotate_dt<PQ_BF16>(x, q_out, scale_out, idx_ij, theta, scales, rows, hh, krot, group_size, s);
+      break;
+  }
+  return pq::launch_status("pq_rotate_mxfp4 launch");
 }
 
 extern "C" int pq_rotate_quant_i8(const void* x, int x_dtype, const uint32_t* rot_idx, const float* rot_cs,

@@ -39,6 +39,10 @@ _DT = {torch.float32: _lib.PQ_F32, torch.float16: _lib.PQ_F16, torch.bfloat16: _
 
 _rotation_lib = torch.library.Library("rotation", "DEF")
 _rotation_lib.define("rotate(Tensor x, Tensor idx_ij, Tensor theta, Tensor? scales, int group_size) -> Tensor")
+# The reference's rotate_and_quant writes NVFP4; this is the same fused op in the OCP MXFP4 format
+# (codes uint8 [..., H/2], E8M0 scales uint8 [..., H/32]).
+_rotation_lib.define("rotate_and_quant_mxfp4(Tensor x, Tensor idx_ij, Tensor theta, Tensor? scales, "
+                     "int group_size) -> (Tensor, Tensor)")
 
 _pq_lib = torch.library.Library("paroquant", "DEF")
 _pq_lib.define("rotate_quant_i8(Tensor x, Tensor rot_idx, Tensor rot_cs, Tensor? scales, int krot, bool input_fp16, "
@@ -125,7 +129,8 @@ def linear_workspace_bytes(m: int, n: int, k: int, krot: int) -> int:
 # rotation::rotate
 # ---------------------------------------------------------------------------
 
-def _rotate_impl(x, idx_ij, theta, scales, group_size):
+def _rotate_args(x, idx_ij, theta, scales):
+    """Checks of rotation::rotate's arguments; contiguous copies and the sizes."""
     _require(x.dtype in _DT, f"rotate only supports Float, Half, and BFloat16, but got {x.dtype}")
     _require(idx_ij.dtype == torch.int16, f"idx_ij must be int16, got {idx_ij.dtype}")
     _require(theta.dtype == x.dtype, f"theta must have x's dtype {x.dtype}, got {theta.dtype}")
@@ -144,17 +149,36 @@ def _rotate_impl(x, idx_ij, theta, scales, group_size):
     for nm, t in (("idx_ij", idx_ij), ("theta", theta)) + ((("scales", scales),) if has_scale else ()):
         _same_device(nm, t, dev)
     xc = x.contiguous()
-    out = torch.empty_like(xc)
-    rows = xc.numel() // h
-    idc, thc = idx_ij.contiguous(), theta.contiguous()
     scc = scales.contiguous() if has_scale else None
+    return xc, idx_ij.contiguous(), theta.contiguous(), scc, xc.numel() // h, h, krot
+
+
+def _rotate_impl(x, idx_ij, theta, scales, group_size):
+    xc, idc, thc, scc, rows, h, krot = _rotate_args(x, idx_ij, theta, scales)
+    dev = x.device
+    out = torch.empty_like(xc)
     lib = _lib.load()
     with _DeviceGuard(dev):
         st = lib.pq_rotate(xc.data_ptr(), out.data_ptr(), idc.data_ptr(), thc.data_ptr(),
-                           scc.data_ptr() if has_scale else None, rows, h, krot, int(group_size), _DT[x.dtype],
-                           _stream(dev))
+                           scc.data_ptr() if scc is not None else None, rows, h, krot, int(group_size),
+                           _DT[x.dtype], _stream(dev))
     _lib.check(st, "rotation::rotate")
     return out
+
+
+def _rotate_mxfp4_impl(x, idx_ij, theta, scales, group_size):
+    xc, idc, thc, scc, rows, h, krot = _rotate_args(x, idx_ij, theta, scales)
+    _require(h % 32 == 0, f"MXFP4 blocks are 32 channels: h={h}")
+    dev = x.device
+    q = torch.empty((*x.shape[:-1], h // 2), dtype=torch.uint8, device=dev)
+    sc = torch.empty((*x.shape[:-1], h // 32), dtype=torch.uint8, device=dev)
+    lib = _lib.load()
+    with _DeviceGuard(dev):
+        st = lib.pq_rotate_mxfp4(xc.data_ptr(), q.data_ptr(), sc.data_ptr(), idc.data_ptr(), thc.data_ptr(),
+                                 scc.data_ptr() if scc is not None else None, rows, h, krot, int(group_size),
+                                 _DT[x.dtype], _stream(dev))
+    _lib.check(st, "rotation::rotate_and_quant_mxfp4")
+    return q, sc
 
 
 _rotation_lib.impl("rotate", _rotate_impl, "CUDA")
@@ -163,6 +187,16 @@ _rotation_lib.impl("rotate", _rotate_impl, "CUDA")
 @torch.library.register_fake("rotation::rotate")
 def _rotate_fake(x, idx_ij, theta, scales, group_size):
     return torch.empty_like(x)
+
+
+_rotation_lib.impl("rotate_and_quant_mxfp4", _rotate_mxfp4_impl, "CUDA")
+
+
+@torch.library.register_fake("rotation::rotate_and_quant_mxfp4")
+def _rotate_mxfp4_fake(x, idx_ij, theta, scales, group_size):
+    h = x.size(-1)
+    return (x.new_empty((*x.shape[:-1], h // 2), dtype=torch.uint8),
+            x.new_empty((*x.shape[:-1], h // 32), dtype=torch.uint8))
 
 
 # ---------------------------------------------------------------------------

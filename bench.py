@@ -55,6 +55,7 @@ def measured_traffic():
         pass
     return None
 INT8_PEAK_TOPS = 5000.0
+FP16_PEAK_TFLOPS = 2500.0
 KROT = 8
 
 
@@ -66,6 +67,29 @@ def gemm_kernel_bytes(M: int, N: int, K: int) -> int:
     """Algorithmic bytes of the GEMM kernel alone: int4 codes, fp16 scales, int4 zeros,
     int8 activations + fp32 token scales in, bf16 out."""
     return N * K // 2 + 2 * N * K // 128 + N * K // 256 + M * K + 4 * M + 2 * M * N
+
+
+def w16_linear_bytes(M: int, N: int, K: int) -> int:
+    """W4A16 linear: int4 codes, fp16 scale + scaled zero per (group, column), rotation operands, fp16 in/out."""
+    return N * K // 2 + 4 * N * K // 128 + 3 * KROT * K + 2 * K + 2 * M * K + 2 * M * N
+
+
+def w16_gemm_bytes(M: int, N: int, K: int) -> int:
+    """W4A16 GEMM kernel alone: int4 codes, fp16 s and sz, fp16 activations in, fp16 out."""
+    return N * K // 2 + 4 * N * K // 128 + 2 * M * K + 2 * M * N
+
+
+def w16_meta(wmeta):
+    """s | sz << 16 metadata of the W4A16 GEMM for the weights behind a W4A8 wmeta (s | z << 16), with
+    sz = fp16(-(s * z)) as WQLinear stores it; the packed codes are shared."""
+    import torch
+
+    s_bits = (wmeta & 0xFFFF).long()
+    z = ((wmeta >> 16) & 0xF).float()
+    s = torch.where(s_bits >= 32768, s_bits - 65536, s_bits).to(torch.int16).view(torch.float16).float()
+    sz_bits = (-(s * z)).to(torch.float16).view(torch.int16).long() & 0xFFFF
+    m = s_bits | (sz_bits << 16)
+    return torch.where(m >= 2 ** 31, m - 2 ** 32, m).to(torch.int32).contiguous()
 
 
 def log(msg: str) -> None:
@@ -83,6 +107,7 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-verify", action="store_true", help="skip the 36-layer speculative verify block (M = 16)")
     ap.add_argument("--no-ragged", action="store_true", help="skip the ragged packed batch")
+    ap.add_argument("--no-w4a16", action="store_true", help="skip the W4A16 (WQLinear) figures")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first copy 256 MiB device to device 3 times: the known-size kernel that calibrates "
@@ -352,6 +377,88 @@ def main() -> int:
         log(f"ragged batch {lens} (M={Mr}): {rms:.3f} ms/layer, {ragged['tops']:.0f} TOPS")
         del gr, outs, Xr
 
+    # ---- W4A16 (WQLinear.forward): the same layers with fp16 activations ---
+    # Each linear: rotation (fp16 result) + W4A16 GEMM (paroquant::w4a16_linear), fp16 in / out; the pool's
+    # packed codes are shared, with s | sz metadata.  Decode M = 1 over the 8-layer pool (one graph), the
+    # decode GEMM alone, and prefill M = 3072 (layer, GEMMs alone, each shape's GEMM alone).
+    w16 = None
+    if not args.no_w4a16:
+        f16 = torch.float16
+        w16_pool = [[(m.rotate_linear.rotation, m.rotate_linear.qlinear.qweight,
+                      w16_meta(m.rotate_linear.qlinear.scales), N, K) for m, (N, K) in zip(L, shapes)]
+                    for L in pool]
+
+        def run16(li, X, gemm_only=False):
+            xa, xo, xm, xd = X
+            outs = []
+            for (rot, wp, wm16, N, K), x in zip(w16_pool[li], (xa, xa, xa, xo, xm, xm, xd)):
+                if gemm_only:
+                    outs.append(torch.ops.paroquant.w4a16_gemm(x, wp, wm16, None, f16))
+                else:
+                    outs.append(torch.ops.paroquant.w4a16_linear(x, rot.rot_idx, rot.rot_cs, rot.scales_f32,
+                                                                 rot.krot, wp, wm16, None, None, False, f16))
+            return outs
+
+        def capture16(xs, gemm_only, layers):
+            for li in layers:
+                run16(li, xs[li], gemm_only)
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                outs = [run16(li, xs[li], gemm_only) for li in layers]
+            return gr, outs
+
+        x16 = [tuple(a.to(f16) for a in X) for X in make_inputs(1, 8001)]
+        gr, _ = capture16(x16, False, range(P))
+        d_ms = time_graphs([gr], args.steps // P, -(-args.warmup // P)) / P
+        d_b = sum(w16_linear_bytes(1, N, K) for N, K in shapes)
+        del gr
+        gr, _ = capture16(x16, True, range(P))
+        dg_ms = time_graphs([gr], max(10, args.steps // 10), 3) / P
+        dg_b = sum(w16_gemm_bytes(1, N, K) for N, K in shapes)
+        del gr
+        log(f"W4A16 decode M=1: {d_ms * 1e3:.1f} us/layer ({d_b / (d_ms * 1e-3) / 1e9:.0f} GB/s); GEMMs alone "
+            f"{dg_ms * 1e3 / 7:.2f} us/launch ({dg_b / (dg_ms * 1e-3) / 1e9:.0f} GB/s)")
+        w16 = {"decode_M1": {"us_per_layer": round(d_ms * 1e3, 2), "GBps": round(d_b / (d_ms * 1e-3) / 1e9, 1),
+                             "frac_hbm": round(d_b / (d_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                             "gemm_only_us_per_launch": round(dg_ms * 1e3 / 7, 3),
+                             "gemm_only_GBps": round(dg_b / (dg_ms * 1e-3) / 1e9, 1),
+                             "gemm_only_frac_hbm": round(dg_b / (dg_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
+        if not args.no_prefill:
+            M = 3072
+            g = workloads.generator(6200, device=dev)
+            Xp = [tuple(workloads.activations(M, K, g, device=dev).to(f16) for K in (4096, 4096, 4096, 12288))]
+            flops = sum(2 * M * N * K for N, K in shapes)
+            pres = {}
+            for gemm_only in (False, True):
+                gr, outs = capture16(Xp, gemm_only, [0])
+                pres[gemm_only] = time_graphs([gr], args.prefill_steps, 3)
+                del gr, outs
+            per_shape = {}
+            xa, xo, xm, xd = Xp[0]
+            for idx, x in ((0, xa), (1, xa), (4, xm), (6, xd)):
+                rot, wp, wm16, N, K = w16_pool[0][idx]
+                torch.ops.paroquant.w4a16_gemm(x, wp, wm16, None, f16)
+                g1 = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g1):
+                    torch.ops.paroquant.w4a16_gemm(x, wp, wm16, None, f16)
+                sms = time_graphs([g1], args.prefill_steps, 3)
+                per_shape[f"{N}x{K}"] = {"us": round(sms * 1e3, 1),
+                                         "pct_fp16_peak": round(100 * 2 * M * N * K / (sms * 1e-3) / 1e12
+                                                                / FP16_PEAK_TFLOPS, 2)}
+                del g1
+            lt = flops / (pres[False] * 1e-3) / 1e12
+            gt = flops / (pres[True] * 1e-3) / 1e12
+            w16["prefill_M3072"] = {"ms_per_layer": round(pres[False], 4), "tflops": round(lt, 1),
+                                    "pct_fp16_peak": round(100 * lt / FP16_PEAK_TFLOPS, 2),
+                                    "gemm_only_tflops": round(gt, 1),
+                                    "gemm_only_pct_fp16_peak": round(100 * gt / FP16_PEAK_TFLOPS, 2),
+                                    "gemm_per_shape": per_shape}
+            log(f"W4A16 prefill M=3072: {pres[False]:.3f} ms/layer, {lt:.0f} TFLOPS ({100 * lt / FP16_PEAK_TFLOPS:.1f}%);"
+                f" GEMMs alone {gt:.0f} TFLOPS; per shape " + ", ".join(f"{k} {v['us']} us ({v['pct_fp16_peak']}%)"
+                                                                      for k, v in per_shape.items()))
+            del Xp
+        del w16_pool
+
     # ---- CPU baseline: the oracle on the host ------------------------------
     cpu = None
     if not args.no_cpu:
@@ -397,6 +504,7 @@ def main() -> int:
         "prefill_M3072": prefill,
         "verify_block_M16": verify,
         "ragged_batch": ragged,
+        "w4a16": w16,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

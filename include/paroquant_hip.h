@@ -29,6 +29,8 @@
  *                        rotation::rotate -> MarlinW4A8Linear.forward
  *                        (paroquant_marlin_w4a8.py:59-65, 314-333;
  *                        rotation_linear.py:120-124)
+ *   pq_rotate_mxfp4      rotation::rotate_and_quant (rotation.cu:62-111),
+ *                        in the OCP MXFP4 format instead of NVFP4
  *   pq_w4a16_gemm        torch.ops.awq.gemv / torch.ops.awq.gemm behind
  *                        WQLinear.forward (qmodule.py:207-232)
  *   pq_w4a16_prepack     the weight preparation those kernels need
@@ -75,6 +77,19 @@ const char* pq_last_error(void);
 int pq_rotate(const void* x, void* y, const int16_t* idx_ij, const void* theta,
               const void* scales, int64_t rows, int64_t h, int krot, int group_size,
               int dtype, void* stream);
+
+/* Fused rotation + OCP MXFP4 quantization: the rotation of pq_rotate (same
+ * arguments and rules), then, per row and per block of 32 channels of the
+ * float32 result v, the shared exponent e = floor(log2(max|v|)) - 2 clamped
+ * to [-127, 127] and the E2M1 code of each v / 2^e (round to nearest even,
+ * saturating at +-6, sign kept).  q_out: uint8 [rows, h/2], element 2i in
+ * the low nibble of byte i, 4-byte aligned; scale_out: uint8 [rows, h/32],
+ * the E8M0 byte e + 127, or 0xFF for a block holding a NaN.
+ * Reference: rotation::rotate_and_quant (rotation.cu:62-111, 230-315, 587),
+ * which writes NVFP4 (16-element blocks, FP8 scales, a global scale); this
+ * entry point is its counterpart in the MX format gfx950 multiplies natively. */
+int pq_rotate_mxfp4(const void* x, uint8_t* q_out, uint8_t* scale_out, const int16_t* idx_ij, const void* theta,
+                    const void* scales, int64_t rows, int64_t h, int krot, int group_size, int dtype, void* stream);
 
 /* Packs rotation parameters (host memory, host code; no GPU involved) into
  * the operand layout of the fused kernels, G = h/128, KP = 8 for krot <= 8,

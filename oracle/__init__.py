@@ -19,6 +19,8 @@ the path so that the HIP kernels can be checked against it:
                (quantization_utils.py:18-73)
   rmsnorm.py   the decoder layer's RMSNorm (+ residual add) in front of a
                shared-input group (modeling_qwen3_vl.py:354-359)
+  mxfp4.py     OCP MXFP4 quantization of the rotated rows (the MX counterpart
+               of rotation::rotate_and_quant, rotation.cu:62-111)
   w4a16.py     the W4A16 linear: WQLinear.forward (qmodule.py:207-232) and
                RotateLinearInt4 over it (rotation_linear.py:136-139)
 
@@ -45,6 +47,10 @@ Pinning status of each function (how each is checked, see tests/test_oracle_*.py
               when sz = -s*z is representable, and a brute-force loop for
               the GEMM.  The external kernels' accumulation order and
               rounding are parity unpinned (not in the reference tree).
+  mxfp4       E2M1 grid against the format's bit-level definition, E8M0
+              bytes against torch.float8_e8m0fnu, rounding against an
+              exhaustive nearest-value search with explicit ties, round trip
+              of representable blocks.
   packing     pack_intweight / pseudo_quantize_tensor against golden vectors
               written by importing the reference's own functions in the
               build container (tests/golden/make_golden.py); AWQ order

@@ -192,3 +192,19 @@ def test_w4a16_argument_checks():
     assert linear(m=64) == 4 and "workspace" in _err(lib)
     assert linear(m=64, ws=p, wsb=need64 - 1) == 4
     assert linear(m=64, ws=ctypes.c_void_p(272), wsb=need64) == 4
+
+
+def test_rotate_mxfp4_argument_checks():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+
+    def call(x=p, q=p, s=p, rows=4, h=256, krot=8, gs=128, dt=2):
+        return lib.pq_rotate_mxfp4(x, q, s, p, p, None, rows, h, krot, gs, dt, None)
+
+    assert call(gs=32) == 2 and "group_size" in _err(lib)
+    assert call(krot=3) == 2
+    assert call(h=200) == 1
+    assert call(dt=9) == 2
+    assert call(q=ctypes.c_void_p(258)) == 1 and "aligned" in _err(lib)
+    assert call(s=None) == 1 and "null" in _err(lib)
+    assert call(rows=0) == 0
