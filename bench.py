@@ -108,6 +108,7 @@ def main() -> int:
     ap.add_argument("--no-verify", action="store_true", help="skip the 36-layer speculative verify block (M = 16)")
     ap.add_argument("--no-ragged", action="store_true", help="skip the ragged packed batch")
     ap.add_argument("--no-w4a16", action="store_true", help="skip the W4A16 (WQLinear) figures")
+    ap.add_argument("--no-mxfp4", action="store_true", help="skip the fused rotation + MXFP4 figures")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first copy 256 MiB device to device 3 times: the known-size kernel that calibrates "
@@ -459,6 +460,38 @@ def main() -> int:
             del Xp
         del w16_pool
 
+    # ---- fused rotation + MXFP4 quant (rotation::rotate_and_quant_mxfp4) ----
+    # bf16 activations [M, 4096] through a KROT = 8 rotation with channel scales, beside rotation::rotate
+    # alone on the same input.  Bytes: x in, codes (K/2) + E8M0 scales (K/32) out, rotation parameters.
+    mx = None
+    if not args.no_mxfp4:
+        mx = {}
+        K = 4096
+        g = workloads.generator(6300, device=dev)
+        pairs, theta, cs = workloads.rotation_params(K, g, device=dev)
+        th16, cs16 = theta.to(torch.bfloat16), cs.to(torch.bfloat16)
+        for M in (16, 3072):
+            xm = workloads.activations(M, K, g, device=dev)
+            res = {}
+            for name, fn in (("mxfp4", lambda: torch.ops.rotation.rotate_and_quant_mxfp4(xm, pairs, th16, cs16, 128)),
+                             ("rotate", lambda: torch.ops.rotation.rotate(xm, pairs, th16, cs16, 128))):
+                fn()
+                gr = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gr):
+                    for _ in range(10):
+                        fn()
+                res[name] = time_graphs([gr], max(5, args.prefill_steps), 2) / 10
+                del gr
+            params = 2 * KROT * K // 2 + 2 * KROT * K + 2 * K
+            b_mx = 2 * M * K + M * K // 2 + M * K // 32 + params
+            b_rot = 4 * M * K + params
+            mx[f"M{M}"] = {"us": round(res["mxfp4"] * 1e3, 2), "GBps": round(b_mx / (res["mxfp4"] * 1e-3) / 1e9, 1),
+                           "frac_hbm": round(b_mx / (res["mxfp4"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                           "rotate_alone_us": round(res["rotate"] * 1e3, 2),
+                           "rotate_alone_GBps": round(b_rot / (res["rotate"] * 1e-3) / 1e9, 1)}
+            log(f"rotate+MXFP4 M={M} K={K}: {res['mxfp4'] * 1e3:.1f} us ({mx[f'M{M}']['GBps']:.0f} GB/s); "
+                f"rotate alone {res['rotate'] * 1e3:.1f} us ({mx[f'M{M}']['rotate_alone_GBps']:.0f} GB/s)")
+
     # ---- CPU baseline: the oracle on the host ------------------------------
     cpu = None
     if not args.no_cpu:
@@ -505,6 +538,7 @@ def main() -> int:
         "verify_block_M16": verify,
         "ragged_batch": ragged,
         "w4a16": w16,
+        "rotate_mxfp4_K4096": mx,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

@@ -47,7 +47,7 @@ def _run(x, pairs, th, sc, gs):
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("gs,krot,h,rows", [(128, 8, 4096, 5), (128, 1, 256, 1), (64, 4, 192, 33),
                                             (128, 16, 384, 9), (64, 8, 64, 3), (128, 2, 12288, 2),
-                                            (128, 8, 4096, 1000)])
+                                            (128, 8, 4096, 1000), (128, 8, 4096, 1029), (64, 4, 192, 2048)])
 @pytest.mark.parametrize("with_scale", [True, False])
 def test_mxfp4_matches_oracle(dt, gs, krot, h, rows, with_scale):
     print(f"mxfp4 dt={dt} gs={gs} krot={krot} h={h} rows={rows} scale={with_scale}", flush=True)

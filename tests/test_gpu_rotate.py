@@ -27,7 +27,8 @@ def _params(rng, krot, h, gs):
 
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("gs,krot,h,rows", [(128, 8, 4096, 5), (128, 1, 256, 1), (64, 4, 192, 33),
-                                            (128, 16, 384, 9), (64, 8, 64, 3), (128, 2, 12288, 2)])
+                                            (128, 16, 384, 9), (64, 8, 64, 3), (128, 2, 12288, 2),
+                                            (128, 8, 1024, 1030), (64, 16, 320, 2048)])
 @pytest.mark.parametrize("with_scale", [True, False])
 def test_rotate_matches_oracle(dt, gs, krot, h, rows, with_scale):
     print(f"rotate dt={dt} gs={gs} krot={krot} h={h} rows={rows} scale={with_scale}", flush=True)
@@ -46,9 +47,12 @@ def test_rotate_matches_oracle(dt, gs, krot, h, rows, with_scale):
     if dt == "f32":
         assert rel_fro(got, ref) < 1e-5
     else:
-        # outputs rounded to fp16/bf16: within one unit of the storage format
+        # outputs rounded to fp16/bf16: within one unit of the storage format, plus the float32
+        # rounding of the layer chain (cos/sin from sincosf vs the oracle's float64 table, up to
+        # ~1e-6 of the row's magnitude after 16 layers), which shows on values near zero
         ulp = 2.0 ** (-10 if dt == "f16" else -7)
-        assert np.all(np.abs(got - ref) <= ulp * np.abs(ref) + 1e-6)
+        slack = 1e-5 * np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+        assert np.all(np.abs(got - ref) <= ulp * np.abs(ref) + slack)
         assert rel_fro(got, ref) < 1e-2
 
 
