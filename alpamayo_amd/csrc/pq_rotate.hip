@@ -22,111 +22,152 @@ using pqd::quant4;
 
 namespace {
 
-constexpr int kRotRows = 4;   // rows per workgroup of the plain rotation kernel
+constexpr int kRotRows = 16;   // rows per workgroup of the plain rotation kernel
 
 
 // ---------------------------------------------------------------------------
-// rotation::rotate.  One wave per (4 rows x 128 channels); lane t owns pair t
-// of the chunk (for group 64 the chunk holds two groups).  The 4 x 128 fp32
-// tile lives in LDS; pairs are read per layer and masked to the group so a
-// bad index can never address outside the tile.
+// rotation::rotate.  A workgroup of 4 waves takes 16 rows x 128 channels (for
+// group 64 the chunk holds two groups).  The 64 pairs' indices (masked to the
+// group, so a bad index can never address outside the tile) and cos/sin of
+// every layer are derived once per workgroup into LDS -- each sincosf serves
+// 16 rows.  Wave w owns rows 4w .. 4w+3 as a channel-major LDS tile (one
+// float4 = the wave's 4 rows of a channel), so lane l applies a layer to its
+// pair with two 16-byte reads and two 16-byte writes.
 // ---------------------------------------------------------------------------
 //
 // MX: instead of the rotated values, their OCP MXFP4 quantization (fused
 // rotate + quant): y receives the E2M1 codes [rows][h/2] (element 2i in the
 // low nibble of byte i) and sc the E8M0 scales [rows][h/32] (0xFF when the
-// block holds a NaN).  Thread t quantizes 8 channels of tile row t/16; the
-// 4 threads of a 32-channel block exchange their absmax by lane shuffles.
+// block holds a NaN).  Lane l quantizes channels 2l, 2l+1 of its wave's rows;
+// the 16 lanes of a 32-channel block exchange their absmax by shuffles.
+constexpr int kRotWaves = 4;
+constexpr int kRotRowsPerWave = 4;
+constexpr int kRotMaxLayers = 16;
+
 template <int DT, int G, bool SCALE, bool MX>
-__global__ __launch_bounds__(64) void rotate_kernel(const void* __restrict__ x, void* __restrict__ y,
-                                                    uint8_t* __restrict__ sc, const int16_t* __restrict__ idx,
-                                                    const void* __restrict__ theta,
-                                                    const void* __restrict__ scales, int64_t rows,
-                                                    int h, int krot) {
-  __shared__ float tile[kRotRows][128];
+__global__ __launch_bounds__(kRotWaves * 64) void rotate_kernel(const void* __restrict__ x, void* __restrict__ y,
+                                                                uint8_t* __restrict__ sc,
+                                                                const int16_t* __restrict__ idx,
+                                                                const void* __restrict__ theta,
+                                                                const void* __restrict__ scales, int64_t rows,
+                                                                int h, int krot) {
+  static_assert(kRotRows == kRotWaves * kRotRowsPerWave && kRotRowsPerWave == 4, "a float4 per channel and wave");
+  __shared__ float4 tile[kRotWaves][128];
+  __shared__ float2 s_cs[kRotMaxLayers][64];
+  __shared__ uint32_t s_ij[kRotMaxLayers][64];
+  constexpr int NT = kRotWaves * 64;
   const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int w = t >> 6;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kRotRows;
   const int ch0 = blockIdx.y * 128;
 
-#pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    const int local = t + 64 * half;
-    const int ch = ch0 + local;
-    float s = 1.0f;
-    if (SCALE && ch < h) s = pq_load_as_f32<DT>(scales, ch);
-#pragma unroll
-    for (int r = 0; r < kRotRows; ++r) {
-      const int64_t row = row0 + r;
-      float v = 0.0f;
-      if (row < rows && ch < h) v = pq_load_as_f32<DT>(x, row * h + ch) * s;
-      tile[r][local] = v;
-    }
-  }
-
-  const int P = blockIdx.y * 64 + t;  // pair index within the row; theta column
-  const bool active = P < (h >> 1);
-  const int gi = P / (G / 2);
-  const int pp = P % (G / 2);
-  const int base = gi * G - ch0;  // group start inside the 128-channel tile
-  __syncthreads();
-
-  for (int r = 0; r < krot; ++r) {
-    if (active) {
+  // Layer parameters of the chunk's 64 pairs.  A pair past h (the second
+  // half of a 64-channel tail) turns its own two channels, which hold zeros
+  // and are never stored, by the identity.
+  for (int e = t; e < krot * 64; e += NT) {
+    const int r = e >> 6, p = e & 63;
+    const int P = blockIdx.y * 64 + p;   // pair index within the row; theta column
+    float c = 1.0f, sn = 0.0f;
+    uint32_t ij = static_cast<uint32_t>(2 * p) | (static_cast<uint32_t>(2 * p + 1) << 8);
+    if (P < (h >> 1)) {
+      const int gi = P / (G / 2);
+      const int pp = P % (G / 2);
+      const int base = gi * G - ch0;   // group start inside the 128-channel tile
       const int64_t o = static_cast<int64_t>(r) * h + gi * G + 2 * pp;
       const int i = base + (idx[o] & (G - 1));
       const int j = base + (idx[o + 1] & (G - 1));
       const float th = pq_load_as_f32<DT>(theta, static_cast<int64_t>(r) * (h >> 1) + P);
-      float sn, cs;
-      sincosf(th, &sn, &cs);
+      sincosf(th, &sn, &c);
+      ij = static_cast<uint32_t>(i) | (static_cast<uint32_t>(j) << 8);
+    }
+    s_cs[r][p] = make_float2(c, sn);
+    s_ij[r][p] = ij;
+  }
+  // Wave w loads its own rows: lane l channels 2l, 2l+1 of each (coalesced).
+  float4* wt = tile[w];
+  {
+    const int ch = ch0 + 2 * lane;
+    float s0 = 1.0f, s1 = 1.0f;
+    if (SCALE && ch < h) {
+      s0 = pq_load_as_f32<DT>(scales, ch);
+      s1 = pq_load_as_f32<DT>(scales, ch + 1);
+    }
+    float va[kRotRowsPerWave], vb[kRotRowsPerWave];
 #pragma unroll
-      for (int rr = 0; rr < kRotRows; ++rr) {
-        const float xi = tile[rr][i];
-        const float xj = tile[rr][j];
-        tile[rr][i] = fmaf(xi, cs, xj * sn);
-        tile[rr][j] = fmaf(xj, cs, -(xi * sn));
+    for (int rr = 0; rr < kRotRowsPerWave; ++rr) {
+      const int64_t row = row0 + w * kRotRowsPerWave + rr;
+      va[rr] = 0.0f;
+      vb[rr] = 0.0f;
+      if (row < rows && ch < h) {
+        va[rr] = pq_load_as_f32<DT>(x, row * h + ch);
+        vb[rr] = pq_load_as_f32<DT>(x, row * h + ch + 1);
+        if (SCALE) {
+          va[rr] = va[rr] * s0;
+          vb[rr] = vb[rr] * s1;
+        }
       }
     }
-    __syncthreads();
+    wt[2 * lane] = make_float4(va[0], va[1], va[2], va[3]);
+    wt[2 * lane + 1] = make_float4(vb[0], vb[1], vb[2], vb[3]);
+  }
+  __syncthreads();
+
+  for (int r = 0; r < krot; ++r) {
+    const float2 cs = s_cs[r][lane];
+    const uint32_t ij = s_ij[r][lane];
+    const int i = static_cast<int>(ij & 0xffu), j = static_cast<int>(ij >> 8);
+    const float4 xi = wt[i];
+    const float4 xj = wt[j];
+    float4 ni, nj;
+    ni.x = fmaf(xi.x, cs.x, xj.x * cs.y);
+    nj.x = fmaf(xj.x, cs.x, -(xi.x * cs.y));
+    ni.y = fmaf(xi.y, cs.x, xj.y * cs.y);
+    nj.y = fmaf(xj.y, cs.x, -(xi.y * cs.y));
+    ni.z = fmaf(xi.z, cs.x, xj.z * cs.y);
+    nj.z = fmaf(xj.z, cs.x, -(xi.z * cs.y));
+    ni.w = fmaf(xi.w, cs.x, xj.w * cs.y);
+    nj.w = fmaf(xj.w, cs.x, -(xi.w * cs.y));
+    wt[i] = ni;
+    wt[j] = nj;
+    // The sub-tile is this wave's alone, and a wave's LDS operations complete
+    // in issue order: the next layer's reads see these writes without a
+    // workgroup barrier.  The fence keeps the compiler from moving them.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
   }
 
+  // Lane l of wave w holds channels 2l, 2l+1 of the wave's 4 rows.
+  const float4 fa = wt[2 * lane], fb = wt[2 * lane + 1];
+  const float va[kRotRowsPerWave] = {fa.x, fa.y, fa.z, fa.w};
+  const float vb[kRotRowsPerWave] = {fb.x, fb.y, fb.z, fb.w};
+  const int ch = ch0 + 2 * lane;
   if constexpr (MX) {
-    static_assert(kRotRows * 128 == 64 * 8, "8 channels per thread");
-    const int r = t >> 4;
-    const int c8 = (t & 15) * 8;
-    float v[8];
-    float am = 0.0f;
-    bool nan = false;
+    // a 32-channel block = 16 lanes: absmax and the NaN flag over them by shuffles
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      v[e] = tile[r][c8 + e];
-      am = fmaxf(am, fabsf(v[e]));
-      nan = nan || (v[e] != v[e]);
-    }
-    am = fmaxf(am, __shfl_xor(am, 1));
-    am = fmaxf(am, __shfl_xor(am, 2));
-    int nn = nan ? 1 : 0;
-    nn |= __shfl_xor(nn, 1);
-    nn |= __shfl_xor(nn, 2);
-    const int ex = pqd::mx_shared_exp(am);
-    const float inv = pqd::mx_inv_scale(ex);
-    uint32_t w = 0;
+    for (int rr = 0; rr < kRotRowsPerWave; ++rr) {
+      float am = fmaxf(fabsf(va[rr]), fabsf(vb[rr]));
+      int nn = (va[rr] != va[rr]) || (vb[rr] != vb[rr]) ? 1 : 0;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) w |= pqd::mx_e2m1(v[e] * inv) << (4 * e);
-    const int64_t row = row0 + r;
-    const int ch = ch0 + c8;
-    if (row < rows && ch < h) {
-      *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(y) + row * (h >> 1) + (ch >> 1)) = w;
-      if ((t & 3) == 0) sc[row * (h >> 5) + (ch >> 5)] = nn ? 0xFFu : static_cast<uint8_t>(ex + 127);
+      for (int d = 1; d < 16; d <<= 1) {
+        am = fmaxf(am, __shfl_xor(am, d));
+        nn |= __shfl_xor(nn, d);
+      }
+      const int ex = pqd::mx_shared_exp(am);
+      const float inv = pqd::mx_inv_scale(ex);
+      const uint32_t code = pqd::mx_e2m1(va[rr] * inv) | (pqd::mx_e2m1(vb[rr] * inv) << 4);
+      const int64_t row = row0 + w * kRotRowsPerWave + rr;
+      if (row < rows && ch < h) {
+        static_cast<uint8_t*>(y)[row * (h >> 1) + (ch >> 1)] = static_cast<uint8_t>(code);
+        if ((lane & 15) == 0) sc[row * (h >> 5) + (ch >> 5)] = nn ? 0xFFu : static_cast<uint8_t>(ex + 127);
+      }
     }
   } else {
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const int local = t + 64 * half;
-      const int ch = ch0 + local;
-#pragma unroll
-      for (int r = 0; r < kRotRows; ++r) {
-        const int64_t row = row0 + r;
-        if (row < rows && ch < h) pq_store_from_f32<DT>(y, row * h + ch, tile[r][local]);
+    for (int rr = 0; rr < kRotRowsPerWave; ++rr) {
+      const int64_t row = row0 + w * kRotRowsPerWave + rr;
+      if (row < rows && ch < h) {
+        pq_store_from_f32<DT>(y, row * h + ch, va[rr]);
+        pq_store_from_f32<DT>(y, row * h + ch + 1, vb[rr]);
       }
     }
   }
@@ -475,8 +516,11 @@ template <int DT, int G, bool SCALE>
 void launch_rotate(const void* x, void* y, uint8_t* sc, const int16_t* idx, const void* theta, const void* scales,
                    int64_t rows, int h, int krot, hipStream_t stream) {
   dim3 grid(static_cast<unsigned>((rows + kRotRows - 1) / kRotRows), static_cast<unsigned>((h + 127) / 128));
-  if (sc != nullptr) rotate_kernel<DT, G, SCALE, true><<<grid, 64, 0, stream>>>(x, y, sc, idx, theta, scales, rows, h, krot);
-  else rotate_kernel<DT, G, SCALE, false><<<grid, 64, 0, stream>>>(x, y, sc, idx, theta, scales, rows, h, krot);
+  if (sc != nullptr)
+    rotate_kernel<DT, G, SCALE, true><<<grid, kRotWaves * 64, 0, stream>>>(x, y, sc, idx, theta, scales, rows, h, krot);
+  else
+    rotate_kernel<DT, G, SCALE, false><<<grid, kRotWaves * 64, 0, stream>>>(x, y, sc, idx, theta, scales, rows, h,
+                                                                            krot);
 }
 
 // sc == nullptr: rotated values into y; else MXFP4 codes into y, scales into sc.
