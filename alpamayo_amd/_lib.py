@@ -20,6 +20,7 @@ PQ_F32, PQ_F16, PQ_BF16 = 0, 1, 2
 # flags of pq_rotate_quant_i8
 PQ_RQ_INPUT_FP16 = 1
 PQ_RQ_MATERIALIZE_FP16 = 2
+PQ_PRO_RMSNORM, PQ_PRO_ADD, PQ_PRO_SWIGLU = 1, 2, 3
 
 STATUS_NAMES = {0: "PQ_OK", 1: "PQ_ERR_ARG", 2: "PQ_ERR_UNSUPPORTED", 3: "PQ_ERR_HIP", 4: "PQ_ERR_WORKSPACE"}
 STATUS_CODE = {v: k for k, v in STATUS_NAMES.items()}
@@ -60,6 +61,9 @@ SIGNATURES = {
                                     _P, _SZ, _P]),
     "pq_w4a8_linear_group_rmsnorm": (_INT, [_P, _P, _P, ctypes.c_float, _P, _P, _INT, ctypes.POINTER(LinearMember),
                                             _INT, _INT, _INT, _I64, _I64, _INT, _UINT, _P, _SZ, _P]),
+    "pq_w4a8_linear_split_path": (_INT, [_I64, _I64]),
+    "pq_w4a8_linear_group_fused": (_INT, [_P, _P, _P, ctypes.c_float, _INT, _P, _P, _INT, ctypes.POINTER(LinearMember),
+                                          _INT, _INT, _INT, _I64, _I64, _INT, _UINT, _P, _SZ, _P]),
     "pq_w4a16_prepack": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _INT, _P]),
     "pq_w4a16_gemm": (_INT, [_P, _P, _P, _P, _INT, _P, _INT, _I64, _I64, _I64, _INT, _P]),
     "pq_w4a16_linear_workspace_size": (_SZ, [_I64, _I64]),

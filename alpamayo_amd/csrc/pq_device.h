@@ -230,6 +230,14 @@ __device__ __forceinline__ float rms_apply(float s, float r, float w) {
   return round_to_dt<DT>(w * round_to_dt<DT>(s * r));
 }
 
+// A gated MLP's activation in the module's rounding: round(round(silu(g)) * u),
+// silu(g) = g / (1 + exp(-g)) in float32.
+template <int DT>
+__device__ __forceinline__ float swiglu(float g, float u) {
+  const float a = round_to_dt<DT>(g / (1.0f + expf(-g)));
+  return round_to_dt<DT>(a * u);
+}
+
 // One wave rotates 128-channel group g of the first min(M, MR) rows: channel
 // scale, the krot register-chain layers, then the rotated values go to xr
 // (fp16 when MAT16, else fp32; row stride h) and each row's absmax over the
@@ -237,10 +245,12 @@ __device__ __forceinline__ float rms_apply(float s, float r, float w) {
 // is first rounded through fp16.  Rows past M repeat row M-1 and store
 // nothing.
 //
-// With NORM the wave first computes each row's RMSNorm factor over the whole
-// row (every wave of the launch gets the same bits), then rotates the
-// normalized values of its group and, when h_out / s_out are set, writes
-// them and the residual sum s for the group's channels.
+// With NORM the group's rows first go through the prologue of `mode`
+// (PQ_PRO_*): RMSNORM computes each row's RMSNorm factor over the whole row
+// (every wave of the launch gets the same bits) and normalizes, ADD adds the
+// residual, SWIGLU forms silu(x) * up; the wave rotates the result and, when
+// h_out / s_out are set, writes it (h) or the residual sum s for the group's
+// channels.
 template <int DT, int KP, bool MAT16, int MR, bool NORM = false>
 __device__ __forceinline__ void rotate_group_rows(const void* __restrict__ x, const uint32_t* __restrict__ rot_idx,
                                                   const float* __restrict__ rot_cs, const float* __restrict__ scales,
@@ -249,7 +259,8 @@ __device__ __forceinline__ void rotate_group_rows(const void* __restrict__ x, co
                                                   const void* __restrict__ nres = nullptr,
                                                   const void* __restrict__ nw = nullptr,
                                                   void* __restrict__ h_out = nullptr,
-                                                  void* __restrict__ s_out = nullptr, float eps = 0.0f) {
+                                                  void* __restrict__ s_out = nullptr, float eps = 0.0f,
+                                                  int mode = PQ_PRO_RMSNORM) {
   const int G = h >> 7;
   const bool in16 = (flags & PQ_RQ_INPUT_FP16) != 0;
   const bool has_scales = scales != nullptr;
@@ -279,25 +290,43 @@ __device__ __forceinline__ void rotate_group_rows(const void* __restrict__ x, co
     xhi[m] = pq_raw_to_f32<DT>(xb[m]);
   }
   if constexpr (NORM) {
-    const float w0 = pq_load_as_f32<DT>(nw, g * 128 + lane), w1 = pq_load_as_f32<DT>(nw, g * 128 + 64 + lane);
+    if (mode == PQ_PRO_SWIGLU) {
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      const int mm = m < M ? m : M - 1;
-      const int64_t ro = static_cast<int64_t>(mm) * h;
-      const float r = rms_inv(row_sumsq<DT>(x, nres, ro, h, lane), h, eps);
-      if (nres != nullptr) {
-        xlo[m] = round_to_dt<DT>(xlo[m] + pq_load_as_f32<DT>(nres, ro + g * 128 + lane));
-        xhi[m] = round_to_dt<DT>(xhi[m] + pq_load_as_f32<DT>(nres, ro + g * 128 + 64 + lane));
+      for (int m = 0; m < MR; ++m) {
+        const int mm = m < M ? m : M - 1;
+        const int64_t ro = static_cast<int64_t>(mm) * h;
+        xlo[m] = swiglu<DT>(xlo[m], pq_load_as_f32<DT>(nres, ro + g * 128 + lane));
+        xhi[m] = swiglu<DT>(xhi[m], pq_load_as_f32<DT>(nres, ro + g * 128 + 64 + lane));
+        if (m < M && h_out != nullptr) {
+          pq_store_from_f32<DT>(h_out, ro + g * 128 + lane, xlo[m]);
+          pq_store_from_f32<DT>(h_out, ro + g * 128 + 64 + lane, xhi[m]);
+        }
       }
-      if (m < M && s_out != nullptr) {
-        pq_store_from_f32<DT>(s_out, ro + g * 128 + lane, xlo[m]);
-        pq_store_from_f32<DT>(s_out, ro + g * 128 + 64 + lane, xhi[m]);
-      }
-      xlo[m] = rms_apply<DT>(xlo[m], r, w0);
-      xhi[m] = rms_apply<DT>(xhi[m], r, w1);
-      if (m < M && h_out != nullptr) {
-        pq_store_from_f32<DT>(h_out, ro + g * 128 + lane, xlo[m]);
-        pq_store_from_f32<DT>(h_out, ro + g * 128 + 64 + lane, xhi[m]);
+    } else {
+      const bool norm = mode == PQ_PRO_RMSNORM;
+      const void* nwp = norm ? nw : x;   // ADD has no weight: a harmless stand-in, unused
+      const float w0 = pq_load_as_f32<DT>(nwp, g * 128 + lane), w1 = pq_load_as_f32<DT>(nwp, g * 128 + 64 + lane);
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const int mm = m < M ? m : M - 1;
+        const int64_t ro = static_cast<int64_t>(mm) * h;
+        const float r = norm ? rms_inv(row_sumsq<DT>(x, nres, ro, h, lane), h, eps) : 1.0f;
+        if (nres != nullptr) {
+          xlo[m] = round_to_dt<DT>(xlo[m] + pq_load_as_f32<DT>(nres, ro + g * 128 + lane));
+          xhi[m] = round_to_dt<DT>(xhi[m] + pq_load_as_f32<DT>(nres, ro + g * 128 + 64 + lane));
+        }
+        if (m < M && s_out != nullptr) {
+          pq_store_from_f32<DT>(s_out, ro + g * 128 + lane, xlo[m]);
+          pq_store_from_f32<DT>(s_out, ro + g * 128 + 64 + lane, xhi[m]);
+        }
+        if (norm) {
+          xlo[m] = rms_apply<DT>(xlo[m], r, w0);
+          xhi[m] = rms_apply<DT>(xhi[m], r, w1);
+          if (m < M && h_out != nullptr) {
+            pq_store_from_f32<DT>(h_out, ro + g * 128 + lane, xlo[m]);
+            pq_store_from_f32<DT>(h_out, ro + g * 128 + 64 + lane, xhi[m]);
+          }
+        }
       }
     }
   }

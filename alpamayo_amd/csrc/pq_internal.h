@@ -58,12 +58,18 @@ constexpr int kSplitMaxRows = 16;
 // roundings to x's dtype, mean and rsqrt in float32.  The members rotate h;
 // h and s are also written when h_out / s_out are set ([m][k], x's dtype).
 // w: [k] in x's dtype.
+//
+// mode generalizes the prologue (PQ_PRO_*): RMSNORM as above; ADD rotates
+// s = x + res (rounded to x's dtype) and writes it to s_out when set; SWIGLU
+// rotates h = round(round(silu(x)) * res) (silu in float32: x / (1 + exp(-x)))
+// and writes it to h_out when set.
 struct NormArgs {
   const void* res;
   const void* w;
   void* h_out;
   void* s_out;
   float eps;
+  int mode;
 };
 
 // Rotation of m <= kSplitMaxRows rows with one wave per 128-channel group,

@@ -121,6 +121,8 @@ extern "C" size_t pq_w4a8_linear_workspace_size(int64_t m, int64_t n, int64_t k,
   return group_workspace_size(m, k, 1);
 }
 
+extern "C" int pq_w4a8_linear_split_path(int64_t m, int64_t k) { return m > 0 && use_split(m, k) ? 1 : 0; }
+
 extern "C" size_t pq_w4a8_linear_group_workspace_size(int64_t m, int64_t k, int count) {
   return group_workspace_size(m, k, count);
 }
@@ -141,26 +143,42 @@ extern "C" int pq_w4a8_linear_group(const void* x, int x_dtype, const pq_linear_
                       workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int pq_w4a8_linear_group_fused(const void* x, const void* x2, const void* norm_weight, float eps, int mode,
+                                          void* h_out, void* sum_out, int x_dtype, const pq_linear_member* members,
+                                          int count, int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot,
+                                          unsigned flags, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* who = "pq_w4a8_linear_group_fused";
+  PQ_REQUIRE(mode == PQ_PRO_RMSNORM || mode == PQ_PRO_ADD || mode == PQ_PRO_SWIGLU, PQ_ERR_ARG, "%s: mode %d", who,
+             mode);
+  PQ_REQUIRE(x_dtype == PQ_F32 || x_dtype == PQ_F16 || x_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED, "%s: x dtype code %d",
+             who, x_dtype);
+  if (mode == PQ_PRO_RMSNORM)
+    PQ_REQUIRE(eps >= 0.0f && eps < 1.0f, PQ_ERR_ARG, "%s: eps=%g must be in [0, 1)", who, static_cast<double>(eps));
+  if (m > 0) {
+    const size_t es = static_cast<size_t>(pq::dtype_size(x_dtype));
+    if (mode == PQ_PRO_RMSNORM)
+      PQ_REQUIRE(norm_weight != nullptr && pq::aligned_to(norm_weight, es), PQ_ERR_ARG,
+                 "%s: norm_weight must be non-null and aligned to its dtype", who);
+    else
+      PQ_REQUIRE(x2 != nullptr, PQ_ERR_ARG, "%s: mode %d needs x2 (the residual / up rows)", who, mode);
+    PQ_REQUIRE(x2 == nullptr || pq::aligned_to(x2, 16), PQ_ERR_ARG, "%s: x2 (the residual or up rows) must be 16-byte aligned", who);
+    PQ_REQUIRE((h_out == nullptr || pq::aligned_to(h_out, es)) && (sum_out == nullptr || pq::aligned_to(sum_out, es)),
+               PQ_ERR_ARG, "%s: h_out and sum_out must be aligned to x's dtype", who);
+    PQ_REQUIRE(sum_out == nullptr || (mode != PQ_PRO_SWIGLU && x2 != nullptr), PQ_ERR_ARG,
+               "%s: sum_out needs a residual (and no SwiGLU)", who);
+    PQ_REQUIRE(h_out == nullptr || mode != PQ_PRO_ADD, PQ_ERR_ARG, "%s: h_out has no meaning for the add", who);
+  }
+  const pq::NormArgs pro = {x2, mode == PQ_PRO_RMSNORM ? norm_weight : nullptr, h_out, sum_out, eps, mode};
+  return linear_group(who, x, x_dtype, members, count, bias_dtype, y_dtype, m, k, krot, flags, workspace,
+                      workspace_bytes, static_cast<hipStream_t>(stream), &pro);
+}
+
 extern "C" int pq_w4a8_linear_group_rmsnorm(const void* x, const void* residual, const void* norm_weight, float eps,
                                             void* h_out, void* sum_out, int x_dtype,
                                             const pq_linear_member* members, int count, int bias_dtype,
                                             int y_dtype, int64_t m, int64_t k, int krot, unsigned flags,
                                             void* workspace, size_t workspace_bytes, void* stream) {
-  const char* who = "pq_w4a8_linear_group_rmsnorm";
-  PQ_REQUIRE(x_dtype == PQ_F32 || x_dtype == PQ_F16 || x_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED, "%s: x dtype code %d",
-             who, x_dtype);
-  PQ_REQUIRE(eps >= 0.0f && eps < 1.0f, PQ_ERR_ARG, "%s: eps=%g must be in [0, 1)", who, static_cast<double>(eps));
-  if (m > 0) {
-    const size_t es = static_cast<size_t>(pq::dtype_size(x_dtype));
-    PQ_REQUIRE(norm_weight != nullptr && pq::aligned_to(norm_weight, es), PQ_ERR_ARG,
-               "%s: norm_weight must be non-null and aligned to its dtype", who);
-    PQ_REQUIRE(residual == nullptr || pq::aligned_to(residual, 16), PQ_ERR_ARG,
-               "%s: residual must be 16-byte aligned", who);
-    PQ_REQUIRE((h_out == nullptr || pq::aligned_to(h_out, es)) && (sum_out == nullptr || pq::aligned_to(sum_out, es)),
-               PQ_ERR_ARG, "%s: h_out and sum_out must be aligned to x's dtype", who);
-    PQ_REQUIRE(sum_out == nullptr || residual != nullptr, PQ_ERR_ARG, "%s: sum_out needs a residual", who);
-  }
-  const pq::NormArgs norm = {residual, norm_weight, h_out, sum_out, eps};
-  return linear_group(who, x, x_dtype, members, count, bias_dtype, y_dtype, m, k, krot, flags, workspace,
-                      workspace_bytes, static_cast<hipStream_t>(stream), &norm);
+  return pq_w4a8_linear_group_fused(x, residual, norm_weight, eps, PQ_PRO_RMSNORM, h_out, sum_out, x_dtype, members,
+                                    count, bias_dtype, y_dtype, m, k, krot, flags, workspace, workspace_bytes,
+                                    stream);
 }

@@ -225,10 +225,12 @@ __device__ __forceinline__ void load8(const void* base, int64_t elem, float f[8]
 constexpr int kRQWaves = 8;
 
 //
-// With NORM the block first computes the RMSNorm factor of each of its rows
-// (wave r takes row r, with the same per-row routine as the split rotation),
-// then rotates the normalized values; member 0's blocks also write the
-// normalized rows and the residual sum when asked.
+// With NORM the rows first go through the prologue of nm.mode (PQ_PRO_*):
+// RMSNORM computes the RMSNorm factor of each of the block's rows (wave r
+// takes row r, with the same per-row routine as the split rotation) and
+// rotates the normalized values; ADD rotates x + res; SWIGLU rotates
+// silu(x) * up.  Member 0's blocks also write h / the residual sum s when
+// asked.
 template <int DT, int KP, bool MAT16, int RB, bool NORM>
 __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void* __restrict__ x,
                                                                        const pq::RotGroup grp, int64_t row_begin,
@@ -275,10 +277,14 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
     s1 = sp[(g * 128 + 64 + lane) & smask];
   };
 
-  // RMSNorm: residual rows and norm weights ride along with the inputs
-  // (unconditional loads; without a residual they re-read x and are unused).
+  // Prologue: residual / up rows and norm weights ride along with the
+  // inputs (unconditional loads; without a residual or weight they re-read x
+  // and are unused).
   __shared__ float s_rinv[RB];
+  const bool pro_norm = NORM && nm.mode == PQ_PRO_RMSNORM;
+  const bool pro_glu = NORM && nm.mode == PQ_PRO_SWIGLU;
   const void* nres = NORM && nm.res != nullptr ? nm.res : x;
+  const void* nwp = pro_norm ? nm.w : x;
   uint32_t ra[RB], rb[RB], ran[RB], rbn[RB];
   uint32_t wa = 0, wb = 0, wan = 0, wbn = 0;
   auto load_norm = [&](int g, uint32_t (&va)[RB], uint32_t (&vb)[RB], uint32_t& w0, uint32_t& w1) {
@@ -288,11 +294,11 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
         va[r] = pq_load_raw<DT>(nres, (row0 + r) * h + g * 128 + lane);
         vb[r] = pq_load_raw<DT>(nres, (row0 + r) * h + g * 128 + 64 + lane);
       }
-      w0 = pq_load_raw<DT>(nm.w, g * 128 + lane);
-      w1 = pq_load_raw<DT>(nm.w, g * 128 + 64 + lane);
+      w0 = pq_load_raw<DT>(nwp, g * 128 + lane);
+      w1 = pq_load_raw<DT>(nwp, g * 128 + 64 + lane);
     }
   };
-  if constexpr (NORM) {
+  if (pro_norm) {
     if (w < RB) {
       const float r = pqd::rms_inv(pqd::row_sumsq<DT>(x, nm.res, (row0 + w) * h, h, lane), h, nm.eps);
       if (lane == 0) s_rinv[w] = r;
@@ -320,17 +326,24 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
       float lo = pq_raw_to_f32<DT>(xa[r]), hi = pq_raw_to_f32<DT>(xb[r]);
       if constexpr (NORM) {
         const int64_t ro = (row0 + r) * h + g * 128 + lane;
-        if (nm.res != nullptr) {
-          lo = pqd::round_to_dt<DT>(lo + pq_raw_to_f32<DT>(ra[r]));
-          hi = pqd::round_to_dt<DT>(hi + pq_raw_to_f32<DT>(rb[r]));
+        if (pro_glu) {
+          lo = pqd::swiglu<DT>(lo, pq_raw_to_f32<DT>(ra[r]));
+          hi = pqd::swiglu<DT>(hi, pq_raw_to_f32<DT>(rb[r]));
+        } else {
+          if (nm.res != nullptr) {
+            lo = pqd::round_to_dt<DT>(lo + pq_raw_to_f32<DT>(ra[r]));
+            hi = pqd::round_to_dt<DT>(hi + pq_raw_to_f32<DT>(rb[r]));
+          }
+          if (write_norm && nm.s_out != nullptr) {
+            pq_store_from_f32<DT>(nm.s_out, ro, lo);
+            pq_store_from_f32<DT>(nm.s_out, ro + 64, hi);
+          }
+          if (pro_norm) {
+            lo = pqd::rms_apply<DT>(lo, s_rinv[r], pq_raw_to_f32<DT>(wa));
+            hi = pqd::rms_apply<DT>(hi, s_rinv[r], pq_raw_to_f32<DT>(wb));
+          }
         }
-        if (write_norm && nm.s_out != nullptr) {
-          pq_store_from_f32<DT>(nm.s_out, ro, lo);
-          pq_store_from_f32<DT>(nm.s_out, ro + 64, hi);
-        }
-        lo = pqd::rms_apply<DT>(lo, s_rinv[r], pq_raw_to_f32<DT>(wa));
-        hi = pqd::rms_apply<DT>(hi, s_rinv[r], pq_raw_to_f32<DT>(wb));
-        if (write_norm && nm.h_out != nullptr) {
+        if ((pro_norm || pro_glu) && write_norm && nm.h_out != nullptr) {
           pq_store_from_f32<DT>(nm.h_out, ro, lo);
           pq_store_from_f32<DT>(nm.h_out, ro + 64, hi);
         }
@@ -445,7 +458,8 @@ __global__ __launch_bounds__(kSplitWaves * 64) void rotate_split_kernel(const vo
   const bool first = blockIdx.y == 0;
   pqd::rotate_group_rows<DT, KP, MAT16, MR, NORM>(x, mb.rot_idx, mb.rot_cs, mb.scales, mb.out, mb.out_scale, M, h,
                                                   krot, flags, g, threadIdx.x & 63, nm.res, nm.w,
-                                                  first ? nm.h_out : nullptr, first ? nm.s_out : nullptr, nm.eps);
+                                                  first ? nm.h_out : nullptr, first ? nm.s_out : nullptr, nm.eps,
+                                                  nm.mode);
 }
 
 template <int DT, int KP, bool MAT16, bool NORM>

@@ -64,6 +64,10 @@ _pq_lib.define("w4a8_linear_group_rmsnorm(Tensor x, Tensor? residual, Tensor nor
                "Tensor[] rot_idx, Tensor[] rot_cs, Tensor?[] scales, int krot, Tensor[] wpack, Tensor[] wmeta, "
                "Tensor?[] bias, Tensor? workspace, bool input_fp16, bool materialize_fp16, ScalarType out_dtype, "
                "bool return_normed, bool return_sum) -> Tensor[]")
+_pq_lib.define("w4a8_linear_group_fused(Tensor x, Tensor? x2, Tensor? norm_weight, float eps, int mode, "
+               "Tensor[] rot_idx, Tensor[] rot_cs, Tensor?[] scales, int krot, Tensor[] wpack, Tensor[] wmeta, "
+               "Tensor?[] bias, Tensor? workspace, bool input_fp16, bool materialize_fp16, ScalarType out_dtype, "
+               "bool return_h, bool return_sum) -> Tensor[]")
 _pq_lib.define("w4a16_prepack(Tensor awq_qweight, Tensor scales, Tensor scaled_zeros) -> (Tensor, Tensor)")
 _pq_lib.define("w4a16_gemm(Tensor x, Tensor wpack, Tensor wmeta, Tensor? bias, ScalarType out_dtype) -> Tensor")
 _pq_lib.define("w4a16_linear(Tensor x, Tensor rot_idx, Tensor rot_cs, Tensor? scales, int krot, Tensor wpack, "
@@ -542,44 +546,72 @@ def _linear_group_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, wor
     return [y.view(*x.shape[:-1], y.size(1)) for y in outs]
 
 
-def _linear_group_rmsnorm_impl(x, residual, norm_weight, eps, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
-                               workspace, input_fp16, materialize_fp16, out_dtype, return_normed, return_sum):
+def _linear_group_fused_impl(x, x2, norm_weight, eps, mode, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
+                             workspace, input_fp16, materialize_fp16, out_dtype, return_h, return_sum):
     dev = x.device
     _require(x.dtype in _DT, f"x must be float32/float16/bfloat16, got {x.dtype}")
+    _require(mode in (_lib.PQ_PRO_RMSNORM, _lib.PQ_PRO_ADD, _lib.PQ_PRO_SWIGLU), f"unknown prologue mode {mode}")
     xc = x.contiguous()
     k = xc.size(-1)
-    _require(norm_weight.dtype == x.dtype and norm_weight.numel() == k,
-             f"norm_weight must hold {k} values of x's dtype {x.dtype}")
-    _same_device("norm_weight", norm_weight, dev)
-    w = norm_weight.contiguous()
-    res = None
-    if residual is not None:
-        _require(residual.shape == x.shape and residual.dtype == x.dtype, "residual must match x's shape and dtype")
-        _same_device("residual", residual, dev)
-        res = residual.contiguous()
-    _require(not return_sum or res is not None, "return_sum needs a residual")
+    w = None
+    if mode == _lib.PQ_PRO_RMSNORM:
+        _require(norm_weight is not None and norm_weight.dtype == x.dtype and norm_weight.numel() == k,
+                 f"norm_weight must hold {k} values of x's dtype {x.dtype}")
+        _same_device("norm_weight", norm_weight, dev)
+        w = norm_weight.contiguous()
+    else:
+        _require(x2 is not None, "the add and the SwiGLU need x2 (residual / up)")
+    other = None
+    if x2 is not None:
+        _require(x2.shape == x.shape and x2.dtype == x.dtype, "x2 (residual / up) must match x's shape and dtype")
+        _same_device("x2", x2, dev)
+        other = x2.contiguous()
+    _require(not return_sum or (other is not None and mode != _lib.PQ_PRO_SWIGLU),
+             "return_sum needs a residual (RMSNorm with residual, or the add)")
+    _require(not return_h or mode != _lib.PQ_PRO_ADD, "the add has no h: use return_sum")
     members, outs, keep, bias_dt, m, _ = _group_members(xc, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
                                                         out_dtype)
     count = len(outs)
-    h = torch.empty_like(xc) if return_normed else None
+    h = torch.empty_like(xc) if return_h else None
     sm = torch.empty_like(xc) if return_sum else None
     scratch = _group_scratch(workspace, m, k, count, dev)
     flags = (_lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0) | (_lib.PQ_RQ_MATERIALIZE_FP16 if materialize_fp16 else 0)
     lib = _lib.load()
     with _DeviceGuard(dev):
-        st = lib.pq_w4a8_linear_group_rmsnorm(
-            xc.data_ptr(), res.data_ptr() if res is not None else None, w.data_ptr(), float(eps),
-            h.data_ptr() if h is not None else None, sm.data_ptr() if sm is not None else None, _DT[x.dtype],
-            members, count, bias_dt, _DT[out_dtype], m, k, krot, flags,
-            scratch.data_ptr() if scratch is not None else None, scratch.numel() if scratch is not None else 0,
-            _stream(dev))
-    _lib.check(st, "paroquant::w4a8_linear_group_rmsnorm")
+        st = lib.pq_w4a8_linear_group_fused(
+            xc.data_ptr(), other.data_ptr() if other is not None else None, w.data_ptr() if w is not None else None,
+            float(eps), int(mode), h.data_ptr() if h is not None else None,
+            sm.data_ptr() if sm is not None else None, _DT[x.dtype], members, count, bias_dt, _DT[out_dtype], m, k,
+            krot, flags, scratch.data_ptr() if scratch is not None else None,
+            scratch.numel() if scratch is not None else 0, _stream(dev))
+    _lib.check(st, "paroquant::w4a8_linear_group_fused")
     res_out = [y.view(*x.shape[:-1], y.size(1)) for y in outs]
     if h is not None:
         res_out.append(h.view(x.shape))
     if sm is not None:
         res_out.append(sm.view(x.shape))
     return res_out
+
+
+_pq_lib.impl("w4a8_linear_group_fused", _linear_group_fused_impl, "CUDA")
+
+
+@torch.library.register_fake("paroquant::w4a8_linear_group_fused")
+def _linear_group_fused_fake(x, x2, norm_weight, eps, mode, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
+                             workspace, input_fp16, materialize_fp16, out_dtype, return_h, return_sum):
+    outs = [x.new_empty((*x.shape[:-1], w.size(0) * 16), dtype=out_dtype) for w in wpack]
+    if return_h:
+        outs.append(torch.empty_like(x))
+    if return_sum:
+        outs.append(torch.empty_like(x))
+    return outs
+
+
+def _linear_group_rmsnorm_impl(x, residual, norm_weight, eps, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
+                               workspace, input_fp16, materialize_fp16, out_dtype, return_normed, return_sum):
+    return _linear_group_fused_impl(x, residual, norm_weight, eps, _lib.PQ_PRO_RMSNORM, rot_idx, rot_cs, scales, krot,
+                                    wpack, wmeta, bias, workspace, input_fp16, materialize_fp16, out_dtype,
+                                    return_normed, return_sum)
 
 
 _pq_lib.impl("w4a8_linear_group_rmsnorm", _linear_group_rmsnorm_impl, "CUDA")
@@ -603,6 +635,11 @@ _pq_lib.impl("w4a8_linear_group", _linear_group_impl, "CUDA")
 def _linear_group_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16,
                        materialize_fp16, out_dtype):
     return [x.new_empty((*x.shape[:-1], w.size(0) * 16), dtype=out_dtype) for w in wpack]
+
+
+def split_path(m: int, k: int) -> bool:
+    """True when the linear entry points run m tokens of k features on the split-rotation kernel pair."""
+    return bool(_lib.load().pq_w4a8_linear_split_path(m, k))
 
 
 def linear_group_workspace_bytes(m: int, k: int, count: int) -> int:

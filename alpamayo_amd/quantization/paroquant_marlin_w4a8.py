@@ -123,12 +123,7 @@ class SharedInputRotateLinears(nn.Module):
     def _rotate_linears(self):
         return [m.rotate_linear if self.bf16_inputs else m for m in self.members]
 
-    def forward(self, x: torch.Tensor, norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
-                residual: torch.Tensor | None = None, return_normed: bool = False, return_sum: bool = False):
-        """The members' outputs on x, or, with ``norm_weight``, on the decoder layer's RMSNorm of
-        x (+ residual): h = weight * (s * rsqrt(mean(s^2) + eps)) with s = x + residual, in x's dtype
-        (Qwen3VLTextRMSNorm.forward, modeling_qwen3_vl.py:354-359), computed inside the group's
-        rotation launch.  ``return_normed`` / ``return_sum`` append h / s to the outputs."""
+    def _args(self, x):
         rls = self._rotate_linears()
         for rl in rls:
             rl.qlinear._check_loaded()
@@ -138,16 +133,52 @@ class SharedInputRotateLinears(nn.Module):
         need = _ops.linear_group_workspace_bytes(x.numel() // k, k, len(rls))
         if self.workspace.numel() < need or self.workspace.device != x.device:
             self.workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
-        args = ([rl.rotation.rot_idx for rl in rls], [rl.rotation.rot_cs for rl in rls],
+        return ([rl.rotation.rot_idx for rl in rls], [rl.rotation.rot_cs for rl in rls],
                 [rl.rotation.scales_f32 for rl in rls], rls[0].rotation.krot, [rl.qlinear.qweight for rl in rls],
                 [rl.qlinear.scales for rl in rls], [rl.qlinear.bias for rl in rls], self.workspace,
                 self.bf16_inputs, True, x.dtype)
-        if norm_weight is None:
-            if residual is not None or return_normed or return_sum:
-                raise ValueError("residual / return_normed / return_sum need norm_weight")
-            return tuple(torch.ops.paroquant.w4a8_linear_group(x, *args))
-        outs = torch.ops.paroquant.w4a8_linear_group_rmsnorm(x, residual, norm_weight.to(x.dtype), float(eps), *args,
-                                                             return_normed, return_sum)
+
+    def forward(self, x: torch.Tensor, norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                residual: torch.Tensor | None = None, return_normed: bool = False, return_sum: bool = False):
+        """The members' outputs on x; with ``norm_weight``, on the decoder layer's RMSNorm of
+        x (+ residual): h = weight * (s * rsqrt(mean(s^2) + eps)) with s = x + residual, in x's dtype
+        (Qwen3VLTextRMSNorm.forward, modeling_qwen3_vl.py:354-359); with only ``residual``, on
+        s = x + residual (a decoder layer's residual add).  The norm runs inside the group's rotation
+        launch; the add does where the group runs the split rotation (decode sizes), and as a
+        separate torch add otherwise, which measured faster there.  ``return_normed`` /
+        ``return_sum`` append h / s to the outputs."""
+        args = self._args(x)
+        if norm_weight is not None:
+            outs = torch.ops.paroquant.w4a8_linear_group_fused(x, residual, norm_weight.to(x.dtype), float(eps),
+                                                               _ops._lib.PQ_PRO_RMSNORM, *args, return_normed,
+                                                               return_sum)
+        elif residual is not None:
+            if return_normed:
+                raise ValueError("return_normed needs norm_weight (the add alone returns its sum: return_sum)")
+            if _ops.split_path(x.numel() // x.size(-1), x.size(-1)):
+                outs = torch.ops.paroquant.w4a8_linear_group_fused(x, residual, None, 0.0, _ops._lib.PQ_PRO_ADD,
+                                                                   *args, False, return_sum)
+            else:   # the row kernel: a separate add is cheaper (same result bit for bit)
+                s = x + residual
+                outs = list(torch.ops.paroquant.w4a8_linear_group(s, *args)) + ([s] if return_sum else [])
+        else:
+            if return_normed or return_sum:
+                raise ValueError("return_normed / return_sum need norm_weight or residual")
+            outs = torch.ops.paroquant.w4a8_linear_group(x, *args)
+        return tuple(outs)
+
+    def forward_swiglu(self, gate: torch.Tensor, up: torch.Tensor, return_act: bool = False):
+        """The members' outputs on act = silu(gate) * up in the inputs' dtype (a gated MLP's down_proj
+        input, patches.py:541-548: silu in float32, rounded, times up, rounded), formed inside the
+        group's rotation launch where the group runs the split rotation (decode sizes), by torch's
+        silu and mul otherwise (measured faster there).  ``return_act`` appends act."""
+        args = self._args(gate)
+        if _ops.split_path(gate.numel() // gate.size(-1), gate.size(-1)):
+            outs = torch.ops.paroquant.w4a8_linear_group_fused(gate, up, None, 0.0, _ops._lib.PQ_PRO_SWIGLU, *args,
+                                                               return_act, False)
+        else:   # the row kernel: separate elementwise kernels are cheaper (same rows, up to silu's last bit)
+            act = torch.nn.functional.silu(gate) * up
+            outs = list(torch.ops.paroquant.w4a8_linear_group(act, *args)) + ([act] if return_act else [])
         return tuple(outs)
 
 

@@ -303,8 +303,9 @@ def main() -> int:
 
     # ---- speculative verify block: 36 chained layers at M = 16 -------------
     # Per layer a -> (q, k, v) = L(a); o = L_o(q); h = RMSNorm_bf16(a + o) (eps 1e-6, weight U(0.8, 1.2));
-    # d = L_down(silu(L_gate(h)) * L_up(h)); next a = h + d.  The norm and the residual add run inside the
-    # gate/up group's rotation launch.  Fresh random int4 weights per layer; the whole block is captured as one
+    # d = L_down(silu(L_gate(h)) * L_up(h)); next a = h + d.  The norm and its residual add run inside the
+    # gate/up group's rotation launch, silu * mul inside the down linear's, the h + d add inside the next
+    # layer's q/k/v rotation.  Fresh random int4 weights per layer; the whole block is captured as one
     # graph.  Reported: time per verified block, and the 252 quantized linears of the
     # block alone (the same linears and inputs without the norms / activations in between).
     verify = None
@@ -317,26 +318,32 @@ def main() -> int:
             L = [workloads.build_module(workloads.linear_spec(n, N, K, g, device=dev), dev)
                  for n, (N, K) in zip(names, shapes)]
             w_norm = (0.8 + 0.4 * torch.rand(H, generator=g, device=dev)).to(torch.bfloat16)
-            vlayers.append((L, SharedInputRotateLinears(L[0:3]), SharedInputRotateLinears(L[4:6]), w_norm))
+            vlayers.append((L, SharedInputRotateLinears(L[0:3]), SharedInputRotateLinears(L[4:6]),
+                            SharedInputRotateLinears(L[6:7]), w_norm))
         torch.cuda.synchronize()
         log(f"verify block: {Lv} layers built ({time.time() - t0:.1f}s)")
         a0 = workloads.activations(Mv, H, workloads.generator(3000, device=dev), device=dev)
 
         def run_block(a):
-            for L, qkv, gu, w_norm in vlayers:
-                q, _, _ = qkv(a)
+            h = d = None
+            for L, qkv, gu, down, w_norm in vlayers:
+                if d is None:
+                    q, _, _ = qkv(a)
+                else:
+                    # a = h + d (the previous layer's residual add) inside the q/k/v rotation launch
+                    q, _, _, a = qkv(h, residual=d, return_sum=True)
                 o = L[3](q)
                 # h = RMSNorm(a + o) inside the gate/up group's rotation launch (also returned: next a = h + d)
                 gt, up, h = gu(o, norm_weight=w_norm, eps=1e-6, residual=a, return_normed=True)
-                d = L[6](torch.nn.functional.silu(gt) * up)
-                a = h + d
-            return a
+                # silu(gate) * up inside the down linear's rotation launch
+                (d,) = down.forward_swiglu(gt, up)
+            return h + d
 
         lin_in = [(a0, a0, a0, torch.nn.functional.silu(a0[:, :1].repeat(1, 3 * H)))]   # fixed inputs per layer
 
         def run_linears():
             xa, _, _, xd = lin_in[0]
-            for L, qkv, gu, _ in vlayers:
+            for L, qkv, gu, _, _ in vlayers:
                 q, _, _ = qkv(xa)
                 L[3](q)
                 gu(xa)
@@ -357,6 +364,34 @@ def main() -> int:
                   "linears_frac_hbm": round(vb / (vres["linears"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         log(f"verify block M=16 x 36 layers: {vres['block']:.3f} ms/block; quantized linears alone "
             f"{vres['linears']:.3f} ms ({verify['linears_GBps']:.0f} GB/s)")
+        # The same 36-layer chain at one token: a decode step's quantized linears with the layer's
+        # elementwise steps between them.  At this size the residual add and silu * mul also run inside
+        # the rotation launches (the split-rotation path); "unfused" runs them as torch ops.
+        a1 = workloads.activations(1, H, workloads.generator(3010, device=dev), device=dev)
+
+        def run_block_unfused(a):
+            h = d = None
+            for L, qkv, gu, _, w_norm in vlayers:
+                if d is not None:
+                    a = h + d
+                q, _, _ = qkv(a)
+                o = L[3](q)
+                gt, up, h = gu(o, norm_weight=w_norm, eps=1e-6, residual=a, return_normed=True)
+                d = L[6](torch.nn.functional.silu(gt) * up)
+            return h + d
+
+        dres = {}
+        for key, fn in (("fused", lambda: run_block(a1)), ("unfused", lambda: run_block_unfused(a1))):
+            fn()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                fn()
+            dres[key] = time_graphs([gr], max(5, args.prefill_steps), 2)
+            del gr
+        verify["decode_chain_M1"] = {"ms_per_step": round(dres["fused"], 4),
+                                     "elementwise_as_torch_ops_ms": round(dres["unfused"], 4)}
+        log(f"decode chain M=1 x 36 layers: {dres['fused']:.3f} ms/step; with the add and silu*mul as torch "
+            f"ops {dres['unfused']:.3f} ms")
         del vlayers
 
     # ---- ragged packed batch: 8 requests of U{1..512} tokens ----------------

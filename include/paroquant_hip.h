@@ -64,6 +64,11 @@ enum pq_dtype { PQ_F32 = 0, PQ_F16 = 1, PQ_BF16 = 2 };
 #define PQ_RQ_INPUT_FP16 1u        /* round the input to fp16 first (the bf16->fp16 wrapper cast) */
 #define PQ_RQ_MATERIALIZE_FP16 2u  /* round rotated values to fp16 before quantizing */
 
+/* Prologue of pq_w4a8_linear_group_fused: what the members rotate, from x and x2. */
+#define PQ_PRO_RMSNORM 1  /* h = RMSNorm(x + x2) (x2 may be NULL), as pq_w4a8_linear_group_rmsnorm */
+#define PQ_PRO_ADD 2      /* s = x + x2 (the residual add of a decoder layer) */
+#define PQ_PRO_SWIGLU 3   /* h = silu(x) * x2 (x = gate, x2 = up: a gated MLP's down_proj input) */
+
 int pq_abi_version(void);
 const char* pq_last_error(void);
 
@@ -188,6 +193,14 @@ typedef struct pq_linear_member {
   int64_t n;               /* output features, a positive multiple of 16 */
 } pq_linear_member;
 
+/* 1 when pq_w4a8_linear (and the group entry points) run m tokens of k
+ * features as a split rotation (one wave per 128-channel group for all rows)
+ * plus a GEMM that quantizes A in its prologue, 0 when they run the row
+ * rotate+quant kernel plus the GEMM.  Callers use it to decide whether an
+ * elementwise step is cheaper fused into the rotation launch (it is on the
+ * split path) or as a separate kernel.  No counterpart in the reference. */
+int pq_w4a8_linear_split_path(int64_t m, int64_t k);
+
 /* Bytes of workspace pq_w4a8_linear_group needs for count members sharing an
  * [m, k] input: count times what pq_w4a8_linear needs for one (it does not
  * depend on n). */
@@ -260,6 +273,27 @@ int pq_w4a16_linear(const void* x, int x_dtype, const uint32_t* rot_idx, const f
                     const uint8_t* wpack, const uint32_t* wmeta, const void* bias, int bias_dtype, void* y,
                     int y_dtype, int64_t m, int64_t n, int64_t k, int krot, unsigned flags, void* workspace,
                     size_t workspace_bytes, void* stream);
+
+/* pq_w4a8_linear_group behind a decoder layer's elementwise step, chosen by
+ * mode (PQ_PRO_*), in the same two launches; the members read
+ *   PQ_PRO_RMSNORM: h = RMSNorm(x + x2) exactly as pq_w4a8_linear_group_rmsnorm
+ *                   (x2 = residual, may be NULL; norm_weight, eps as there);
+ *   PQ_PRO_ADD:     s = x + x2 (rounded to x's dtype; x2 required);
+ *   PQ_PRO_SWIGLU:  h = round(round(silu(x)) * x2), silu(x) = x / (1 + exp(-x))
+ *                   in float32 (x = gate, x2 = up, both [m, k]).
+ * h_out ([m, k], x's dtype, RMSNORM / SWIGLU) and sum_out (s, RMSNORM with
+ * x2 / ADD) are written when non-NULL; x2 16-byte aligned.  norm_weight and
+ * eps are read for RMSNORM only.
+ * Reference: the Qwen3-VL decoder layer around its linears
+ * (src/alpamayo_r1/models/qwen3_vl/modeling_qwen3_vl.py:354-359 RMSNorm,
+ * the residual adds of the layer, and the MLP's down_proj(act(gate) * up),
+ * patches.py:541-548), each linear a BF16RotateLinearWrapper
+ * (paroquant_marlin_w4a8.py:59-65).  No counterpart of the fusion itself in
+ * the reference. */
+int pq_w4a8_linear_group_fused(const void* x, const void* x2, const void* norm_weight, float eps, int mode,
+                               void* h_out, void* sum_out, int x_dtype, const pq_linear_member* members, int count,
+                               int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot, unsigned flags,
+                               void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

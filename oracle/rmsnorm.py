@@ -1,4 +1,7 @@
-"""RMSNorm in front of a shared-input group of W4A8 linears -- TEST INFRASTRUCTURE ONLY.
+"""Elementwise steps of a decoder layer in front of its W4A8 linears -- TEST INFRASTRUCTURE ONLY.
+
+RMSNorm (below), the residual add (``residual_sum``) and the gated MLP's
+activation (``swiglu``).
 
 Restates Qwen3VLTextRMSNorm.forward
 (src/alpamayo_r1/models/qwen3_vl/modeling_qwen3_vl.py:354-359) with the
@@ -58,3 +61,13 @@ def rmsnorm(x: np.ndarray, weight: np.ndarray, eps: float, residual: np.ndarray 
     w = np.asarray(weight, dtype=np.float32)
     h = round_to(w * round_to(s * r, dtype), dtype)
     return h, s
+
+
+def swiglu(gate: np.ndarray, up: np.ndarray, dtype: str = "bf16") -> np.ndarray:
+    """A gated MLP's down_proj input, act_fn(gate_proj(x)) * up_proj(x) with SiLU
+    (patches.py:541-548), in the module's rounding: silu in float32
+    (g / (1 + exp(-g))) rounded to `dtype`, times up, rounded to `dtype`."""
+    g = np.asarray(gate, dtype=np.float32)
+    with np.errstate(over="ignore"):
+        a = round_to(g / (np.float32(1) + np.exp(-g)), dtype)
+    return round_to(a * np.asarray(up, dtype=np.float32), dtype)

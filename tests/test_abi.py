@@ -208,3 +208,36 @@ def test_rotate_mxfp4_argument_checks():
     assert call(q=ctypes.c_void_p(258)) == 1 and "aligned" in _err(lib)
     assert call(s=None) == 1 and "null" in _err(lib)
     assert call(rows=0) == 0
+
+
+def test_linear_group_fused_argument_checks():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    mem = (_lib.LinearMember * 1)()
+    mem[0] = _lib.LinearMember(256, 256, None, 256, 256, None, 256, 64)
+    args = dict(count=1, bias_dtype=0, y_dtype=2, m=1, k=4096, krot=8, flags=3, ws=p, wsb=1 << 20, stream=None)
+
+    def call(mode, x2=p, w=None, eps=0.0, h=None, s=None, **kw):
+        a = dict(args, **kw)
+        return lib.pq_w4a8_linear_group_fused(p, x2, w, eps, mode, h, s, 2, mem, a["count"], a["bias_dtype"],
+                                              a["y_dtype"], a["m"], a["k"], a["krot"], a["flags"], a["ws"], a["wsb"],
+                                              a["stream"])
+
+    assert call(7) == 1 and "mode" in _err(lib)
+    assert call(_lib.PQ_PRO_ADD, x2=None) == 1 and "x2" in _err(lib)
+    assert call(_lib.PQ_PRO_SWIGLU, x2=None) == 1
+    assert call(_lib.PQ_PRO_ADD, h=p) == 1 and "h_out" in _err(lib)
+    assert call(_lib.PQ_PRO_SWIGLU, s=p) == 1 and "sum_out" in _err(lib)
+    assert call(_lib.PQ_PRO_RMSNORM, w=None, eps=1e-6) == 1 and "norm_weight" in _err(lib)
+    assert call(_lib.PQ_PRO_ADD, x2=ctypes.c_void_p(258)) == 1 and "aligned" in _err(lib)
+    assert call(_lib.PQ_PRO_SWIGLU, m=0) == 0
+
+
+def test_split_path_rule():
+    lib = _lib.load()
+    assert lib.pq_w4a8_linear_split_path(1, 4096) == 1
+    assert lib.pq_w4a8_linear_split_path(3, 4096) == 1
+    assert lib.pq_w4a8_linear_split_path(1, 12288) == 1
+    assert lib.pq_w4a8_linear_split_path(4, 4096) == 0
+    assert lib.pq_w4a8_linear_split_path(2, 12288) == 0
+    assert lib.pq_w4a8_linear_split_path(0, 4096) == 0

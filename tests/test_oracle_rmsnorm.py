@@ -4,6 +4,7 @@ reference's Qwen3VLTextRMSNorm.forward, modeling_qwen3_vl.py:354-359), and
 by invariants (scale invariance, unit mean square, eps dominance)."""
 
 import numpy as np
+import pytest
 import torch
 
 from oracle import linear as olin
@@ -50,3 +51,26 @@ def test_eps_dominates_tiny_rows():
     x = np.full((2, 256), 1e-8, np.float32)
     h, _ = orms.rmsnorm(x, np.ones(256, np.float32), 1e-6, dtype="f32")
     np.testing.assert_allclose(h, 1e-8 / np.sqrt(1e-16 + 1e-6), rtol=1e-5)
+
+
+@pytest.mark.parametrize("dtype,tdt", [("bf16", torch.bfloat16), ("f16", torch.float16)])
+def test_swiglu_matches_torch_silu_mul(dtype, tdt):
+    """act = silu(g) * u in the module's dtype, against torch's own silu and mul on the CPU."""
+    gen = torch.Generator().manual_seed(5150)
+    g = (3 * torch.randn(64, 1024, generator=gen)).to(tdt)
+    u = torch.randn(64, 1024, generator=gen).to(tdt)
+    ref = (torch.nn.functional.silu(g) * u).float().numpy()
+    got = orms.swiglu(g.float().numpy(), u.float().numpy(), dtype)
+    # a one-ulp difference in silu(g) (float32 exp of numpy vs torch's vector exp) can move the
+    # product by up to two ulps of the result: 2^-9 relative for fp16, 2^-6 for bf16
+    ulp = np.maximum(np.abs(got), np.abs(ref)).astype(np.float64) * 2.0 ** (-9 if dtype == "f16" else -6)
+    diff = np.abs(got.astype(np.float64) - ref)
+    assert np.all(diff <= ulp + 6e-8)   # (+ the fp16 subnormal step)
+    assert np.mean(diff == 0) >= 0.999
+
+
+def test_swiglu_special_values():
+    g = np.array([0.0, -0.0, 100.0, -100.0, 1e-30], dtype=np.float32)
+    u = np.array([5.0, 5.0, 2.0, 2.0, 1.0], dtype=np.float32)
+    a = orms.swiglu(g, u, "f32")
+    assert a[0] == 0 and a[2] == 200.0 and abs(a[3]) < 1e-40 and a[4] == np.float32(0.5e-30)
