@@ -325,7 +325,18 @@ constexpr int kPfStages = 3;
 constexpr int kPfGroupM = 4;   // tile rows walked together by one XCD's run of tiles
 constexpr int kPfBStride = 1024 + 128;
 
-template <int BM, int BN, int WM, int WN, bool PARTIALS>
+// Wait until at most `ahead` groups of copies (L copies each) are in flight.
+template <int L, int A>
+__device__ __forceinline__ void wait_groups(int ahead) {
+  if constexpr (A == 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (ahead >= A) wait_vmcnt<L * A>();
+    else wait_groups<L, A - 1>(ahead);
+  }
+}
+
+template <int BM, int BN, int WM, int WN, bool PARTIALS, int ST = kPfStages>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
     const pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* __restrict__ partials, int M, int K) {
   constexpr int NW = WM * WN;
@@ -456,7 +467,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn)
           T[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[tm], b[tn], T[tm][tn], 0, 0, 0);
-      if (i == 1 && ig < G) issue(ig, ig % kPfStages);
+      if (i == 1 && ig < G) issue(ig, ig % ST);
     }
     if constexpr (PARTIALS) {
 #pragma unroll
@@ -480,23 +491,25 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
     }
   };
 
-  // Stage g % 3 holds group g.  Before computing g, each wave waits for its
-  // own loads of g (those of g+1 may stay in flight), then a barrier makes
-  // everybody's loads of g visible and retires everybody's use of the stage
-  // that group g+2 is about to overwrite.
+  // Stage g % ST holds group g; the copies run ST-1 groups ahead.  Before
+  // computing g, each wave waits for its own loads of g (those of the later
+  // groups may stay in flight), then a barrier makes everybody's loads of g
+  // visible and retires everybody's use of the stage that group g+ST-1 is
+  // about to overwrite (group g-1's).
   // The tile's activation scales go to LDS past the ring ahead of every
   // other load, so the first wait covers them (the partials mode has none).
   if (!PARTIALS && wave * 64 < BM) {
     const int r = min(wave * 64 + lane, BM - 1);
-    lds_copy4(xs + min(bm * BM + r, M - 1), lds0 + kPfStages * STAGE + wave * 256);
+    lds_copy4(xs + min(bm * BM + r, M - 1), lds0 + ST * STAGE + wave * 256);
   }
-  issue(0, 0);
-  if (G > 1) issue(1, 1);
+  static_assert(LOADS * (ST - 2) < 64, "vmcnt range");
+#pragma unroll
+  for (int q = 0; q < ST - 1; ++q)
+    if (q < G) issue(q, q);
   for (int g = 0; g < G; ++g) {
-    if (g + 1 < G) wait_vmcnt<LOADS>();
-    else wait_vmcnt<0>();
+    wait_groups<LOADS, ST - 2>(min(G - 1 - g, ST - 2));
     __builtin_amdgcn_s_barrier();
-    compute(g % kPfStages, g, g + 2);
+    compute(g % ST, g, g + ST - 1);
   }
   if constexpr (PARTIALS) return;
 
@@ -509,8 +522,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
   // values are loaded once and the output type is a template parameter:
   // a global load or a dtype branch inside the element loop makes the
   // compiler wait for the stores in flight (vmcnt(0)) at every join.
-  static_assert(kPfStages * STAGE >= WM * 32 * (BN * 4 + 32), "output slice fits in the stage ring");
-  const float* xs_tile = reinterpret_cast<const float*>(smem + kPfStages * STAGE);
+  static_assert(ST * STAGE >= WM * 32 * (BN * 4 + 32), "output slice fits in the stage ring");
+  const float* xs_tile = reinterpret_cast<const float*>(smem + ST * STAGE);
   const bool has_bias = bias != nullptr;
   float bv[TN];
 #pragma unroll
@@ -554,28 +567,33 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
   else emit(std::integral_constant<int, PQ_BF16>{});
 }
 
-template <int BM, int BN, int WM, int WN, bool PARTIALS>
+template <int BM, int BN, int WM, int WN, bool PARTIALS, int ST = kPfStages>
 void launch_prefill_t(pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* partials, int M, int K,
                       hipStream_t stream) {
   constexpr int STAGE = BM * 128 + (BN / 16) * kPfBStride + BN * 4;
   grp.first[0] = 0;
   for (int i = 0; i < grp.count; ++i) grp.first[i + 1] = grp.first[i] + (grp.mem[i].n + BN - 1) / BN;
   const unsigned grid = static_cast<unsigned>(((M + BM - 1) / BM) * grp.first[grp.count]);
-  gemm_prefill<BM, BN, WM, WN, PARTIALS><<<grid, WM * WN * 64, kPfStages * STAGE + BM * 4, stream>>>(
+  gemm_prefill<BM, BN, WM, WN, PARTIALS, ST><<<grid, WM * WN * 64, ST * STAGE + BM * 4, stream>>>(
       grp, bias_dtype, y_dtype, partials, M, K);
 }
 
 // 192 x 256 tiles (8 waves of 192 x 32) when there are enough of them to
-// fill the chip, else 128 x 128 (4 waves, several workgroups per CU).
+// fill the chip, else 128 x 128 (4 waves, several workgroups per CU) when
+// those fill it, else 64 x 128 (k/v at M = 3072: 43.4 -> 37.2 us).
 template <bool PARTIALS>
 void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32_t* partials, int M, int K,
                     hipStream_t stream) {
   int64_t bn_tiles = 0;
   for (int i = 0; i < grp.count; ++i) bn_tiles += (grp.mem[i].n + 255) / 256;
+  int64_t bn128 = 0;
+  for (int i = 0; i < grp.count; ++i) bn128 += (grp.mem[i].n + 127) / 128;
   if (static_cast<int64_t>((M + 191) / 192) * bn_tiles >= 256)
     launch_prefill_t<192, 256, 1, 8, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
-  else
+  else if (static_cast<int64_t>((M + 127) / 128) * bn128 >= 256)
     launch_prefill_t<128, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
+  else   // narrow outputs (k/v): twice the workgroups of 128-row tiles
+    launch_prefill_t<64, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
 }
 
 // ---------------------------------------------------------------------------
