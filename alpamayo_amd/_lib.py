@@ -21,6 +21,7 @@ PQ_F32, PQ_F16, PQ_BF16 = 0, 1, 2
 PQ_RQ_INPUT_FP16 = 1
 PQ_RQ_MATERIALIZE_FP16 = 2
 PQ_PRO_RMSNORM, PQ_PRO_ADD, PQ_PRO_SWIGLU = 1, 2, 3
+PQ_ROWS_SAME, PQ_ROWS_MXFP4 = 0, 1
 
 STATUS_NAMES = {0: "PQ_OK", 1: "PQ_ERR_ARG", 2: "PQ_ERR_UNSUPPORTED", 3: "PQ_ERR_HIP", 4: "PQ_ERR_WORKSPACE"}
 STATUS_CODE = {v: k for k, v in STATUS_NAMES.items()}
@@ -46,6 +47,7 @@ SIGNATURES = {
     "pq_last_error": (ctypes.c_char_p, []),
     "pq_rotate": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _INT, _INT, _INT, _P]),
     "pq_rotate_mxfp4": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _INT, _INT, _INT, _P]),
+    "pq_rotate_rows": (_INT, [_P, _INT, _P, _P, _P, _P, _P, _I64, _I64, _INT, _INT, _P]),
     "pq_rotate_quant_i8": (_INT, [_P, _INT, _P, _P, _P, _P, _P, _P, _I64, _I64, _INT, _UINT, _P]),
     "pq_quant_i8": (_INT, [_P, _INT, _P, _P, _I64, _I64, _P]),
     "pq_w4a8_workspace_size": (_SZ, [_I64, _I64, _I64, _INT]),

@@ -29,7 +29,7 @@ constexpr int kRotRows = 16;   // rows per workgroup of the plain rotation kerne
 // rotation::rotate.  A workgroup of 4 waves takes 16 rows x 128 channels (for
 // group 64 the chunk holds two groups).  The 64 pairs' indices (masked to the
 // group, so a bad index can never address outside the tile) and cos/sin of
-// every layer are derived once per workgroup into LDS -- each sincosf serves
+// every layer are derived once per workgroup into LDS -- each sincos serves
 // 16 rows.  Wave w owns rows 4w .. 4w+3 as a channel-major LDS tile (one
 // float4 = the wave's 4 rows of a channel), so lane l applies a layer to its
 // pair with two 16-byte reads and two 16-byte writes.
@@ -78,7 +78,13 @@ __global__ __launch_bounds__(kRotWaves * 64) void rotate_kernel(const void* __re
       const int i = base + (idx[o] & (G - 1));
       const int j = base + (idx[o + 1] & (G - 1));
       const float th = pq_load_as_f32<DT>(theta, static_cast<int64_t>(r) * (h >> 1) + P);
-      sincosf(th, &sn, &c);
+      // cos and sin of the stored angle in float64, rounded once to float32:
+      // the values the host derives for the fused kernels' operands, so this
+      // kernel and those agree bit for bit
+      double sd, cd;
+      sincos(static_cast<double>(th), &sd, &cd);
+      c = static_cast<float>(cd);
+      sn = static_cast<float>(sd);
       ij = static_cast<uint32_t>(i) | (static_cast<uint32_t>(j) << 8);
     }
     s_cs[r][p] = make_float2(c, sn);
@@ -231,12 +237,21 @@ constexpr int kRQWaves = 8;
 // rotates the normalized values; ADD rotates x + res; SWIGLU rotates
 // silu(x) * up.  Member 0's blocks also write h / the residual sum s when
 // asked.
-template <int DT, int KP, bool MAT16, int RB, bool NORM>
+//
+// OUT selects what the block writes: kRqInt8 the int8 codes and token
+// scales (and the fp16 rows when asked); kRqRows the rotated rows in x's
+// dtype (the rotation::rotate result); kRqMxfp4 their OCP MXFP4 codes and
+// E8M0 scales (mb.out / mb.xrot, the rotation::rotate_and_quant_mxfp4
+// result).  The last two take no prologue, no fp16 rounding and no flags.
+constexpr int kRqInt8 = 0, kRqRows = 1, kRqMxfp4 = 2;
+
+template <int DT, int KP, bool MAT16, int RB, bool NORM, int OUT = kRqInt8>
 __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void* __restrict__ x,
                                                                        const pq::RotGroup grp, int64_t row_begin,
                                                                        int h, int krot, unsigned flags,
                                                                        const pq::NormArgs nm) {
   static_assert(RB <= kRQWaves, "one wave per row for the norm factors");
+  static_assert(OUT == kRqInt8 || (!MAT16 && !NORM), "plain and MXFP4 outputs come from the float32 rows");
   const pq::RotMember& mb = grp.mem[blockIdx.y];
   const uint32_t* __restrict__ rot_idx = mb.rot_idx;
   const float* __restrict__ rot_cs = mb.rot_cs;
@@ -384,6 +399,76 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
     sb = sbn;
     wa = wan;
     wb = wbn;
+  }
+
+  if constexpr (OUT == kRqRows) {
+    // the rotated rows in x's dtype, 8 elements (16 or 32 bytes) per thread per step
+    __syncthreads();
+    const int per_row = h >> 3;
+    for (int e = t; e < RB * per_row; e += kRQWaves * 64) {
+      const int r = e / per_row;
+      const int c8 = (e - r * per_row) * 8;
+      const float* src = reinterpret_cast<const float*>(rowbuf) + r * h + c8;
+      const float4 a = *reinterpret_cast<const float4*>(src);
+      const float4 b = *reinterpret_cast<const float4*>(src + 4);
+      const int64_t o = (row0 + r) * h + c8;
+      if constexpr (DT == PQ_F32) {
+        float* dst = static_cast<float*>(mb.out) + o;
+        *reinterpret_cast<float4*>(dst) = a;
+        *reinterpret_cast<float4*>(dst + 4) = b;
+      } else {
+        const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        uint32_t wd[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t lo = DT == PQ_F16 ? pq_f32_to_f16(f[2 * q]) : pq_f32_to_bf16(f[2 * q]);
+          const uint32_t hi = DT == PQ_F16 ? pq_f32_to_f16(f[2 * q + 1]) : pq_f32_to_bf16(f[2 * q + 1]);
+          wd[q] = lo | (hi << 16);
+        }
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(mb.out) + o) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+      }
+    }
+    return;
+  } else if constexpr (OUT == kRqMxfp4) {
+    // 32-channel blocks: 4 consecutive threads of 8 channels each exchange their absmax
+    __syncthreads();
+    const int per_row = h >> 3;
+    uint8_t* __restrict__ codes = static_cast<uint8_t*>(mb.out);
+    uint8_t* __restrict__ mxs = static_cast<uint8_t*>(mb.xrot);
+    for (int e0 = 0; e0 < RB * per_row; e0 += kRQWaves * 64) {   // uniform trip count: the shuffles see every lane
+      const int e = e0 + t;
+      const bool live = e < RB * per_row;
+      const int ee = live ? e : 0;
+      const int r = ee / per_row;
+      const int c8 = (ee - r * per_row) * 8;
+      const float* src = reinterpret_cast<const float*>(rowbuf) + r * h + c8;
+      const float4 a = *reinterpret_cast<const float4*>(src);
+      const float4 b = *reinterpret_cast<const float4*>(src + 4);
+      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      float am = 0.0f;
+      bool nan = false;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        am = fmaxf(am, fabsf(v[q]));
+        nan = nan || (v[q] != v[q]);
+      }
+      am = fmaxf(am, __shfl_xor(am, 1));
+      am = fmaxf(am, __shfl_xor(am, 2));
+      int nn = nan ? 1 : 0;
+      nn |= __shfl_xor(nn, 1);
+      nn |= __shfl_xor(nn, 2);
+      const int ex = pqd::mx_shared_exp(am);
+      const float inv = pqd::mx_inv_scale(ex);
+      uint32_t wd = 0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) wd |= pqd::mx_e2m1(v[q] * inv) << (4 * q);
+      if (live) {
+        const int64_t row = row0 + r;
+        *reinterpret_cast<uint32_t*>(codes + row * (h >> 1) + (c8 >> 1)) = wd;
+        if ((c8 & 31) == 0) mxs[row * (h >> 5) + (c8 >> 5)] = nn ? 0xFFu : static_cast<uint8_t>(ex + 127);
+      }
+    }
+    return;
   }
 
 #pragma unroll
@@ -560,29 +645,38 @@ inline int rq_rows_per_block(int64_t rows, int h, bool mat16) {
   return rb;
 }
 
-template <int DT, int KP, bool MAT16, int RB, bool NORM>
+template <int DT, int KP, bool MAT16, int RB, bool NORM, int OUT = kRqInt8>
 void launch_rq_rb(const void* x, const pq::RotGroup& grp, int64_t row_begin, int64_t nblocks, int h, int krot,
                   unsigned flags, const pq::NormArgs& nm, hipStream_t stream) {
   if (nblocks <= 0) return;
   const size_t lds = static_cast<size_t>(RB) * h * (MAT16 ? 2 : 4);
   const dim3 grid(static_cast<unsigned>(nblocks), static_cast<unsigned>(grp.count));
-  rotate_quant_kernel<DT, KP, MAT16, RB, NORM><<<grid, kRQWaves * 64, lds, stream>>>(x, grp, row_begin, h, krot,
-                                                                                     flags, nm);
+  rotate_quant_kernel<DT, KP, MAT16, RB, NORM, OUT><<<grid, kRQWaves * 64, lds, stream>>>(x, grp, row_begin, h,
+                                                                                          krot, flags, nm);
 }
 
-template <int DT, int KP, bool MAT16, bool NORM>
+template <int DT, int KP, bool MAT16, bool NORM, int OUT = kRqInt8>
 void launch_rq(const void* x, const pq::RotGroup& grp, int64_t rows, int h, int krot, unsigned flags,
                const pq::NormArgs& nm, hipStream_t stream) {
   const int rb = rq_rows_per_block(rows, h, MAT16);
   const int64_t full = rows / rb;
   switch (rb) {
-    case 8: launch_rq_rb<DT, KP, MAT16, 8, NORM>(x, grp, 0, full, h, krot, flags, nm, stream); break;
-    case 4: launch_rq_rb<DT, KP, MAT16, 4, NORM>(x, grp, 0, full, h, krot, flags, nm, stream); break;
-    case 2: launch_rq_rb<DT, KP, MAT16, 2, NORM>(x, grp, 0, full, h, krot, flags, nm, stream); break;
+    case 8: launch_rq_rb<DT, KP, MAT16, 8, NORM, OUT>(x, grp, 0, full, h, krot, flags, nm, stream); break;
+    case 4: launch_rq_rb<DT, KP, MAT16, 4, NORM, OUT>(x, grp, 0, full, h, krot, flags, nm, stream); break;
+    case 2: launch_rq_rb<DT, KP, MAT16, 2, NORM, OUT>(x, grp, 0, full, h, krot, flags, nm, stream); break;
     default: break;
   }
   const int64_t done = rb > 1 ? full * rb : 0;   // the remaining rows, one block each
-  launch_rq_rb<DT, KP, MAT16, 1, NORM>(x, grp, done, rows - done, h, krot, flags, nm, stream);
+  launch_rq_rb<DT, KP, MAT16, 1, NORM, OUT>(x, grp, done, rows - done, h, krot, flags, nm, stream);
+}
+
+// The register-chain rotation of whole rows with a plain (OUT = kRqRows) or
+// MXFP4 (kRqMxfp4) output, on packed operands.
+template <int DT, int OUT>
+void launch_rotate_rows_dt(const void* x, const pq::RotGroup& grp, int64_t rows, int h, int krot,
+                           hipStream_t stream) {
+  if (krot <= 8) launch_rq<DT, 8, false, false, OUT>(x, grp, rows, h, krot, 0u, pq::NormArgs{}, stream);
+  else launch_rq<DT, 16, false, false, OUT>(x, grp, rows, h, krot, 0u, pq::NormArgs{}, stream);
 }
 
 template <int DT, bool NORM>
@@ -694,6 +788,50 @@ extern "C" int pq_rotate_mxfp4(const void* x, uint8_t* q_out, uint8_t* scale_out
       break;
   }
   return pq::launch_status("pq_rotate_mxfp4 launch");
+}
+
+// rotation::rotate / rotation::rotate_and_quant_mxfp4 on packed operands
+// (pq_rotation_pack): the register-chain rotation of the fused kernels,
+// whole rows per workgroup.  Its cos/sin are the packed float32 values the
+// host derives in float64, as pq_rotate's kernel derives them on the device,
+// and its layer arithmetic is the same, so the results equal pq_rotate's /
+// pq_rotate_mxfp4's for the pairs and angles the operands were packed from.
+extern "C" int pq_rotate_rows(const void* x, int x_dtype, const uint32_t* rot_idx, const float* rot_cs,
+                              const float* scales, void* out, uint8_t* mx_scales, int64_t rows, int64_t h, int krot,
+                              int out_mode, void* stream) {
+  PQ_REQUIRE(rows >= 0 && rows <= 0x7fffffffLL && h > 0 && h % 128 == 0 && h <= 16384, PQ_ERR_ARG,
+             "pq_rotate_rows: need h %% 128 == 0 and 0 < h <= 16384 (h=%lld, rows=%lld)", (long long)h,
+             (long long)rows);
+  PQ_REQUIRE(krot >= 1 && krot <= 16, PQ_ERR_UNSUPPORTED, "pq_rotate_rows: krot=%d not in 1..16", krot);
+  PQ_REQUIRE(x_dtype == PQ_F32 || x_dtype == PQ_F16 || x_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED,
+             "pq_rotate_rows: x dtype code %d", x_dtype);
+  PQ_REQUIRE(out_mode == PQ_ROWS_SAME || out_mode == PQ_ROWS_MXFP4, PQ_ERR_ARG, "pq_rotate_rows: out_mode %d",
+             out_mode);
+  if (rows == 0) return PQ_OK;
+  PQ_REQUIRE(x && rot_idx && rot_cs && out && (out_mode != PQ_ROWS_MXFP4 || mx_scales), PQ_ERR_ARG,
+             "pq_rotate_rows: null pointer");
+  PQ_REQUIRE(pq::aligned_to(x, 16) && pq::aligned_to(rot_idx, 16) && pq::aligned_to(rot_cs, 16) &&
+                 pq::aligned_to(out, 16),
+             PQ_ERR_ARG, "pq_rotate_rows: x, rot_idx, rot_cs and out must be 16-byte aligned");
+  pq::RotGroup grp{};
+  grp.count = 1;
+  grp.mem[0] = {rot_idx, rot_cs, scales, out, nullptr, mx_scales};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int hh = static_cast<int>(h);
+  if (out_mode == PQ_ROWS_SAME) {
+    switch (x_dtype) {
+      case PQ_F32: launch_rotate_rows_dt<PQ_F32, kRqRows>(x, grp, rows, hh, krot, s); break;
+      case PQ_F16: launch_rotate_rows_dt<PQ_F16, kRqRows>(x, grp, rows, hh, krot, s); break;
+      default: launch_rotate_rows_dt<PQ_BF16, kRqRows>(x, grp, rows, hh, krot, s); break;
+    }
+  } else {
+    switch (x_dtype) {
+      case PQ_F32: launch_rotate_rows_dt<PQ_F32, kRqMxfp4>(x, grp, rows, hh, krot, s); break;
+      case PQ_F16: launch_rotate_rows_dt<PQ_F16, kRqMxfp4>(x, grp, rows, hh, krot, s); break;
+      default: launch_rotate_rows_dt<PQ_BF16, kRqMxfp4>(x, grp, rows, hh, krot, s); break;
+    }
+  }
+  return pq::launch_status("pq_rotate_rows launch");
 }
 
 extern "C" int pq_rotate_quant_i8(const void* x, int x_dtype, const uint32_t* rot_idx, const float* rot_cs,

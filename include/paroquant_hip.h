@@ -96,6 +96,23 @@ int pq_rotate(const void* x, void* y, const int16_t* idx_ij, const void* theta,
 int pq_rotate_mxfp4(const void* x, uint8_t* q_out, uint8_t* scale_out, const int16_t* idx_ij, const void* theta,
                     const void* scales, int64_t rows, int64_t h, int krot, int group_size, int dtype, void* stream);
 
+/* pq_rotate (out_mode PQ_ROWS_SAME: out [rows, h] in x_dtype) or
+ * pq_rotate_mxfp4 (PQ_ROWS_MXFP4: out = codes [rows, h/2], mx_scales
+ * [rows, h/32]) on packed rotation operands (pq_rotation_pack, group 128,
+ * cos/sin of each angle evaluated in float64 and rounded to float32) and
+ * float32 channel scales (or NULL): the register-chain kernel of the fused
+ * linear, whole rows per workgroup.  The results equal pq_rotate's /
+ * pq_rotate_mxfp4's on the pairs and angles the operands were packed from.
+ * h % 128 == 0, h <= 16384, krot in 1..16; x, out, rot_idx, rot_cs 16-byte
+ * aligned.  Reference: rotation::rotate (rotation.cu:456-493) and the fused
+ * rotate_and_quant (rotation.cu:62-111), in the MX format for the latter. */
+int pq_rotate_rows(const void* x, int x_dtype, const uint32_t* rot_idx, const float* rot_cs, const float* scales,
+                   void* out, uint8_t* mx_scales, int64_t rows, int64_t h, int krot, int out_mode, void* stream);
+
+/* out_mode of pq_rotate_rows */
+#define PQ_ROWS_SAME 0   /* rotated rows in x's dtype (rotation::rotate) */
+#define PQ_ROWS_MXFP4 1  /* OCP MXFP4 codes + E8M0 scales (rotation::rotate_and_quant_mxfp4) */
+
 /* Packs rotation parameters (host memory, host code; no GPU involved) into
  * the operand layout of the fused kernels, G = h/128, KP = 8 for krot <= 8,
  * else 16:
