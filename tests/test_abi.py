@@ -241,3 +241,19 @@ def test_split_path_rule():
     assert lib.pq_w4a8_linear_split_path(4, 4096) == 0
     assert lib.pq_w4a8_linear_split_path(2, 12288) == 0
     assert lib.pq_w4a8_linear_split_path(0, 4096) == 0
+
+
+def test_rotate_rows_argument_checks():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+
+    def call(x=p, dt=2, out=p, mxs=None, rows=4, h=256, krot=8, mode=0):
+        return lib.pq_rotate_rows(x, dt, p, p, None, out, mxs, rows, h, krot, mode, None)
+
+    assert call(h=192) == 1
+    assert call(krot=17) == 2
+    assert call(dt=5) == 2
+    assert call(mode=3) == 1 and "out_mode" in _err(lib)
+    assert call(mode=1) == 1 and "null" in _err(lib)              # MXFP4 needs the scale buffer
+    assert call(x=ctypes.c_void_p(264)) == 1 and "aligned" in _err(lib)
+    assert call(rows=0) == 0
