@@ -31,7 +31,9 @@
 //   gemm_prefill M > 16: 192x256 (or 128x128) output tiles, 8 (or 4) waves
 //                side by side along n, operands copied from global memory
 //                straight into a 3-stage LDS ring, v_mfma_i32_32x32x32_i8
-//                tiles, the output staged through LDS for 16-byte stores.
+//                tiles, the output staged through LDS for 16-byte stores;
+//                the 192x256 tiles run their 32-row tiles in pairs, scaling
+//                the previous pair's partials under the current pair's MFMAs.
 #include <type_traits>
 
 #include "pq_device.h"
@@ -336,7 +338,7 @@ __device__ __forceinline__ void wait_groups(int ahead) {
   }
 }
 
-template <int BM, int BN, int WM, int WN, bool PARTIALS, int ST = kPfStages>
+template <int BM, int BN, int WM, int WN, bool PARTIALS, int ST = kPfStages, bool TP = false>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
     const pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* __restrict__ partials, int M, int K) {
   constexpr int NW = WM * WN;
@@ -491,6 +493,88 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
     }
   };
 
+  // Tile-pair form of compute (TP): the wave runs its tiles two at a time --
+  // the four k-steps of tiles 2p and 2p+1, two independent MFMA chains --
+  // and scales the previous pair's partials in between, one MFMA then eight
+  // VALU (four converts, four fmas), enforced with sched_group_barrier.
+  // Only two pairs of partials are live; the group's B fragments are
+  // unpacked once up front.
+  auto compute_tp = [&](int stage, int ig) {
+    static_assert(TM % 2 == 0, "tiles in pairs");
+    const uint8_t* As = smem + stage * STAGE;
+    const uint8_t* Bs = As + A_BYTES;
+    const uint32_t* Ms = reinterpret_cast<const uint32_t*>(Bs + B_BYTES);
+    float sc[TN];
+    v4i b[4][TN];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const uint32_t meta = Ms[bcol[tn]];
+      const uint32_t zb = meta_zero_bias(meta);
+      sc[tn] = meta_scale(meta);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint2 w = *reinterpret_cast<const uint2*>(Bs + (bcol[tn] >> 4) * kPfBStride +
+                                                        ((2 * hj + (i >> 1)) * 16 + (bcol[tn] & 15)) * 16 + (i & 1) * 8);
+        b[i][tn] = unpack16(w.x, w.y, zb);
+      }
+    }
+    // A fragments of the current pair; each k-step's are reloaded for the
+    // next pair right after their MFMAs issue (six MFMAs hide the latency)
+    v4i a[2][4];
+    auto load_frag = [&](int tile, int i) {
+      const int r = arow[tile];
+      return *reinterpret_cast<const v4i*>(As + r * 128 + (((hj * 4 + i) ^ pf_swz(r)) << 4));
+    };
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[t2][i] = load_frag(t2, i);
+    v16i T[2][2][TN];
+#pragma unroll
+    for (int p = 0; p < TM / 2; ++p) {
+      const int cb = p & 1;
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) T[cb][t2][tn] = v16i{};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+          for (int tn = 0; tn < TN; ++tn) {
+            T[cb][t2][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[t2][i], b[i][tn], T[cb][t2][tn], 0, 0, 0);
+            if (p > 0) {
+#pragma unroll
+              for (int v = 4 * i; v < 4 * i + 4; ++v)
+                acc[2 * p - 2 + t2][tn][v] =
+                    fmaf(static_cast<float>(T[cb ^ 1][t2][tn][v]), sc[tn], acc[2 * p - 2 + t2][tn][v]);
+            }
+          }
+        if (p + 1 < TM / 2) {
+#pragma unroll
+          for (int t2 = 0; t2 < 2; ++t2) a[t2][i] = load_frag(2 * p + 2 + t2, i);
+        }
+      }
+      if (p > 0) {
+#pragma unroll
+        for (int q = 0; q < 8 * TN; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);   // eight VALU
+        }
+      }
+      if (p == 0 && ig < G) issue(ig, ig % ST);
+    }
+    constexpr int LP = (TM / 2 - 1) & 1;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          acc[TM - 2 + t2][tn][v] = fmaf(static_cast<float>(T[LP][t2][tn][v]), sc[tn], acc[TM - 2 + t2][tn][v]);
+  };
+
   // Stage g % ST holds group g; the copies run ST-1 groups ahead.  Before
   // computing g, each wave waits for its own loads of g (those of the later
   // groups may stay in flight), then a barrier makes everybody's loads of g
@@ -509,7 +593,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
   for (int g = 0; g < G; ++g) {
     wait_groups<LOADS, ST - 2>(min(G - 1 - g, ST - 2));
     __builtin_amdgcn_s_barrier();
-    compute(g % ST, g, g + ST - 1);
+    if constexpr (TP && !PARTIALS) compute_tp(g % ST, g + ST - 1);
+    else compute(g % ST, g, g + ST - 1);
   }
   if constexpr (PARTIALS) return;
 
@@ -567,14 +652,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
   else emit(std::integral_constant<int, PQ_BF16>{});
 }
 
-template <int BM, int BN, int WM, int WN, bool PARTIALS, int ST = kPfStages>
+template <int BM, int BN, int WM, int WN, bool PARTIALS, int ST = kPfStages, bool TP = false>
 void launch_prefill_t(pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* partials, int M, int K,
                       hipStream_t stream) {
   constexpr int STAGE = BM * 128 + (BN / 16) * kPfBStride + BN * 4;
   grp.first[0] = 0;
   for (int i = 0; i < grp.count; ++i) grp.first[i + 1] = grp.first[i] + (grp.mem[i].n + BN - 1) / BN;
   const unsigned grid = static_cast<unsigned>(((M + BM - 1) / BM) * grp.first[grp.count]);
-  gemm_prefill<BM, BN, WM, WN, PARTIALS, ST><<<grid, WM * WN * 64, ST * STAGE + BM * 4, stream>>>(
+  gemm_prefill<BM, BN, WM, WN, PARTIALS, ST, TP><<<grid, WM * WN * 64, ST * STAGE + BM * 4, stream>>>(
       grp, bias_dtype, y_dtype, partials, M, K);
 }
 
@@ -589,7 +674,7 @@ void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32
   int64_t bn128 = 0;
   for (int i = 0; i < grp.count; ++i) bn128 += (grp.mem[i].n + 127) / 128;
   if (static_cast<int64_t>((M + 191) / 192) * bn_tiles >= 256)
-    launch_prefill_t<192, 256, 1, 8, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
+    launch_prefill_t<192, 256, 1, 8, PARTIALS, kPfStages, !PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
   else if (static_cast<int64_t>((M + 127) / 128) * bn128 >= 256)
     launch_prefill_t<128, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
   else   // narrow outputs (k/v): twice the workgroups of 128-row tiles

@@ -23,6 +23,10 @@ ragged packed batch (8 requests of U{1..512} tokens), the roofline of the
 dominant kernel (the decode GEMM at M = 1) and the CPU oracle timed on the
 host.
 
+Every timed region except the headline decode one follows at least
+--warm-seconds of untimed replays (the shader clock settles under sustained
+load); the headline keeps exactly --warmup untimed steps.
+
 Data are synthetic (seeded), weights random-init; one process, one GPU.
 """
 
@@ -110,6 +114,8 @@ def main() -> int:
     ap.add_argument("--no-w4a16", action="store_true", help="skip the W4A16 (WQLinear) figures")
     ap.add_argument("--no-mxfp4", action="store_true", help="skip the fused rotation + MXFP4 figures")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--warm-seconds", type=float, default=0.3,
+                    help="minimum wall time of untimed replays before each timed region")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first copy 256 MiB device to device 3 times: the known-size kernel that calibrates "
                          "the FETCH_SIZE / WRITE_SIZE counter passes")
@@ -187,9 +193,17 @@ def main() -> int:
             outs = [run_layer(li, X, grouped) for li, X in enumerate(xs)]
         return gr, outs, xs
 
-    def time_graphs(graphs, steps, warmup):
-        for i in range(warmup):
+    def time_graphs(graphs, steps, warmup, warm_s=None):
+        # warm up for at least warm_s (default --warm-seconds) of wall time as well as `warmup`
+        # replays: the GPU's clock takes a few hundred ms of sustained load to settle, and a
+        # short compute-bound run timed before that reads several percent slow
+        warm_s = args.warm_seconds if warm_s is None else warm_s
+        t0, i = time.perf_counter(), 0
+        while i < warmup or time.perf_counter() - t0 < warm_s:
             graphs[i % len(graphs)].replay()
+            i += 1
+            if i % len(graphs) == 0:
+                torch.cuda.synchronize()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -212,7 +226,7 @@ def main() -> int:
         for grouped, table in ((True, decode), (False, decode_sep)):
             gr, _, _ = capture_layers(M, 5000 + M, grouped)
             # K steps = K / P replays of the pool graph (steps is a multiple of P)
-            ms = time_graphs([gr], args.steps // P, -(-args.warmup // P)) / P
+            ms = time_graphs([gr], args.steps // P, -(-args.warmup // P), warm_s=0.0) / P
             table[M] = (ms, b / (ms * 1e-3) / 1e9)
             log(f"decode M={M} {'grouped ' if grouped else 'separate'}: {ms * 1e3:.1f} us/layer, "
                 f"{table[M][1]:.0f} GB/s")
