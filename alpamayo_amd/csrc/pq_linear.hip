@@ -2,7 +2,8 @@
 // int4 x int8 GEMM) behind one entry point, pq_w4a8_linear.  Two kernels
 // either way, chosen by the number of tokens m:
 //
-//   split (decode: m * k <= 12288, e.g. one token): the rotation runs with
+//   split (decode: m * k <= 12288, e.g. one token, or up to 4 tokens when
+//     k >= 8192): the rotation runs with
 //     one wave per 128-channel group (K/128 waves spread over the chip, each
 //     rotation parameter read once) and writes the rotated rows plus each
 //     row's absmax per group; the decode GEMM derives the token scales and
@@ -27,9 +28,14 @@ namespace {
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Measured on the Qwen3-8B shapes: the split path wins while each GEMM
-// workgroup can request all of A in its prologue at once (m * k <= 12288);
-// beyond that the row kernel's whole-row quantization is faster.
-bool use_split(int64_t m, int64_t k) { return m * k <= 12288 && pq::gemm_rotated_supported(m, k); }
+// workgroup can request all of A in its prologue at once (m * k <= 12288),
+// and for long rows up to 4 tokens: the row kernel runs each row on one CU,
+// whose VALU needs about 12 us for the 96 groups of a 12288-channel row
+// (down at m = 2: 12.8 us split against 20.0 us rows; m = 4: 16.6 / 20.8).
+// Beyond that the row kernel's whole-row quantization is faster.
+bool use_split(int64_t m, int64_t k) {
+  return (m * k <= 12288 || (k >= 8192 && m <= 4)) && pq::gemm_rotated_supported(m, k);
+}
 
 size_t split_xr_bytes(int64_t m, int64_t k) { return align_up(static_cast<size_t>(m) * k * sizeof(float), 256); }
 

@@ -182,7 +182,8 @@ int pq_w4a8_prepack(const int32_t* awq_qweight, const uint16_t* awq_scales,
                     int64_t n, int group_size, void* stream);
 
 /* Bytes of scratch pq_w4a8_linear needs between its two kernels: for decode
- * sizes (m*k <= 12288) the rotated rows and per-group maxima, m*k*4 rounded
+ * sizes (m*k <= 12288, or m <= 4 when k >= 8192; pq_w4a8_linear_split_path)
+ * the rotated rows and per-group maxima, m*k*4 rounded
  * up to 256 plus 4*m*(k/128) bytes; otherwise the int8 activations and their
  * scales, m*k rounded up to 256 plus 4*m bytes.  The scratch is written
  * before it is read; its content does not matter. */

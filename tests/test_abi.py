@@ -117,15 +117,17 @@ def test_workspace_size_rules():
     for m in (1, 4, 16, 3072):
         for n, k in ((1024, 4096), (4096, 4096), (12288, 4096), (4096, 12288)):
             assert lib.pq_w4a8_workspace_size(m, n, k, 128) == 0        # no inter-workgroup exchange
-    # decode (m * k <= 12288): rotated rows (fp32 bound) + per-group absmax
+    # decode (m * k <= 12288, or m <= 4 for k >= 8192): rotated rows (fp32 bound) + per-group absmax
     def split(m, k):
         return (m * k * 4 + 255) // 256 * 256 + m * (k // 128) * 4
     assert lib.pq_w4a8_linear_workspace_size(1, 4096, 4096, 8) == split(1, 4096)
     assert lib.pq_w4a8_linear_workspace_size(1, 4096, 12288, 16) == split(1, 12288)
     assert lib.pq_w4a8_linear_workspace_size(3, 4096, 4096, 8) == split(3, 4096)
+    assert lib.pq_w4a8_linear_workspace_size(4, 4096, 12288, 8) == split(4, 12288)
+    assert lib.pq_w4a8_linear_workspace_size(5, 4096, 12288, 8) == (5 * 12288 + 255) // 256 * 256 + 5 * 4
     # otherwise the row path holds xq and xscale
     assert lib.pq_w4a8_linear_workspace_size(4, 4096, 4096, 8) == 4 * 4096 + 16
-    assert lib.pq_w4a8_linear_workspace_size(2, 4096, 12288, 8) == 2 * 12288 + 8
+    assert lib.pq_w4a8_linear_workspace_size(6, 4096, 12288, 8) == 6 * 12288 + 24
     assert lib.pq_w4a8_linear_workspace_size(17, 4096, 4096, 8) == 17 * 4096 + 68
     assert lib.pq_w4a8_linear_workspace_size(3, 64, 100, 8) == 0       # invalid shape -> 0
 
@@ -239,7 +241,14 @@ def test_split_path_rule():
     assert lib.pq_w4a8_linear_split_path(3, 4096) == 1
     assert lib.pq_w4a8_linear_split_path(1, 12288) == 1
     assert lib.pq_w4a8_linear_split_path(4, 4096) == 0
-    assert lib.pq_w4a8_linear_split_path(2, 12288) == 0
+    # long rows: split up to 4 tokens (the row kernel runs a row on one CU)
+    assert lib.pq_w4a8_linear_split_path(2, 12288) == 1
+    assert lib.pq_w4a8_linear_split_path(4, 12288) == 1
+    assert lib.pq_w4a8_linear_split_path(4, 8192) == 1
+    assert lib.pq_w4a8_linear_split_path(4, 16384) == 1
+    assert lib.pq_w4a8_linear_split_path(5, 12288) == 0
+    assert lib.pq_w4a8_linear_split_path(2, 4096) == 1
+    assert lib.pq_w4a8_linear_split_path(4, 6144) == 0
     assert lib.pq_w4a8_linear_split_path(0, 4096) == 0
 
 

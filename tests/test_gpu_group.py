@@ -52,6 +52,7 @@ CASES = [
     (1, 4096, (12288, 12288)),
     (3, 4096, (48, 1552, 16, 4096)),
     (1, 12288, (4096,)),
+    (4, 12288, (4096, 1024)),
     (2, 2048, (1024, 64)),
     (5, 4096, (4096, 1024, 1024)),
     (17, 1024, (48, 1552)),

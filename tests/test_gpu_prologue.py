@@ -21,9 +21,11 @@ from tests.test_gpu_group import _members, _oracle
 pytestmark = pytest.mark.gpu
 
 CASES = [
-    # (M, K, member Ns): split rotation (M*K <= 12288), the row rotate+quant path, ragged row counts
+    # (M, K, member Ns): split rotation (M*K <= 12288, or M <= 4 for K >= 8192), the row
+    # rotate+quant path, ragged row counts
     (1, 4096, (4096, 1024, 1024)),
     (1, 12288, (4096,)),
+    (3, 12288, (4096,)),
     (3, 4096, (1024, 1024)),
     (16, 12288, (4096,)),
     (300, 4096, (4096, 1024)),

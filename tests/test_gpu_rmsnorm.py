@@ -29,10 +29,12 @@ def _bits_close(got_np, ref_np, min_equal=0.999):
 
 
 CASES = [
-    # (M, K, member Ns): split rotation (M*K <= 12288), the row rotate+quant path, ragged row counts
+    # (M, K, member Ns): split rotation (M*K <= 12288, or M <= 4 for K >= 8192), the row
+    # rotate+quant path, ragged row counts
     (1, 4096, (4096, 1024, 1024)),
     (3, 4096, (1024, 1024)),
     (1, 12288, (4096,)),
+    (4, 8192, (1024,)),
     (2, 2048, (1024, 64)),
     (16, 4096, (1024, 512)),
     (300, 4096, (4096, 1024, 1024)),
