@@ -49,6 +49,19 @@ struct RotGroup {
   int count;
 };
 
+// Per-token int8 quantization of a split rotation's output (launch_quant_split):
+// xr [m][k] (fp16 or fp32) and gmax [m][k/128] in, xq [m][k] and xscale [m] out.
+struct QuantMember {
+  const void* xr;
+  const float* gmax;
+  int8_t* xq;
+  float* xscale;
+};
+struct QuantGroup {
+  QuantMember mem[kMaxGroup];
+  int count;
+};
+
 // Rows per launch of the split rotation (and rows the rotated GEMM accepts).
 constexpr int kSplitMaxRows = 16;
 
@@ -76,8 +89,16 @@ struct NormArgs {
 // for every member of the group: xr [m][h] rotated values (fp16 when flags
 // has PQ_RQ_MATERIALIZE_FP16, else fp32) and gmax [m][h/128] the absmax of
 // each row's group.
+// rows_per_wave > 0 spreads the m rows over ceil(m / rows_per_wave) waves
+// per group (each wave then holds at most rows_per_wave rows); 0 keeps all
+// m <= kSplitMaxRows rows in one wave.
 PQ_HIDDEN void launch_rotate_split(const void* x, int x_dtype, const RotGroup& grp, int m, int h, int krot,
-                                   unsigned flags, hipStream_t stream, const NormArgs* norm = nullptr);
+                                   unsigned flags, hipStream_t stream, const NormArgs* norm = nullptr,
+                                   int rows_per_wave = 0);
+// Token scales (absmax / 127 over each row's group maxima) and int8 codes of
+// a split rotation's rows; the same values the rotated decode GEMM derives in
+// its prologue.  mat16: xr holds fp16 (else fp32).
+PQ_HIDDEN void launch_quant_split(const QuantGroup& grp, int m, int h, bool mat16, hipStream_t stream);
 // Rotation + per-token int8 quant of whole rows for every member of the group.
 PQ_HIDDEN void launch_rotate_quant_group(const void* x, int x_dtype, const RotGroup& grp, int64_t rows, int h,
                                          int krot, unsigned flags, hipStream_t stream,

@@ -9,6 +9,9 @@
 //     row's absmax per group; the decode GEMM derives the token scales and
 //     quantizes A into LDS in its prologue, while its first weight blocks
 //     are already in flight.
+//   split3 (k >= 8192 beyond that, up to 16 tokens): the split rotation
+//     with the rows spread over waves, a token-scale + int8 kernel, then
+//     the decode GEMM on int8 A (three launches).
 //   rows (otherwise): pq_rotate_quant_i8 (rotation + absmax + int8 quant of
 //     whole rows per workgroup) into the caller's workspace, then
 //     pq_w4a8_gemm.
@@ -37,16 +40,44 @@ bool use_split(int64_t m, int64_t k) {
   return (m * k <= 12288 || (k >= 8192 && m <= 4)) && pq::gemm_rotated_supported(m, k);
 }
 
-size_t split_xr_bytes(int64_t m, int64_t k) { return align_up(static_cast<size_t>(m) * k * sizeof(float), 256); }
+// Long rows past the split pair, up to 16 tokens: the split rotation with
+// its rows spread over waves (kSplitRowsPerWave rows each), a small kernel
+// for the token scales and int8 codes, then the decode GEMM on int8 A.  The
+// row kernel would run each row on one CU (down, k = 12288, at m = 6: 17.8 us
+// against 22.2 us; m = 16: 20.0 / 24.0).  At k = 4096 the third launch costs
+// more than it saves (q at m = 16: 13.3 us against 11.7 us rows).
+constexpr int kSplitRowsPerWave = 4;
+bool use_split3(int64_t m, int64_t k) {
+  return !use_split(m, k) && m >= 1 && m <= pq::kSplitMaxRows && k >= 8192 && k <= 16384;
+}
 
-// Workspace of a group of `count` linears: the members' per-row data back
-// to back -- decode: count x align256(4*m*k) of rotated rows, then count x
-// 4*m*(k/128) of group maxima; rows path: count x align256(m*k) of int8
-// activations, then count x 4*m of token scales.
+enum class Path { kSplit, kSplit3, kRows };
+Path choose_path(int64_t m, int64_t k) {
+  return use_split(m, k) ? Path::kSplit : use_split3(m, k) ? Path::kSplit3 : Path::kRows;
+}
+
+size_t split_xr_bytes(int64_t m, int64_t k) { return align_up(static_cast<size_t>(m) * k * sizeof(float), 256); }
+size_t xq_bytes(int64_t m, int64_t k) { return align_up(static_cast<size_t>(m) * k, 256); }
+
+// Per member: the bytes of its row data (a) and of its per-row scalars (s).
+// The workspace of a group of `count` linears holds count a-blocks, then
+// count s-blocks.  split: a = rotated rows (fp32 bound), s = group maxima
+// [m][k/128]; split3: a = rotated rows then int8 codes, s = group maxima then
+// token scales [m]; rows: a = int8 codes, s = token scales.
+void block_bytes(Path path, int64_t m, int64_t k, size_t* a, size_t* s) {
+  const size_t gm = static_cast<size_t>(m) * (k / 128) * sizeof(float), ts = static_cast<size_t>(m) * sizeof(float);
+  switch (path) {
+    case Path::kSplit: *a = split_xr_bytes(m, k); *s = gm; break;
+    case Path::kSplit3: *a = split_xr_bytes(m, k) + xq_bytes(m, k); *s = gm + ts; break;
+    default: *a = xq_bytes(m, k); *s = ts; break;
+  }
+}
+
 size_t group_workspace_size(int64_t m, int64_t k, int count) {
   if (m <= 0 || k <= 0 || k % 128 || count < 1 || count > pq::kMaxGroup) return 0;
-  if (use_split(m, k)) return count * (split_xr_bytes(m, k) + static_cast<size_t>(m) * (k / 128) * sizeof(float));
-  return count * (align_up(static_cast<size_t>(m) * k, 256) + static_cast<size_t>(m) * sizeof(float));
+  size_t a = 0, s = 0;
+  block_bytes(choose_path(m, k), m, k, &a, &s);
+  return count * (a + s);
 }
 
 int linear_group(const char* who, const void* x, int x_dtype, const pq_linear_member* members, int count,
@@ -96,25 +127,44 @@ int linear_group(const char* who, const void* x, int x_dtype, const pq_linear_me
   pq::RotGroup rg{};
   pq::GemmGroup gg{};
   rg.count = gg.count = count;
-  const bool split = use_split(m, k);
-  const size_t a_bytes = split ? split_xr_bytes(m, k) : align_up(static_cast<size_t>(m) * k, 256);
-  const size_t s_bytes = split ? static_cast<size_t>(m) * (k / 128) * sizeof(float) : static_cast<size_t>(m) * 4;
+  const Path path = choose_path(m, k);
+  size_t a_bytes = 0, s_bytes = 0;
+  block_bytes(path, m, k, &a_bytes, &s_bytes);
+  const bool mat16 = (flags & PQ_RQ_MATERIALIZE_FP16) != 0;
+  pq::QuantGroup qg{};
+  qg.count = count;
   for (int i = 0; i < count; ++i) {
     const pq_linear_member& mb = members[i];
-    void* a = ws + i * a_bytes;
+    char* a = ws + i * a_bytes;
     float* sc = reinterpret_cast<float*>(ws + count * a_bytes + i * s_bytes);
     rg.mem[i] = {mb.rot_idx, mb.rot_cs, mb.scales, a, sc, nullptr};
-    if (split)
+    if (path == Path::kSplit) {
       gg.mem[i] = {nullptr, nullptr, a, sc, mb.wpack, mb.wmeta, mb.bias, mb.y, static_cast<int>(mb.n)};
-    else
-      gg.mem[i] = {static_cast<const int8_t*>(a), sc, nullptr, nullptr, mb.wpack, mb.wmeta, mb.bias, mb.y,
+    } else if (path == Path::kSplit3) {
+      int8_t* xq = reinterpret_cast<int8_t*>(a + split_xr_bytes(m, k));
+      float* xs = sc + m * (k / 128);
+      qg.mem[i] = {a, sc, xq, xs};
+      gg.mem[i] = {xq, xs, nullptr, nullptr, mb.wpack, mb.wmeta, mb.bias, mb.y, static_cast<int>(mb.n)};
+    } else {
+      gg.mem[i] = {reinterpret_cast<const int8_t*>(a), sc, nullptr, nullptr, mb.wpack, mb.wmeta, mb.bias, mb.y,
                    static_cast<int>(mb.n)};
+    }
   }
-  if (split) pq::launch_rotate_split(x, x_dtype, rg, M, K, krot, flags, s, norm);
-  else pq::launch_rotate_quant_group(x, x_dtype, rg, m, K, krot, flags, s, norm);
-  int st = pq::launch_status(split ? "linear rotation launch" : "linear rotate+quant launch");
+  int st = PQ_OK;
+  if (path == Path::kRows) {
+    pq::launch_rotate_quant_group(x, x_dtype, rg, m, K, krot, flags, s, norm);
+    st = pq::launch_status("linear rotate+quant launch");
+  } else {
+    pq::launch_rotate_split(x, x_dtype, rg, M, K, krot, flags, s, norm,
+                            path == Path::kSplit3 ? kSplitRowsPerWave : 0);
+    st = pq::launch_status("linear rotation launch");
+    if (st == PQ_OK && path == Path::kSplit3) {
+      pq::launch_quant_split(qg, M, K, mat16, s);
+      st = pq::launch_status("linear quant launch");
+    }
+  }
   if (st != PQ_OK) return st;
-  const int aq = split ? ((flags & PQ_RQ_MATERIALIZE_FP16) ? 1 : 2) : 0;
+  const int aq = path == Path::kSplit ? (mat16 ? 1 : 2) : 0;
   pq::launch_gemm_group(gg, aq, bias_dtype, y_dtype, M, K, s);
   return pq::launch_status("linear GEMM launch");
 }
@@ -127,7 +177,9 @@ extern "C" size_t pq_w4a8_linear_workspace_size(int64_t m, int64_t n, int64_t k,
   return group_workspace_size(m, k, 1);
 }
 
-extern "C" int pq_w4a8_linear_split_path(int64_t m, int64_t k) { return m > 0 && use_split(m, k) ? 1 : 0; }
+extern "C" int pq_w4a8_linear_split_path(int64_t m, int64_t k) {
+  return m > 0 && choose_path(m, k) != Path::kRows ? 1 : 0;
+}
 
 extern "C" size_t pq_w4a8_linear_group_workspace_size(int64_t m, int64_t k, int count) {
   return group_workspace_size(m, k, count);

@@ -541,18 +541,72 @@ __global__ __launch_bounds__(kSplitWaves * 64) void rotate_split_kernel(const vo
   const pq::RotMember& mb = grp.mem[blockIdx.y];
   // the normalized rows and the residual sum are the same for every member: member 0 writes them
   const bool first = blockIdx.y == 0;
-  pqd::rotate_group_rows<DT, KP, MAT16, MR, NORM>(x, mb.rot_idx, mb.rot_cs, mb.scales, mb.out, mb.out_scale, M, h,
-                                                  krot, flags, g, threadIdx.x & 63, nm.res, nm.w,
-                                                  first ? nm.h_out : nullptr, first ? nm.s_out : nullptr, nm.eps,
-                                                  nm.mode);
+  // grid.z: chunks of MR rows; the row pointers move to the chunk's first row
+  const int row0 = blockIdx.z * MR;
+  const int64_t e0 = static_cast<int64_t>(row0) * h;
+  constexpr int xsz = DT == PQ_F32 ? 4 : 2;
+  auto at = [](const void* p, int64_t bytes) -> void* {
+    return p == nullptr ? nullptr : const_cast<char*>(static_cast<const char*>(p)) + bytes;
+  };
+  pqd::rotate_group_rows<DT, KP, MAT16, MR, NORM>(
+      at(x, e0 * xsz), mb.rot_idx, mb.rot_cs, mb.scales, at(mb.out, e0 * (MAT16 ? 2 : 4)),
+      mb.out_scale + static_cast<int64_t>(row0) * (h >> 7), min(MR, M - row0), h, krot, flags, g, threadIdx.x & 63,
+      at(nm.res, e0 * xsz), nm.w, first ? at(nm.h_out, e0 * xsz) : nullptr, first ? at(nm.s_out, e0 * xsz) : nullptr,
+      nm.eps, nm.mode);
+}
+
+// Per-token int8 quantization of the split rotation's rows, for token counts
+// where the GEMM should not re-derive it in every workgroup.  grid (chunks of
+// 2048 channels, rows, members); each thread quantizes 8 channels.  The token
+// absmax is the largest group maximum in the unsigned order of its bits (the
+// maxima are >= 0), as the rotated decode GEMM takes it, so both give the
+// same codes and scales.
+template <bool MAT16>
+__global__ __launch_bounds__(256) void quant_split_kernel(const pq::QuantGroup grp, int h) {
+  const pq::QuantMember& mb = grp.mem[blockIdx.z];
+  const int row = blockIdx.y;
+  const int G = h >> 7;
+  const int lane = threadIdx.x & 63;
+  const float* gm = mb.gmax + static_cast<int64_t>(row) * G;
+  uint32_t u = 0;
+  for (int i = lane; i < G; i += 64) u = max(u, __float_as_uint(gm[i]));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) u = max(u, static_cast<uint32_t>(__shfl_xor(static_cast<int>(u), o)));
+  const float am = __uint_as_float(u);
+  const int c8 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (c8 >= h) return;
+  const int64_t o = static_cast<int64_t>(row) * h + c8;
+  float f[8];
+  if constexpr (MAT16) {
+    const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(mb.xr) + o);
+    const uint32_t wds[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f[2 * q] = pq_f16_to_f32(static_cast<uint16_t>(wds[q] & 0xffffu));
+      f[2 * q + 1] = pq_f16_to_f32(static_cast<uint16_t>(wds[q] >> 16));
+    }
+  } else {
+    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(mb.xr) + o);
+    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(mb.xr) + o + 4);
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  }
+  const float inv = pqd::inv_scale(am);
+  uint2 q;
+  q.x = pqd::quant4(f[0], f[1], f[2], f[3], inv);
+  q.y = pqd::quant4(f[4], f[5], f[6], f[7], inv);
+  *reinterpret_cast<uint2*>(mb.xq + o) = q;
+  if (c8 == 0) mb.xscale[row] = am / 127.0f;
 }
 
 template <int DT, int KP, bool MAT16, bool NORM>
 void launch_split_kp(const void* x, const pq::RotGroup& grp, int M, int h, int krot, unsigned flags,
-                     const pq::NormArgs& nm, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>((h / 128 + kSplitWaves - 1) / kSplitWaves), static_cast<unsigned>(grp.count));
+                     const pq::NormArgs& nm, int rows_per_wave, hipStream_t stream) {
+  const int rows = rows_per_wave > 0 && rows_per_wave < M ? rows_per_wave : M;
+  const dim3 grid(static_cast<unsigned>((h / 128 + kSplitWaves - 1) / kSplitWaves), static_cast<unsigned>(grp.count),
+                  static_cast<unsigned>((M + rows - 1) / rows));
 #define PQ_SPLIT(MR_)                                                                                      \
-  if (M <= MR_) {                                                                                          \
+  if (rows <= MR_) {                                                                                       \
     rotate_split_kernel<DT, KP, MAT16, MR_, NORM><<<grid, kSplitWaves * 64, 0, stream>>>(x, grp, M, h, krot, \
                                                                                         flags, nm);          \
     return;                                                                                                \
@@ -563,22 +617,22 @@ void launch_split_kp(const void* x, const pq::RotGroup& grp, int M, int h, int k
 
 template <int DT, bool NORM>
 void launch_split_norm(const void* x, const pq::RotGroup& grp, int M, int h, int krot, unsigned flags,
-                       const pq::NormArgs& nm, hipStream_t stream) {
+                       const pq::NormArgs& nm, int rpw, hipStream_t stream) {
   const bool mat16 = (flags & PQ_RQ_MATERIALIZE_FP16) != 0;
   if (krot <= 8) {
-    if (mat16) launch_split_kp<DT, 8, true, NORM>(x, grp, M, h, krot, flags, nm, stream);
-    else launch_split_kp<DT, 8, false, NORM>(x, grp, M, h, krot, flags, nm, stream);
+    if (mat16) launch_split_kp<DT, 8, true, NORM>(x, grp, M, h, krot, flags, nm, rpw, stream);
+    else launch_split_kp<DT, 8, false, NORM>(x, grp, M, h, krot, flags, nm, rpw, stream);
   } else {
-    if (mat16) launch_split_kp<DT, 16, true, NORM>(x, grp, M, h, krot, flags, nm, stream);
-    else launch_split_kp<DT, 16, false, NORM>(x, grp, M, h, krot, flags, nm, stream);
+    if (mat16) launch_split_kp<DT, 16, true, NORM>(x, grp, M, h, krot, flags, nm, rpw, stream);
+    else launch_split_kp<DT, 16, false, NORM>(x, grp, M, h, krot, flags, nm, rpw, stream);
   }
 }
 
 template <int DT>
 void launch_split_dt(const void* x, const pq::RotGroup& grp, int M, int h, int krot, unsigned flags,
-                     const pq::NormArgs* norm, hipStream_t stream) {
-  if (norm != nullptr) launch_split_norm<DT, true>(x, grp, M, h, krot, flags, *norm, stream);
-  else launch_split_norm<DT, false>(x, grp, M, h, krot, flags, pq::NormArgs{}, stream);
+                     const pq::NormArgs* norm, int rpw, hipStream_t stream) {
+  if (norm != nullptr) launch_split_norm<DT, true>(x, grp, M, h, krot, flags, *norm, rpw, stream);
+  else launch_split_norm<DT, false>(x, grp, M, h, krot, flags, pq::NormArgs{}, rpw, stream);
 }
 
 // Per-token quant of an existing activation: absmax pass, then quant pass.
@@ -709,12 +763,18 @@ void launch_quant(const void* x, int8_t* xq, float* xscale, int64_t rows, int h,
 
 namespace pq {
 void launch_rotate_split(const void* x, int x_dtype, const RotGroup& grp, int m, int h, int krot, unsigned flags,
-                         hipStream_t stream, const NormArgs* norm) {
+                         hipStream_t stream, const NormArgs* norm, int rows_per_wave) {
   switch (x_dtype) {
-    case PQ_F32: launch_split_dt<PQ_F32>(x, grp, m, h, krot, flags, norm, stream); break;
-    case PQ_F16: launch_split_dt<PQ_F16>(x, grp, m, h, krot, flags, norm, stream); break;
-    default: launch_split_dt<PQ_BF16>(x, grp, m, h, krot, flags, norm, stream); break;
+    case PQ_F32: launch_split_dt<PQ_F32>(x, grp, m, h, krot, flags, norm, rows_per_wave, stream); break;
+    case PQ_F16: launch_split_dt<PQ_F16>(x, grp, m, h, krot, flags, norm, rows_per_wave, stream); break;
+    default: launch_split_dt<PQ_BF16>(x, grp, m, h, krot, flags, norm, rows_per_wave, stream); break;
   }
+}
+
+void launch_quant_split(const QuantGroup& grp, int m, int h, bool mat16, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>((h / 8 + 255) / 256), static_cast<unsigned>(m), static_cast<unsigned>(grp.count));
+  if (mat16) quant_split_kernel<true><<<grid, 256, 0, stream>>>(grp, h);
+  else quant_split_kernel<false><<<grid, 256, 0, stream>>>(grp, h);
 }
 
 void launch_rotate_quant_group(const void* x, int x_dtype, const RotGroup& grp, int64_t rows, int h, int krot,

@@ -53,6 +53,7 @@ CASES = [
     (3, 4096, (48, 1552, 16, 4096)),
     (1, 12288, (4096,)),
     (4, 12288, (4096, 1024)),
+    (9, 12288, (4096, 1040, 16)),
     (2, 2048, (1024, 64)),
     (5, 4096, (4096, 1024, 1024)),
     (17, 1024, (48, 1552)),

@@ -26,6 +26,7 @@ CASES = [
     (1, 4096, (4096, 1024, 1024)),
     (1, 12288, (4096,)),
     (3, 12288, (4096,)),
+    (7, 12288, (1024, 48)),
     (3, 4096, (1024, 1024)),
     (16, 12288, (4096,)),
     (300, 4096, (4096, 1024)),

@@ -35,6 +35,7 @@ CASES = [
     (3, 4096, (1024, 1024)),
     (1, 12288, (4096,)),
     (4, 8192, (1024,)),
+    (13, 8192, (1024, 64)),
     (2, 2048, (1024, 64)),
     (16, 4096, (1024, 512)),
     (300, 4096, (4096, 1024, 1024)),
