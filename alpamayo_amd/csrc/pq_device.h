@@ -203,18 +203,29 @@ __device__ __forceinline__ float wave_sum(float v) {
 template <int DT>
 __device__ __forceinline__ float row_sumsq(const void* __restrict__ x, const void* __restrict__ res, int64_t row_off,
                                            int h, int lane) {
+  // The loads of kB chunks are issued together (indices clamped into the row,
+  // so they stay unconditional); the sum then runs over the chunks in the
+  // same order as one chunk at a time, so the result does not change.
+  constexpr int kB = 4;
   float acc = 0.0f;
-  for (int c8 = lane * 8; c8 < h; c8 += 512) {
-    float f[8];
-    load8_as_f32<DT>(x, row_off + c8, f);
-    if (res != nullptr) {
-      float r[8];
-      load8_as_f32<DT>(res, row_off + c8, r);
+  for (int c0 = lane * 8; c0 < h; c0 += 512 * kB) {
+    float f[kB][8], r[kB][8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) f[e] = round_to_dt<DT>(f[e] + r[e]);
+    for (int b = 0; b < kB; ++b) {
+      const int c8 = min(c0 + 512 * b, h - 8);
+      load8_as_f32<DT>(x, row_off + c8, f[b]);
+      if (res != nullptr) load8_as_f32<DT>(res, row_off + c8, r[b]);
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc = acc + f[e] * f[e];
+    for (int b = 0; b < kB; ++b) {
+      if (c0 + 512 * b >= h) break;
+      if (res != nullptr) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[b][e] = round_to_dt<DT>(f[b][e] + r[b][e]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = acc + f[b][e] * f[b][e];
+    }
   }
   return wave_sum(acc);
 }
