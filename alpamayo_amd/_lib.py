@@ -59,6 +59,9 @@ SIGNATURES = {
     "pq_w4a8_linear": (_INT, [_P, _INT, _P, _P, _P, _P, _P, _P, _INT, _P, _INT, _I64, _I64, _I64, _INT, _UINT, _P, _SZ,
                               _P]),
     "pq_w4a8_linear_group_workspace_size": (_SZ, [_I64, _I64, _INT]),
+    "pq_w4a16_linear_group_workspace_size": (_SZ, [_I64, _I64, _INT]),
+    "pq_w4a16_linear_group": (_INT, [_P, _INT, ctypes.POINTER(LinearMember), _INT, _INT, _INT, _I64, _I64, _INT, _UINT,
+                                     _P, _SZ, _P]),
     "pq_w4a8_linear_group": (_INT, [_P, _INT, ctypes.POINTER(LinearMember), _INT, _INT, _INT, _I64, _I64, _INT, _UINT,
                                     _P, _SZ, _P]),
     "pq_w4a8_linear_group_rmsnorm": (_INT, [_P, _P, _P, ctypes.c_float, _P, _P, _INT, ctypes.POINTER(LinearMember),

@@ -95,16 +95,29 @@ __device__ __forceinline__ v8h dequant8(uint32_t w, v2h s2, v2h z2) {
 // ---------------------------------------------------------------------------
 constexpr int kW16SkinnyRows = 16;
 
+// Linears that share their input, as one decode GEMM launch: member i owns
+// workgroups first[i] .. first[i+1]-1 (set by the launcher).
+struct W16Group {
+  W16Args mem[pq::kMaxGroup];
+  int first[pq::kMaxGroup + 1];
+  int count;
+};
+
 template <int NT, int W, int U>
-__global__ __launch_bounds__(W * 64) void w16_skinny(const W16Args ar, int bias_dtype, int y_dtype, int M, int K) {
+__global__ __launch_bounds__(W * 64) void w16_skinny(const W16Group grp, int bias_dtype, int y_dtype, int M, int K) {
   __shared__ float red[W][NT][4][64];
+  int mi = 0;   // the member that owns this workgroup (wave-uniform)
+#pragma unroll
+  for (int i = 1; i < pq::kMaxGroup; ++i)
+    if (i < grp.count && static_cast<int>(blockIdx.x) >= grp.first[i]) mi = i;
+  const W16Args& ar = grp.mem[mi];
   const int G = K >> 7;
   const int N = ar.n;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar branches
   const int lane = threadIdx.x & 63;
   const int c = lane & 15;
   const int j = lane >> 4;
-  const int tile0 = blockIdx.x * NT;
+  const int tile0 = (static_cast<int>(blockIdx.x) - grp.first[mi]) * NT;
   // Rows past M repeat row M-1: MFMA rows are independent and those results
   // are never stored.
   const uint16_t* ap = ar.x + static_cast<int64_t>(c < M ? c : M - 1) * K + j * 32;
@@ -385,10 +398,12 @@ struct W16SkinnyCfg {
 // About 4-6 waves per SIMD over the grid, two column tiles per workgroup
 // for wide outputs (768+ tiles), never more waves than K groups, and the
 // shallowest batch of at least two groups that divides the K groups.
-W16SkinnyCfg choose_w16_skinny(int64_t n, int64_t k) {
+// In a group, n is the members' total and two tiles per workgroup need an
+// even tile count in every member.
+W16SkinnyCfg choose_w16_skinny(int64_t n, int64_t k, bool even = true) {
   const int G = static_cast<int>(k / 128);
   const int tiles = static_cast<int>(n / 16);
-  const int nt = (tiles % 2 == 0 && tiles >= 768) ? 2 : 1;
+  const int nt = (even && tiles % 2 == 0 && tiles >= 768) ? 2 : 1;
   const int64_t wgs = tiles / nt;
   int w = wgs * 16 <= 6144 ? 16 : wgs * 8 <= 6144 ? 8 : 4;
   while (w > 4 && w > G) w >>= 1;
@@ -401,16 +416,24 @@ W16SkinnyCfg choose_w16_skinny(int64_t n, int64_t k) {
 }
 
 template <int NT, int W, int U>
-void launch_w16_skinny_nwu(const W16Args& ar, int bias_dtype, int y_dtype, int M, int K, hipStream_t stream) {
-  const unsigned grid = static_cast<unsigned>(ar.n / 16 / NT);
-  w16_skinny<NT, W, U><<<grid, W * 64, 0, stream>>>(ar, bias_dtype, y_dtype, M, K);
+void launch_w16_skinny_nwu(W16Group grp, int bias_dtype, int y_dtype, int M, int K, hipStream_t stream) {
+  grp.first[0] = 0;
+  for (int i = 0; i < grp.count; ++i) grp.first[i + 1] = grp.first[i] + grp.mem[i].n / 16 / NT;
+  const unsigned grid = static_cast<unsigned>(grp.first[grp.count]);
+  w16_skinny<NT, W, U><<<grid, W * 64, 0, stream>>>(grp, bias_dtype, y_dtype, M, K);
 }
 
-void launch_w16_skinny(const W16Args& ar, int bias_dtype, int y_dtype, int M, int K, hipStream_t stream) {
-  const W16SkinnyCfg cfg = choose_w16_skinny(ar.n, K);
+void launch_w16_skinny(const W16Group& grp, int bias_dtype, int y_dtype, int M, int K, hipStream_t stream) {
+  int64_t n = 0;
+  bool even = true;
+  for (int i = 0; i < grp.count; ++i) {
+    n += grp.mem[i].n;
+    even = even && (grp.mem[i].n / 16) % 2 == 0;
+  }
+  const W16SkinnyCfg cfg = choose_w16_skinny(n, K, even);
 #define PQ_W16(NT_, W_, U_)                                                        \
   if (cfg.nt == NT_ && cfg.w == W_ && cfg.u == U_) {                               \
-    launch_w16_skinny_nwu<NT_, W_, U_>(ar, bias_dtype, y_dtype, M, K, stream);     \
+    launch_w16_skinny_nwu<NT_, W_, U_>(grp, bias_dtype, y_dtype, M, K, stream);     \
     return;                                                                        \
   }
 #define PQ_W16_NT(NT_)                                                             \
@@ -422,13 +445,25 @@ void launch_w16_skinny(const W16Args& ar, int bias_dtype, int y_dtype, int M, in
 #undef PQ_W16_NT
 #undef PQ_W16
   // every configuration choose_w16_skinny makes is listed above
-  if (cfg.nt == 2) launch_w16_skinny_nwu<2, 4, 4>(ar, bias_dtype, y_dtype, M, K, stream);
-  else launch_w16_skinny_nwu<1, 4, 4>(ar, bias_dtype, y_dtype, M, K, stream);
+  if (cfg.nt == 2) launch_w16_skinny_nwu<2, 4, 4>(grp, bias_dtype, y_dtype, M, K, stream);
+  else launch_w16_skinny_nwu<1, 4, 4>(grp, bias_dtype, y_dtype, M, K, stream);
+}
+
+// Decode sizes: one skinny launch over all members; larger m: one prefill
+// launch per member.
+void launch_w16_gemm_group(const W16Group& grp, int bias_dtype, int y_dtype, int M, int K, hipStream_t stream) {
+  if (M <= kW16SkinnyRows) {
+    launch_w16_skinny(grp, bias_dtype, y_dtype, M, K, stream);
+  } else {
+    for (int i = 0; i < grp.count; ++i) launch_w16_prefill(grp.mem[i], bias_dtype, y_dtype, M, K, stream);
+  }
 }
 
 void launch_w16_gemm(const W16Args& ar, int bias_dtype, int y_dtype, int M, int K, hipStream_t stream) {
-  if (M <= kW16SkinnyRows) launch_w16_skinny(ar, bias_dtype, y_dtype, M, K, stream);
-  else launch_w16_prefill(ar, bias_dtype, y_dtype, M, K, stream);
+  W16Group grp{};
+  grp.mem[0] = ar;
+  grp.count = 1;
+  launch_w16_gemm_group(grp, bias_dtype, y_dtype, M, K, stream);
 }
 
 int check_w16_args(const char* who, int64_t m, int64_t n, int64_t k, int bias_dtype, const void* bias, int y_dtype) {
@@ -482,13 +517,21 @@ extern "C" int pq_w4a16_gemm(const void* x, const uint8_t* wpack, const uint32_t
 
 extern "C" size_t pq_w4a16_linear_workspace_size(int64_t m, int64_t k) { return w16_linear_workspace(m, k); }
 
-extern "C" int pq_w4a16_linear(const void* x, int x_dtype, const uint32_t* rot_idx, const float* rot_cs,
-                               const float* scales, const uint8_t* wpack, const uint32_t* wmeta, const void* bias,
-                               int bias_dtype, void* y, int y_dtype, int64_t m, int64_t n, int64_t k, int krot,
-                               unsigned flags, void* workspace, size_t workspace_bytes, void* stream) {
-  const char* who = "pq_w4a16_linear";
-  int st = check_w16_args(who, m, n, k, bias_dtype, bias, y_dtype);
-  if (st != PQ_OK) return st;
+namespace {
+
+// The rotations of all members in one launch (grid.y = member), each into
+// its own workspace block, then one GEMM launch over all members at decode
+// sizes.
+int w16_linear_group(const char* who, const void* x, int x_dtype, const pq_linear_member* members, int count,
+                     int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot, unsigned flags, void* workspace,
+                     size_t workspace_bytes, hipStream_t s) {
+  PQ_REQUIRE(count >= 1 && count <= pq::kMaxGroup, PQ_ERR_ARG, "%s: count=%d not in 1..%d", who, count,
+             pq::kMaxGroup);
+  PQ_REQUIRE(members != nullptr, PQ_ERR_ARG, "%s: null member table", who);
+  for (int i = 0; i < count; ++i) {
+    int st = check_w16_args(who, m, members[i].n, k, bias_dtype, members[i].bias, y_dtype);
+    if (st != PQ_OK) return st;
+  }
   PQ_REQUIRE(k <= 16384, PQ_ERR_ARG, "%s: k=%lld must be at most 16384", who, (long long)k);
   PQ_REQUIRE(krot >= 1 && krot <= 16, PQ_ERR_UNSUPPORTED, "%s: krot=%d not in 1..16", who, krot);
   PQ_REQUIRE(x_dtype == PQ_F32 || x_dtype == PQ_F16 || x_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED, "%s: x dtype code %d",
@@ -496,35 +539,65 @@ extern "C" int pq_w4a16_linear(const void* x, int x_dtype, const uint32_t* rot_i
   PQ_REQUIRE((flags & ~static_cast<unsigned>(PQ_RQ_INPUT_FP16)) == 0, PQ_ERR_ARG, "%s: unknown flags 0x%x", who,
              flags);
   if (m == 0) return PQ_OK;
-  PQ_REQUIRE(x && rot_idx && rot_cs && wpack && wmeta && y, PQ_ERR_ARG, "%s: null pointer", who);
-  PQ_REQUIRE(pq::aligned_to(x, 16) && pq::aligned_to(rot_idx, 16) && pq::aligned_to(rot_cs, 16) &&
-                 pq::aligned_to(wpack, 16) && pq::aligned_to(wmeta, 4) && pq::aligned_to(y, pq::dtype_size(y_dtype)),
-             PQ_ERR_ARG, "%s: misaligned pointer", who);
-  const size_t need = w16_linear_workspace(m, k);
+  PQ_REQUIRE(x && pq::aligned_to(x, 16), PQ_ERR_ARG, "%s: x must be non-null and 16-byte aligned", who);
+  for (int i = 0; i < count; ++i) {
+    const pq_linear_member& mb = members[i];
+    PQ_REQUIRE(mb.rot_idx && mb.rot_cs && mb.wpack && mb.wmeta && mb.y, PQ_ERR_ARG, "%s: member %d: null pointer",
+               who, i);
+    PQ_REQUIRE(pq::aligned_to(mb.rot_idx, 16) && pq::aligned_to(mb.rot_cs, 16) && pq::aligned_to(mb.wpack, 16) &&
+                   pq::aligned_to(mb.wmeta, 4) && pq::aligned_to(mb.y, pq::dtype_size(y_dtype)),
+               PQ_ERR_ARG, "%s: member %d: misaligned pointer", who, i);
+  }
+  const size_t per = w16_linear_workspace(m, k);
+  const size_t need = count * per;
   PQ_REQUIRE(workspace != nullptr && workspace_bytes >= need && pq::aligned_to(workspace, 256), PQ_ERR_WORKSPACE,
-             "%s: a 256-byte aligned workspace of %zu bytes is needed for m=%lld k=%lld, got %zu", who, need,
-             (long long)m, (long long)k, workspace ? workspace_bytes : (size_t)0);
+             "%s: a 256-byte aligned workspace of %zu bytes is needed for m=%lld k=%lld count=%d, got %zu", who, need,
+             (long long)m, (long long)k, count, workspace ? workspace_bytes : (size_t)0);
 
   // The rotation writes its result rounded to fp16 (the reference's
   // rotation output for fp16 activations), which is this GEMM's A operand.
-  hipStream_t s = static_cast<hipStream_t>(stream);
   const int M = static_cast<int>(m), K = static_cast<int>(k);
   char* ws = static_cast<char*>(workspace);
-  void* rows = ws;
+  const bool split = m <= pq::kSplitMaxRows;
   pq::RotGroup rg{};
-  rg.count = 1;
-  const unsigned rflags = flags | PQ_RQ_MATERIALIZE_FP16;
-  if (m <= pq::kSplitMaxRows) {
-    float* gmax = reinterpret_cast<float*>(ws + align_up(static_cast<size_t>(m) * k * 2, 256));
-    rg.mem[0] = {rot_idx, rot_cs, scales, rows, gmax, nullptr};
-    pq::launch_rotate_split(x, x_dtype, rg, M, K, krot, rflags, s);
-  } else {
-    rg.mem[0] = {rot_idx, rot_cs, scales, nullptr, nullptr, rows};
-    pq::launch_rotate_quant_group(x, x_dtype, rg, m, K, krot, rflags, s);
+  W16Group gg{};
+  rg.count = gg.count = count;
+  for (int i = 0; i < count; ++i) {
+    const pq_linear_member& mb = members[i];
+    char* rows = ws + i * per;
+    float* gmax = reinterpret_cast<float*>(rows + align_up(static_cast<size_t>(m) * k * 2, 256));
+    if (split) rg.mem[i] = {mb.rot_idx, mb.rot_cs, mb.scales, rows, gmax, nullptr};
+    else rg.mem[i] = {mb.rot_idx, mb.rot_cs, mb.scales, nullptr, nullptr, rows};
+    gg.mem[i] = {reinterpret_cast<const uint16_t*>(rows), mb.wpack, mb.wmeta, mb.bias, mb.y, static_cast<int>(mb.n)};
   }
-  st = pq::launch_status("pq_w4a16_linear rotation launch");
+  const unsigned rflags = flags | PQ_RQ_MATERIALIZE_FP16;
+  if (split) pq::launch_rotate_split(x, x_dtype, rg, M, K, krot, rflags, s);
+  else pq::launch_rotate_quant_group(x, x_dtype, rg, m, K, krot, rflags, s);
+  int st = pq::launch_status("W4A16 linear rotation launch");
   if (st != PQ_OK) return st;
-  const W16Args ar = {static_cast<const uint16_t*>(rows), wpack, wmeta, bias, y, static_cast<int>(n)};
-  launch_w16_gemm(ar, bias_dtype, y_dtype, M, K, s);
-  return pq::launch_status("pq_w4a16_linear GEMM launch");
+  launch_w16_gemm_group(gg, bias_dtype, y_dtype, M, K, s);
+  return pq::launch_status("W4A16 linear GEMM launch");
+}
+
+}  // namespace
+
+extern "C" int pq_w4a16_linear(const void* x, int x_dtype, const uint32_t* rot_idx, const float* rot_cs,
+                               const float* scales, const uint8_t* wpack, const uint32_t* wmeta, const void* bias,
+                               int bias_dtype, void* y, int y_dtype, int64_t m, int64_t n, int64_t k, int krot,
+                               unsigned flags, void* workspace, size_t workspace_bytes, void* stream) {
+  const pq_linear_member one = {rot_idx, rot_cs, scales, wpack, wmeta, bias, y, n};
+  return w16_linear_group("pq_w4a16_linear", x, x_dtype, &one, 1, bias_dtype, y_dtype, m, k, krot, flags, workspace,
+                          workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t pq_w4a16_linear_group_workspace_size(int64_t m, int64_t k, int count) {
+  if (count < 1 || count > pq::kMaxGroup) return 0;
+  return count * w16_linear_workspace(m, k);
+}
+
+extern "C" int pq_w4a16_linear_group(const void* x, int x_dtype, const pq_linear_member* members, int count,
+                                     int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot, unsigned flags,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  return w16_linear_group("pq_w4a16_linear_group", x, x_dtype, members, count, bias_dtype, y_dtype, m, k, krot, flags,
+                          workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }

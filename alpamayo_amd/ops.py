@@ -73,6 +73,9 @@ _pq_lib.define("w4a8_linear_group_fused(Tensor x, Tensor? x2, Tensor? norm_weigh
                "bool return_h, bool return_sum) -> Tensor[]")
 _pq_lib.define("w4a16_prepack(Tensor awq_qweight, Tensor scales, Tensor scaled_zeros) -> (Tensor, Tensor)")
 _pq_lib.define("w4a16_gemm(Tensor x, Tensor wpack, Tensor wmeta, Tensor? bias, ScalarType out_dtype) -> Tensor")
+_pq_lib.define("w4a16_linear_group(Tensor x, Tensor[] rot_idx, Tensor[] rot_cs, Tensor?[] scales, int krot, "
+               "Tensor[] wpack, Tensor[] wmeta, Tensor?[] bias, Tensor? workspace, bool input_fp16, "
+               "ScalarType out_dtype) -> Tensor[]")
 _pq_lib.define("w4a16_linear(Tensor x, Tensor rot_idx, Tensor rot_cs, Tensor? scales, int krot, Tensor wpack, "
                "Tensor wmeta, Tensor? bias, Tensor? workspace, bool input_fp16, ScalarType out_dtype) -> Tensor")
 
@@ -835,6 +838,41 @@ def _w16_linear_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, works
 
 
 _pq_lib.impl("w4a16_linear", _w16_linear_impl, "CUDA")
+
+
+def _w16_linear_group_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16, out_dtype):
+    """paroquant::w4a16_linear for linears that read the same x, in one rotation launch and (m <= 16) one GEMM."""
+    dev = x.device
+    _require(x.dtype in _DT, f"x must be float32/float16/bfloat16, got {x.dtype}")
+    xc = x.contiguous()
+    members, outs, keep, bias_dt, m, k = _group_members(xc, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
+                                                        out_dtype)
+    count = len(outs)
+    lib = _lib.load()
+    need = int(lib.pq_w4a16_linear_group_workspace_size(m, k, count))
+    scratch = None
+    if need > 0:
+        if (workspace is not None and workspace.dtype == torch.uint8 and workspace.is_contiguous()
+                and workspace.numel() >= need and workspace.data_ptr() % 256 == 0):
+            _same_device("workspace", workspace, dev)
+            scratch = workspace
+        else:
+            scratch = torch.empty(need, dtype=torch.uint8, device=dev)
+    flags = _lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0
+    with _DeviceGuard(dev):
+        st = lib.pq_w4a16_linear_group(xc.data_ptr(), _DT[x.dtype], members, count, bias_dt, _DT[out_dtype], m, k,
+                                       krot, flags, scratch.data_ptr() if scratch is not None else None,
+                                       scratch.numel() if scratch is not None else 0, _stream(dev))
+    _lib.check(st, "paroquant::w4a16_linear_group")
+    return [y.view(*x.shape[:-1], y.size(1)) for y in outs]
+
+
+_pq_lib.impl("w4a16_linear_group", _w16_linear_group_impl, "CUDA")
+
+
+@torch.library.register_fake("paroquant::w4a16_linear_group")
+def _w16_linear_group_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16, out_dtype):
+    return [x.new_empty((*x.shape[:-1], w.size(0) * 16), dtype=out_dtype) for w in wpack]
 
 
 @torch.library.register_fake("paroquant::w4a16_linear")

@@ -438,10 +438,20 @@ def main() -> int:
                       w16_meta(m.rotate_linear.qlinear.scales), N, K) for m, (N, K) in zip(L, shapes)]
                     for L in pool]
 
-        def run16(li, X, gemm_only=False):
+        def group16(members, x):
+            rs = [m[0] for m in members]
+            return torch.ops.paroquant.w4a16_linear_group(
+                x, [r.rot_idx for r in rs], [r.rot_cs for r in rs], [r.scales_f32 for r in rs], rs[0].krot,
+                [m[1] for m in members], [m[2] for m in members], [None] * len(members), None, False, f16)
+
+        def run16(li, X, gemm_only=False, grouped=False):
             xa, xo, xm, xd = X
+            L16 = w16_pool[li]
+            if grouped:   # q/k/v and gate/up as groups over their shared inputs, o and down alone
+                return (group16(L16[0:3], xa) + group16(L16[3:4], xo) + group16(L16[4:6], xm)
+                        + group16(L16[6:7], xd))
             outs = []
-            for (rot, wp, wm16, N, K), x in zip(w16_pool[li], (xa, xa, xa, xo, xm, xm, xd)):
+            for (rot, wp, wm16, N, K), x in zip(L16, (xa, xa, xa, xo, xm, xm, xd)):
                 if gemm_only:
                     outs.append(torch.ops.paroquant.w4a16_gemm(x, wp, wm16, None, f16))
                 else:
@@ -449,12 +459,12 @@ def main() -> int:
                                                                  rot.krot, wp, wm16, None, None, False, f16))
             return outs
 
-        def capture16(xs, gemm_only, layers):
+        def capture16(xs, gemm_only, layers, grouped=False):
             for li in layers:
-                run16(li, xs[li], gemm_only)
+                run16(li, xs[li], gemm_only, grouped)
             gr = torch.cuda.CUDAGraph()
             with torch.cuda.graph(gr):
-                outs = [run16(li, xs[li], gemm_only) for li in layers]
+                outs = [run16(li, xs[li], gemm_only, grouped) for li in layers]
             return gr, outs
 
         x16 = [tuple(a.to(f16) for a in X) for X in make_inputs(1, 8001)]
@@ -462,17 +472,23 @@ def main() -> int:
         d_ms = time_graphs([gr], args.steps // P, -(-args.warmup // P)) / P
         d_b = sum(w16_linear_bytes(1, N, K) for N, K in shapes)
         del gr
+        gr, _ = capture16(x16, False, range(P), grouped=True)
+        dgr_ms = time_graphs([gr], args.steps // P, -(-args.warmup // P)) / P
+        del gr
         gr, _ = capture16(x16, True, range(P))
         dg_ms = time_graphs([gr], max(10, args.steps // 10), 3) / P
         dg_b = sum(w16_gemm_bytes(1, N, K) for N, K in shapes)
         del gr
+        log(f"W4A16 decode M=1 grouped: {dgr_ms * 1e3:.1f} us/layer ({d_b / (dgr_ms * 1e-3) / 1e9:.0f} GB/s)")
         log(f"W4A16 decode M=1: {d_ms * 1e3:.1f} us/layer ({d_b / (d_ms * 1e-3) / 1e9:.0f} GB/s); GEMMs alone "
             f"{dg_ms * 1e3 / 7:.2f} us/launch ({dg_b / (dg_ms * 1e-3) / 1e9:.0f} GB/s)")
         w16 = {"decode_M1": {"us_per_layer": round(d_ms * 1e3, 2), "GBps": round(d_b / (d_ms * 1e-3) / 1e9, 1),
                              "frac_hbm": round(d_b / (d_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                              "gemm_only_us_per_launch": round(dg_ms * 1e3 / 7, 3),
                              "gemm_only_GBps": round(dg_b / (dg_ms * 1e-3) / 1e9, 1),
-                             "gemm_only_frac_hbm": round(dg_b / (dg_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
+                             "gemm_only_frac_hbm": round(dg_b / (dg_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                             "grouped_us_per_layer": round(dgr_ms * 1e3, 2),
+                             "grouped_GBps": round(d_b / (dgr_ms * 1e-3) / 1e9, 1)}}
         if not args.no_prefill:
             M = 3072
             g = workloads.generator(6200, device=dev)

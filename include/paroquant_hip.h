@@ -37,6 +37,8 @@
  *   pq_w4a16_linear      RotateLinearInt4.forward with a WQLinear:
  *                        rotation::rotate -> WQLinear.forward
  *                        (rotation_linear.py:136-139)
+ *   pq_w4a16_linear_group  the same for linears sharing their input
+ *                        (no counterpart)
  */
 #ifndef PAROQUANT_HIP_H
 #define PAROQUANT_HIP_H
@@ -294,6 +296,21 @@ int pq_w4a16_linear(const void* x, int x_dtype, const uint32_t* rot_idx, const f
                     const uint8_t* wpack, const uint32_t* wmeta, const void* bias, int bias_dtype, void* y,
                     int y_dtype, int64_t m, int64_t n, int64_t k, int krot, unsigned flags, void* workspace,
                     size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace pq_w4a16_linear_group needs for count members sharing
+ * an [m, k] input: count times what pq_w4a16_linear needs for one; 0 for a
+ * count outside 1..4. */
+size_t pq_w4a16_linear_group_workspace_size(int64_t m, int64_t k, int count);
+
+/* pq_w4a16_linear for count (1..4) linears that read the same x (q/k/v,
+ * gate/up): one rotation launch over all members and, for m <= 16, one GEMM
+ * launch over their concatenated columns (for larger m, one GEMM launch per
+ * member).  Each member's y is what pq_w4a16_linear gives for it.  Members
+ * as for pq_w4a8_linear_group.  No counterpart in the reference (its
+ * linears run one by one, rotation_linear.py:136-139 each). */
+int pq_w4a16_linear_group(const void* x, int x_dtype, const pq_linear_member* members, int count,
+                          int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot, unsigned flags,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* pq_w4a8_linear_group behind a decoder layer's elementwise step, chosen by
  * mode (PQ_PRO_*), in the same two launches; the members read

@@ -241,6 +241,17 @@ def test_linear_group_fused_argument_checks():
     assert call(_lib.PQ_PRO_SWIGLU, m=0) == 0
 
 
+def test_w4a16_group_workspace_rule():
+    lib = _lib.load()
+    for m, k in ((1, 4096), (16, 12288), (300, 4096)):
+        one = lib.pq_w4a16_linear_workspace_size(m, k)
+        assert one > 0
+        for count in (1, 2, 3, 4):
+            assert lib.pq_w4a16_linear_group_workspace_size(m, k, count) == count * one
+    assert lib.pq_w4a16_linear_group_workspace_size(1, 4096, 0) == 0
+    assert lib.pq_w4a16_linear_group_workspace_size(1, 4096, 5) == 0
+
+
 def test_split_path_rule():
     lib = _lib.load()
     assert lib.pq_w4a8_linear_split_path(1, 4096) == 1

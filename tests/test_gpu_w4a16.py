@@ -243,3 +243,37 @@ def test_graph_replay(m):
         assert torch.equal(out, eager), f"replay {i}"
         rl(x + 1.0)   # eager work between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("m", [1, 5, 16, 20])
+@pytest.mark.parametrize("ns", [(1024, 1040, 64), (12288, 12288)])
+def test_linear_group_matches_single_linears(m, ns):
+    """paroquant::w4a16_linear_group (one rotation launch; one GEMM launch at m <= 16, tiles of every member
+    in one grid) gives each member what paroquant::w4a16_linear gives it alone.  The group's launch may split
+    K over a different number of waves (its workgroup count is the members' total), which changes the
+    float32 summation order: the outputs then agree to one rounding of the output format."""
+    print(f"w4a16 group m={m} ns={ns}", flush=True)
+    from tests.gpu_util import packed_rotation
+
+    k = 4096
+    x = workloads.activations(m, k, workloads.generator(3900 + m)).cuda()
+    args = []
+    for i, n in enumerate(ns):
+        spec = workloads.linear_spec(f"m{i}", n, k, workloads.generator(3910 + 7 * i + n), keep_codes=True)
+        rot_idx, rot_cs, _, _ = packed_rotation(spec.pairs, spec.theta)
+        s, sz = workloads.w16_scales(spec.w)
+        wpack, wmeta = _prepack(spec.w, s, sz)
+        scales = spec.channel_scales.float().reshape(-1).cuda()
+        bias = (torch.randn(n, generator=torch.Generator().manual_seed(i)) * 0.1).half().cuda() if i == 0 else None
+        args.append((rot_idx.cuda(), rot_cs.cuda(), scales, wpack, wmeta, bias))
+    outs = torch.ops.paroquant.w4a16_linear_group(x, [a[0] for a in args], [a[1] for a in args],
+                                                  [a[2] for a in args], 8, [a[3] for a in args],
+                                                  [a[4] for a in args], [a[5] for a in args], None, True,
+                                                  torch.bfloat16)
+    for (ri, rc, sc, wp, wm, b), y, n in zip(args, outs, ns):
+        ref = torch.ops.paroquant.w4a16_linear(x, ri, rc, sc, 8, wp, wm, b, None, True, torch.bfloat16)
+        torch.cuda.synchronize()
+        assert y.shape == (m, n)
+        yf, rf = y.float(), ref.float()
+        rms = rf.pow(2).mean().sqrt()
+        assert torch.all((yf - rf).abs() <= _ULP_REL[torch.bfloat16] * rf.abs() + 1e-4 * rms)
