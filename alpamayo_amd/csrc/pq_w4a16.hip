@@ -485,13 +485,15 @@ int check_w16_args(const char* who, int64_t m, int64_t n, int64_t k, int bias_dt
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Workspace of the linear: the rotated fp16 rows [m][k] (256-byte aligned
-// size), then -- decode sizes, where the split rotation runs -- its
-// per-group maxima (unused by this GEMM).
+// Workspace of the linear (one block per member of a group): the rotated
+// fp16 rows [m][k] (256-byte aligned size), then -- decode sizes, where the
+// split rotation runs -- its per-group maxima (unused by this GEMM); the
+// block is rounded up to 256 bytes so that every member's rows start
+// 256-byte aligned (the GEMM reads them with 16-byte vector loads).
 size_t w16_linear_workspace(int64_t m, int64_t k) {
   if (m <= 0 || k <= 0 || k % 128) return 0;
   const size_t rows = align_up(static_cast<size_t>(m) * k * 2, 256);
-  if (m <= pq::kSplitMaxRows) return rows + static_cast<size_t>(m) * (k / 128) * sizeof(float);
+  if (m <= pq::kSplitMaxRows) return align_up(rows + static_cast<size_t>(m) * (k / 128) * sizeof(float), 256);
   return rows;
 }
 

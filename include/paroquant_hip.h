@@ -282,8 +282,9 @@ int pq_w4a16_gemm(const void* x, const uint8_t* wpack, const uint32_t* wmeta, co
                   void* y, int y_dtype, int64_t m, int64_t n, int64_t k, int group_size, void* stream);
 
 /* Bytes of scratch pq_w4a16_linear needs between its two kernels: the
- * rotated fp16 rows, 2*m*k rounded up to 256, plus 4*m*(k/128) bytes when
- * m <= 16.  Its content does not matter. */
+ * rotated fp16 rows, 2*m*k rounded up to 256, plus, when m <= 16,
+ * 4*m*(k/128) bytes of group maxima, the sum rounded up to 256.  Its content
+ * does not matter. */
 size_t pq_w4a16_linear_workspace_size(int64_t m, int64_t k);
 
 /* y = pq_w4a16_gemm of the rotation of x, rounded to fp16: x [m, k]

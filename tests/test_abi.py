@@ -193,7 +193,9 @@ def test_w4a16_argument_checks():
     assert linear(k=32768) == 1
     assert linear(m=0) == 0
     need1 = lib.pq_w4a16_linear_workspace_size(1, 4096)
-    assert need1 == 2 * 4096 + 4 * 32                       # fp16 row + the split rotation's group maxima
+    assert need1 == 2 * 4096 + 256                           # fp16 row + the split rotation's group maxima,
+    assert lib.pq_w4a16_linear_workspace_size(1, 1152) == 2560          # the sum rounded up to 256 bytes
+    assert lib.pq_w4a16_linear_workspace_size(3, 384) == 2560
     need64 = lib.pq_w4a16_linear_workspace_size(64, 4096)
     assert need64 == 64 * 4096 * 2
     assert lib.pq_w4a16_linear_workspace_size(0, 4096) == 0
@@ -243,9 +245,9 @@ def test_linear_group_fused_argument_checks():
 
 def test_w4a16_group_workspace_rule():
     lib = _lib.load()
-    for m, k in ((1, 4096), (16, 12288), (300, 4096)):
+    for m, k in ((1, 4096), (16, 12288), (300, 4096), (1, 1152), (3, 384), (1, 384)):
         one = lib.pq_w4a16_linear_workspace_size(m, k)
-        assert one > 0
+        assert one > 0 and one % 256 == 0     # every member's block starts 256-byte aligned
         for count in (1, 2, 3, 4):
             assert lib.pq_w4a16_linear_group_workspace_size(m, k, count) == count * one
     assert lib.pq_w4a16_linear_group_workspace_size(1, 4096, 0) == 0

@@ -277,3 +277,35 @@ def test_linear_group_matches_single_linears(m, ns):
         yf, rf = y.float(), ref.float()
         rms = rf.pow(2).mean().sqrt()
         assert torch.all((yf - rf).abs() <= _ULP_REL[torch.bfloat16] * rf.abs() + 1e-4 * rms)
+
+
+@pytest.mark.parametrize("m", [1, 3])
+@pytest.mark.parametrize("k", [384, 1152])
+def test_linear_group_member_blocks_aligned_small_k(m, k):
+    """Groups whose per-member scratch (fp16 rows + group maxima) is not a multiple of 16 bytes before
+    rounding (m * (k / 128) not a multiple of 4): every member's rows still start 256-byte aligned, and each
+    member gets what paroquant::w4a16_linear gives it alone."""
+    print(f"w4a16 group small k={k} m={m}", flush=True)
+    from tests.gpu_util import packed_rotation
+
+    ns = (64, 48, 32)
+    x = workloads.activations(m, k, workloads.generator(3950 + m + k)).cuda()
+    args = []
+    for i, n in enumerate(ns):
+        spec = workloads.linear_spec(f"s{i}", n, k, workloads.generator(3960 + 7 * i + n + k), keep_codes=True)
+        rot_idx, rot_cs, _, _ = packed_rotation(spec.pairs, spec.theta)
+        s, sz = workloads.w16_scales(spec.w)
+        wpack, wmeta = _prepack(spec.w, s, sz)
+        args.append((rot_idx.cuda(), rot_cs.cuda(), spec.channel_scales.float().reshape(-1).cuda(), wpack, wmeta))
+    need = alpamayo_amd.ops._lib.load().pq_w4a16_linear_group_workspace_size(m, k, len(ns))
+    assert need % (256 * len(ns)) == 0
+    outs = torch.ops.paroquant.w4a16_linear_group(x, [a[0] for a in args], [a[1] for a in args],
+                                                  [a[2] for a in args], 8, [a[3] for a in args],
+                                                  [a[4] for a in args], [None] * len(ns), None, True, torch.bfloat16)
+    for (ri, rc, sc, wp, wm), y, n in zip(args, outs, ns):
+        ref = torch.ops.paroquant.w4a16_linear(x, ri, rc, sc, 8, wp, wm, None, None, True, torch.bfloat16)
+        torch.cuda.synchronize()
+        assert y.shape == (m, n)
+        yf, rf = y.float(), ref.float()
+        rms = rf.pow(2).mean().sqrt()
+        assert torch.all((yf - rf).abs() <= _ULP_REL[torch.bfloat16] * rf.abs() + 1e-4 * rms)
