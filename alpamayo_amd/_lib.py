@@ -22,6 +22,7 @@ PQ_RQ_INPUT_FP16 = 1
 PQ_RQ_MATERIALIZE_FP16 = 2
 PQ_PRO_RMSNORM, PQ_PRO_ADD, PQ_PRO_SWIGLU = 1, 2, 3
 PQ_ROWS_SAME, PQ_ROWS_MXFP4 = 0, 1
+PQ_NOALLOC_SCRATCH_BYTES = 16 << 20
 
 STATUS_NAMES = {0: "PQ_OK", 1: "PQ_ERR_ARG", 2: "PQ_ERR_UNSUPPORTED", 3: "PQ_ERR_HIP", 4: "PQ_ERR_WORKSPACE"}
 STATUS_CODE = {v: k for k, v in STATUS_NAMES.items()}
@@ -58,6 +59,8 @@ SIGNATURES = {
     "pq_w4a8_linear_workspace_size": (_SZ, [_I64, _I64, _I64, _INT]),
     "pq_w4a8_linear": (_INT, [_P, _INT, _P, _P, _P, _P, _P, _P, _INT, _P, _INT, _I64, _I64, _I64, _INT, _UINT, _P, _SZ,
                               _P]),
+    "pq_w4a8_linear_noalloc": (_INT, [_P, _INT, _P, _P, _P, _P, _P, _P, _INT, _P, _INT, _I64, _I64, _I64, _INT, _UINT,
+                                      _P]),
     "pq_w4a8_linear_group_workspace_size": (_SZ, [_I64, _I64, _INT]),
     "pq_w4a16_linear_group_workspace_size": (_SZ, [_I64, _I64, _INT]),
     "pq_w4a16_linear_group": (_INT, [_P, _INT, ctypes.POINTER(LinearMember), _INT, _INT, _INT, _I64, _I64, _INT, _UINT,

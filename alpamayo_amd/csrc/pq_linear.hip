@@ -23,8 +23,16 @@
 // Reference: BF16RotateLinearWrapper -> RotateLinearInt4 -> rotation::rotate
 // -> MarlinW4A8Linear (src/alpamayo_r1/utils/quantization/
 // paroquant_marlin_w4a8.py:59-65, 314-333; rotation_linear.py:120-124).
+#include <mutex>
+
 #include "pq_device.h"
 #include "pq_internal.h"
+
+// Scratch of pq_w4a8_linear_noalloc: one array per GPU, resident until the
+// process ends.  Host code never uses this name as an address (on the host it
+// is only a handle); it reads each device's address once with
+// hipGetSymbolAddress and passes that pointer to the kernels.
+static __device__ __align__(256) unsigned char scratch[PQ_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -192,6 +200,55 @@ extern "C" int pq_w4a8_linear(const void* x, int x_dtype, const uint32_t* rot_id
   const pq_linear_member one = {rot_idx, rot_cs, scales, wpack, wmeta, bias, y, n};
   return linear_group("pq_w4a8_linear", x, x_dtype, &one, 1, bias_dtype, y_dtype, m, k, krot, flags, workspace,
                       workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up on the
+// first call made with that device current.
+int noalloc_scratch(const char* who, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  PQ_REQUIRE(e == hipSuccess, PQ_ERR_HIP, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+  PQ_REQUIRE(dev >= 0 && dev < kMaxDevices, PQ_ERR_UNSUPPORTED, "%s: device %d beyond the %d devices supported",
+             who, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    PQ_REQUIRE(e == hipSuccess && p != nullptr, PQ_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s",
+               who, dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PQ_OK;
+}
+
+}  // namespace
+
+extern "C" int pq_w4a8_linear_noalloc(const void* x, int x_dtype, const uint32_t* rot_idx, const float* rot_cs,
+                                      const float* scales, const uint8_t* wpack, const uint32_t* wmeta,
+                                      const void* bias, int bias_dtype, void* y, int y_dtype, int64_t m, int64_t n,
+                                      int64_t k, int krot, unsigned flags, void* stream) {
+  const char* who = "pq_w4a8_linear_noalloc";
+  // Size check first, on the host: nothing touches the GPU for a rejected call.
+  const size_t need = group_workspace_size(m, k, 1);
+  PQ_REQUIRE(need <= PQ_NOALLOC_SCRATCH_BYTES, PQ_ERR_WORKSPACE,
+             "%s: m=%lld k=%lld needs %zu bytes of scratch, above the library's fixed %zu bytes "
+             "(use pq_w4a8_linear with a workspace)",
+             who, (long long)m, (long long)k, need, (size_t)PQ_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (m > 0 && need > 0) {
+    const int st = noalloc_scratch(who, &ws);
+    if (st != PQ_OK) return st;
+  }
+  const pq_linear_member one = {rot_idx, rot_cs, scales, wpack, wmeta, bias, y, n};
+  return linear_group(who, x, x_dtype, &one, 1, bias_dtype, y_dtype, m, k, krot, flags, ws,
+                      ws != nullptr ? (size_t)PQ_NOALLOC_SCRATCH_BYTES : 0, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int pq_w4a8_linear_group(const void* x, int x_dtype, const pq_linear_member* members, int count,

@@ -203,6 +203,30 @@ int pq_w4a8_linear(const void* x, int x_dtype, const uint32_t* rot_idx, const fl
                    int y_dtype, int64_t m, int64_t n, int64_t k, int krot, unsigned flags, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* Bytes of the library's fixed scratch array used by pq_w4a8_linear_noalloc
+ * (one array per GPU, held until the process ends). */
+#define PQ_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* pq_w4a8_linear without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The scratch between its kernels is a
+ * fixed array of PQ_NOALLOC_SCRATCH_BYTES per GPU inside the library (its
+ * address is looked up once per device, on the first call made with that
+ * device current); the call itself allocates nothing.  Same kernels and same
+ * results as pq_w4a8_linear.  Fails with PQ_ERR_WORKSPACE, before touching
+ * the GPU, when pq_w4a8_linear_workspace_size(m, n, k, krot) exceeds
+ * PQ_NOALLOC_SCRATCH_BYTES (e.g. more than about 16.7M int8 activations on
+ * the row path: m = 3072 at k = 4096 fits, at k = 12288 it does not).
+ * Every call on one GPU shares that GPU's array, which keeps the last call's
+ * contents (the kernels write it before reading it; nothing needs to start at
+ * zero): calls that overlap in time on one GPU -- on different streams, or
+ * from different threads -- race and must be serialized by the caller.
+ * No counterpart in the reference; it exists for the callers above. */
+int pq_w4a8_linear_noalloc(const void* x, int x_dtype, const uint32_t* rot_idx, const float* rot_cs,
+                           const float* scales, const uint8_t* wpack, const uint32_t* wmeta, const void* bias,
+                           int bias_dtype, void* y, int y_dtype, int64_t m, int64_t n, int64_t k, int krot,
+                           unsigned flags, void* stream);
+
 /* One linear of a group that shares its input x (pq_w4a8_linear_group). */
 typedef struct pq_linear_member {
   const uint32_t* rot_idx; /* this linear's rotation operands (pq_rotation_pack) */
