@@ -47,6 +47,8 @@ SIGNATURES = {
     "pq_abi_version": (_INT, []),
     "pq_last_error": (ctypes.c_char_p, []),
     "pq_rotate": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _INT, _INT, _INT, _P]),
+    "pq_rotate_backward_workspace_size": (_SZ, [_I64, _I64, _INT]),
+    "pq_rotate_backward": (_INT, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _INT, _INT, _INT, _P, _SZ, _P]),
     "pq_rotate_mxfp4": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _INT, _INT, _INT, _P]),
     "pq_rotate_rows": (_INT, [_P, _INT, _P, _P, _P, _P, _P, _I64, _I64, _INT, _INT, _P]),
     "pq_rotate_quant_i8": (_INT, [_P, _INT, _P, _P, _P, _P, _P, _P, _I64, _I64, _INT, _UINT, _P]),

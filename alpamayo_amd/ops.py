@@ -5,28 +5,34 @@
 the ``paroquant`` namespace:
 
   rotation::rotate(x, idx_ij, theta, scales?, group_size) -> y
+  paroquant::rotate_backward(grad_y, x, idx_ij, theta, scales?, group_size) -> (grad_x, grad_theta, grad_scales)
   paroquant::rotate_quant_i8(x, rot_idx, rot_cs, scales?, krot, input_fp16, materialize_fp16) -> (xq, xscale)
   paroquant::rotate_quant_i8_rot(...)                 -> (xq, xscale, xrot fp16)
   paroquant::quant_i8(x) -> (xq, xscale)
-  paroquant::w4a8_gemm(xq, xscale, wpack, wmeta, bias?, workspace?, out_dtype) -> y
+  paroquant::w4a8_gemm(xq, xscale, wpack, wmeta, bias?, out_dtype) -> y
   paroquant::w4a8_gemm_partials(xq, wpack, wmeta) -> int32 [m, k/128, n]
   paroquant::w4a8_prepack(awq_qweight, awq_scales, awq_qzeros) -> (wpack, wmeta)
-  paroquant::w4a8_linear(x, rot_idx, rot_cs, scales?, krot, wpack, wmeta, bias?, workspace?,
+  paroquant::w4a8_linear(x, rot_idx, rot_cs, scales?, krot, wpack, wmeta, bias?,
                          input_fp16, materialize_fp16, out_dtype) -> y
   paroquant::w4a8_linear_group(x, rot_idx[], rot_cs[], scales?[], krot, wpack[], wmeta[], bias?[],
-                               workspace?, input_fp16, materialize_fp16, out_dtype) -> y[]
+                               input_fp16, materialize_fp16, out_dtype) -> y[]
       (1..4 linears sharing the input x, in two launches for the whole group)
   paroquant::w4a8_linear_group_rmsnorm(x, residual?, norm_weight, eps, <the group's arguments>,
                                        return_normed, return_sum) -> y[] (+ h) (+ x + residual)
       (the same group behind a decoder layer's RMSNorm of x + residual, still two launches)
 
-``pack_rotation`` (host) turns Rotation's pairs/angles into rot_idx/rot_cs.
+``pack_rotation`` (host) turns Rotation's pairs/angles into rot_idx/rot_cs;
+``register_packed_rotation`` lets rotation::rotate find them (it never packs
+them itself).
 
 Implementations are registered for the CUDA (HIP) dispatch key only, like the
 reference (rotation.cu:581-584); CPU tensors raise from the dispatcher.  Each
 op has a fake (meta) kernel so torch.compile and graph capture can trace it.
 Every op allocates its outputs with torch on the input's device and enqueues
-its kernels on the current stream; none synchronises.
+its kernels on the current stream; none synchronises.  Scratch between an
+op's kernels comes from torch's caching allocator (inside a graph capture,
+the graph's pool at fixed addresses); the C ABI below takes it as an
+explicit workspace argument instead.
 """
 
 from __future__ import annotations
@@ -48,36 +54,39 @@ _rotation_lib.define("rotate_and_quant_mxfp4(Tensor x, Tensor idx_ij, Tensor the
                      "int group_size) -> (Tensor, Tensor)")
 
 _pq_lib = torch.library.Library("paroquant", "DEF")
+# Gradients of rotation::rotate (grad_x, grad_theta, grad_scales; the last empty when scales is None).
+_pq_lib.define("rotate_backward(Tensor grad_y, Tensor x, Tensor idx_ij, Tensor theta, Tensor? scales, "
+               "int group_size) -> (Tensor, Tensor, Tensor)")
 _pq_lib.define("rotate_quant_i8(Tensor x, Tensor rot_idx, Tensor rot_cs, Tensor? scales, int krot, bool input_fp16, "
                "bool materialize_fp16) -> (Tensor, Tensor)")
 _pq_lib.define("rotate_quant_i8_rot(Tensor x, Tensor rot_idx, Tensor rot_cs, Tensor? scales, int krot, "
                "bool input_fp16, bool materialize_fp16) -> (Tensor, Tensor, Tensor)")
 _pq_lib.define("quant_i8(Tensor x) -> (Tensor, Tensor)")
-_pq_lib.define("w4a8_gemm(Tensor xq, Tensor xscale, Tensor wpack, Tensor wmeta, Tensor? bias, Tensor? workspace, "
+_pq_lib.define("w4a8_gemm(Tensor xq, Tensor xscale, Tensor wpack, Tensor wmeta, Tensor? bias, "
                "ScalarType out_dtype) -> Tensor")
 _pq_lib.define("w4a8_gemm_partials(Tensor xq, Tensor wpack, Tensor wmeta) -> Tensor")
 _pq_lib.define("w4a8_prepack(Tensor awq_qweight, Tensor awq_scales, Tensor awq_qzeros) -> (Tensor, Tensor)")
 _pq_lib.define("w4a8_linear(Tensor x, Tensor rot_idx, Tensor rot_cs, Tensor? scales, int krot, Tensor wpack, "
-               "Tensor wmeta, Tensor? bias, Tensor? workspace, bool input_fp16, bool materialize_fp16, "
+               "Tensor wmeta, Tensor? bias, bool input_fp16, bool materialize_fp16, "
                "ScalarType out_dtype) -> Tensor")
 _pq_lib.define("w4a8_linear_group(Tensor x, Tensor[] rot_idx, Tensor[] rot_cs, Tensor?[] scales, int krot, "
-               "Tensor[] wpack, Tensor[] wmeta, Tensor?[] bias, Tensor? workspace, bool input_fp16, "
+               "Tensor[] wpack, Tensor[] wmeta, Tensor?[] bias, bool input_fp16, "
                "bool materialize_fp16, ScalarType out_dtype) -> Tensor[]")
 _pq_lib.define("w4a8_linear_group_rmsnorm(Tensor x, Tensor? residual, Tensor norm_weight, float eps, "
                "Tensor[] rot_idx, Tensor[] rot_cs, Tensor?[] scales, int krot, Tensor[] wpack, Tensor[] wmeta, "
-               "Tensor?[] bias, Tensor? workspace, bool input_fp16, bool materialize_fp16, ScalarType out_dtype, "
+               "Tensor?[] bias, bool input_fp16, bool materialize_fp16, ScalarType out_dtype, "
                "bool return_normed, bool return_sum) -> Tensor[]")
 _pq_lib.define("w4a8_linear_group_fused(Tensor x, Tensor? x2, Tensor? norm_weight, float eps, int mode, "
                "Tensor[] rot_idx, Tensor[] rot_cs, Tensor?[] scales, int krot, Tensor[] wpack, Tensor[] wmeta, "
-               "Tensor?[] bias, Tensor? workspace, bool input_fp16, bool materialize_fp16, ScalarType out_dtype, "
+               "Tensor?[] bias, bool input_fp16, bool materialize_fp16, ScalarType out_dtype, "
                "bool return_h, bool return_sum) -> Tensor[]")
 _pq_lib.define("w4a16_prepack(Tensor awq_qweight, Tensor scales, Tensor scaled_zeros) -> (Tensor, Tensor)")
 _pq_lib.define("w4a16_gemm(Tensor x, Tensor wpack, Tensor wmeta, Tensor? bias, ScalarType out_dtype) -> Tensor")
 _pq_lib.define("w4a16_linear_group(Tensor x, Tensor[] rot_idx, Tensor[] rot_cs, Tensor?[] scales, int krot, "
-               "Tensor[] wpack, Tensor[] wmeta, Tensor?[] bias, Tensor? workspace, bool input_fp16, "
+               "Tensor[] wpack, Tensor[] wmeta, Tensor?[] bias, bool input_fp16, "
                "ScalarType out_dtype) -> Tensor[]")
 _pq_lib.define("w4a16_linear(Tensor x, Tensor rot_idx, Tensor rot_cs, Tensor? scales, int krot, Tensor wpack, "
-               "Tensor wmeta, Tensor? bias, Tensor? workspace, bool input_fp16, ScalarType out_dtype) -> Tensor")
+               "Tensor wmeta, Tensor? bias, bool input_fp16, ScalarType out_dtype) -> Tensor")
 
 
 # ---------------------------------------------------------------------------
@@ -163,11 +172,14 @@ def _rotate_args(x, idx_ij, theta, scales):
     return xc, idx_ij.contiguous(), theta.contiguous(), scc, xc.numel() // h, h, krot
 
 
-# Packed operands of rotation::rotate's (pairs, angles, scales), cached per tensor: the register-chain
-# kernel of the fused linear runs whole rows about 1.5x faster than the LDS-tile kernel at large row
-# counts, and gives the same results (both take cos/sin of each angle in float64, rounded once).
-_PACK_CACHE: "OrderedDict" = OrderedDict()
-_PACK_CACHE_MAX = 64
+# Packed operands of rotation::rotate's (pairs, angles, scales), registered by whoever derived them
+# (Rotation.prepare()): the register-chain kernel of the fused linear runs whole rows about 1.5x faster than
+# the LDS-tile kernel at large row counts, and gives the same results (both take cos/sin of each angle in
+# float64, rounded once).  The op itself only looks them up -- it never packs, copies to the host or
+# synchronizes -- and runs the tile kernel, which derives its parameters on the device, when nothing
+# current is registered for its exact tensors.
+_PACK_REGISTRY: "OrderedDict" = OrderedDict()
+_PACK_REGISTRY_MAX = 4096
 _PACKED_MIN_ROWS = 1024
 
 
@@ -175,39 +187,49 @@ def _none_ref():
     return None
 
 
-def _packed_for(idx_ij, theta, scales, group_size):
-    """(rot_idx, rot_cs, scales_f32) on the op's device for these tensors, or None where the packed kernel
-    cannot run them: group 64, K not a multiple of 128 or above 16384, more than 16 layers, pairs that are
-    not perfect matchings, angles that require grad (trained: they change every step), or a first call
-    inside a graph capture (packing reads the pairs and angles on the host)."""
-    krot, h = idx_ij.shape
-    if group_size != 128 or h % 128 or h > 16384 or krot > 16 or theta.requires_grad:
+def tensor_state(t: torch.Tensor | None):
+    """(data pointer, in-place version, device) of t: it changes whenever t is modified in place or replaced.
+    Tensors made under torch.inference_mode() carry no version counter; their pointer and device stand in."""
+    if t is None:
         return None
+    try:
+        ver = t._version
+    except RuntimeError:
+        ver = None
+    return (t.data_ptr(), ver, t.device)
+
+
+def _tensor_state(srcs):
+    return tuple(tensor_state(t) for t in srcs)
+
+
+def register_packed_rotation(idx_ij, theta, scales, rot_idx, rot_cs, scales_f32) -> None:
+    """Records (rot_idx, rot_cs, scales_f32), derived from exactly these (idx_ij, theta, scales) tensors, for
+    rotation::rotate and rotation::rotate_and_quant_mxfp4 on those tensors.  The entry lapses as soon as any of
+    the three tensors is modified in place, freed, or replaced."""
     srcs = (idx_ij, theta, scales)
     key = tuple(id(t) for t in srcs)
-    state = tuple((t.data_ptr(), t._version) if t is not None else None for t in srcs) + (idx_ij.device,)
-    ent = _PACK_CACHE.get(key)
-    if ent is not None:
-        refs, state0, packed = ent
-        if state0 == state and all(r() is t for r, t in zip(refs, srcs)):
-            _PACK_CACHE.move_to_end(key)
-            return packed
-        del _PACK_CACHE[key]
-    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
-        return None
-    th = theta.detach().to("cpu").double()
-    cs = torch.stack([torch.cos(th), torch.sin(th)], dim=-1).float()
-    try:
-        rot_idx, rot_cs = pack_rotation(idx_ij, cs)
-        dev = idx_ij.device
-        sf = scales.detach().reshape(-1).to(dev, torch.float32).contiguous() if scales is not None else None
-        packed = (rot_idx.to(dev), rot_cs.to(dev), sf)
-    except ValueError:
-        packed = None   # not a perfect matching per group and layer: the tile kernel takes it as it is
     refs = tuple(weakref.ref(t) if t is not None else _none_ref for t in srcs)
-    _PACK_CACHE[key] = (refs, state, packed)
-    while len(_PACK_CACHE) > _PACK_CACHE_MAX:
-        _PACK_CACHE.popitem(last=False)
+    _PACK_REGISTRY[key] = (refs, _tensor_state(srcs), (rot_idx, rot_cs, scales_f32))
+    _PACK_REGISTRY.move_to_end(key)
+    while len(_PACK_REGISTRY) > _PACK_REGISTRY_MAX:
+        _PACK_REGISTRY.popitem(last=False)
+
+
+def _packed_for(idx_ij, theta, scales, group_size):
+    """The registered (rot_idx, rot_cs, scales_f32) of these tensors, or None: nothing registered, a stale
+    entry, group 64, or angles that require grad (trained: they change every step)."""
+    if group_size != 128 or theta.requires_grad:
+        return None
+    srcs = (idx_ij, theta, scales)
+    ent = _PACK_REGISTRY.get(tuple(id(t) for t in srcs))
+    if ent is None:
+        return None
+    refs, state, packed = ent
+    if state != _tensor_state(srcs) or not all(r() is t for r, t in zip(refs, srcs)):
+        return None
+    if packed[0].device != idx_ij.device:
+        return None
     return packed
 
 
@@ -265,7 +287,7 @@ _rotation_lib.impl("rotate", _rotate_impl, "CUDA")
 
 @torch.library.register_fake("rotation::rotate")
 def _rotate_fake(x, idx_ij, theta, scales, group_size):
-    return torch.empty_like(x)
+    return x.new_empty(x.shape)
 
 
 _rotation_lib.impl("rotate_and_quant_mxfp4", _rotate_mxfp4_impl, "CUDA")
@@ -276,6 +298,38 @@ def _rotate_mxfp4_fake(x, idx_ij, theta, scales, group_size):
     h = x.size(-1)
     return (x.new_empty((*x.shape[:-1], h // 2), dtype=torch.uint8),
             x.new_empty((*x.shape[:-1], h // 32), dtype=torch.uint8))
+
+
+def _rotate_backward_impl(grad_y, x, idx_ij, theta, scales, group_size):
+    xc, idc, thc, scc, rows, h, krot = _rotate_args(x, idx_ij, theta, scales)
+    _require(grad_y.shape == x.shape and grad_y.dtype == x.dtype,
+             f"grad_y must match x ({tuple(x.shape)}, {x.dtype}), got {tuple(grad_y.shape)}, {grad_y.dtype}")
+    dev = x.device
+    _same_device("grad_y", grad_y, dev)
+    gyc = grad_y.contiguous()
+    gx = torch.empty_like(xc)
+    gth = torch.empty_like(thc)
+    gs = torch.empty_like(scc) if scc is not None else x.new_empty((0,))
+    lib = _lib.load()
+    need = int(lib.pq_rotate_backward_workspace_size(rows, h, krot))
+    ws = torch.empty(need, dtype=torch.uint8, device=dev) if need else None
+    with _DeviceGuard(dev):
+        st = lib.pq_rotate_backward(xc.data_ptr(), gyc.data_ptr(), gx.data_ptr(), gth.data_ptr(),
+                                    gs.data_ptr() if scc is not None else None, idc.data_ptr(), thc.data_ptr(),
+                                    scc.data_ptr() if scc is not None else None, rows, h, krot, int(group_size),
+                                    _DT[x.dtype], ws.data_ptr() if ws is not None else None, need, _stream(dev))
+    _lib.check(st, "paroquant::rotate_backward")
+    return gx.view(x.shape), gth.view(theta.shape), gs.view(scales.shape) if scc is not None else gs
+
+
+_pq_lib.impl("rotate_backward", _rotate_backward_impl, "CUDA")
+
+
+@torch.library.register_fake("paroquant::rotate_backward")
+def _rotate_backward_fake(grad_y, x, idx_ij, theta, scales, group_size):
+    has_scale = scales is not None and scales.numel() > 0
+    return (x.new_empty(x.shape), theta.new_empty(theta.shape),
+            scales.new_empty(scales.shape) if has_scale else x.new_empty((0,)))
 
 
 # ---------------------------------------------------------------------------
@@ -415,7 +469,7 @@ def _check_weights(wpack, wmeta, dev):
     return n, k
 
 
-def _gemm_launch(xq, xs, wpack, wmeta, bias, workspace, out_dtype, m, n, k, dev):
+def _gemm_launch(xq, xs, wpack, wmeta, bias, out_dtype, m, n, k, dev):
     _require(out_dtype in _DT, f"out_dtype must be float32/float16/bfloat16, got {out_dtype}")
     y = torch.empty((m, n), dtype=out_dtype, device=dev)
     if bias is not None:
@@ -425,11 +479,8 @@ def _gemm_launch(xq, xs, wpack, wmeta, bias, workspace, out_dtype, m, n, k, dev)
     need = workspace_bytes(m, n, k)
     ws_ptr, ws_bytes = None, 0
     if need > 0:
-        if workspace is None:
-            workspace = torch.zeros(need, dtype=torch.uint8, device=dev)
-        _same_device("workspace", workspace, dev)
-        _require(workspace.is_contiguous(), "workspace must be contiguous")
-        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+        workspace = torch.zeros(need, dtype=torch.uint8, device=dev)
+        ws_ptr, ws_bytes = workspace.data_ptr(), need
     lib = _lib.load()
     with _DeviceGuard(dev):
         st = lib.pq_w4a8_gemm(xq.data_ptr(), xs.data_ptr(), wpack.data_ptr(), wmeta.data_ptr(),
@@ -440,7 +491,7 @@ def _gemm_launch(xq, xs, wpack, wmeta, bias, workspace, out_dtype, m, n, k, dev)
     return y
 
 
-def _gemm_impl(xq, xscale, wpack, wmeta, bias, workspace, out_dtype):
+def _gemm_impl(xq, xscale, wpack, wmeta, bias, out_dtype):
     dev = xq.device
     n, k = _check_weights(wpack, wmeta, dev)
     _require(xq.dtype == torch.int8 and xq.dim() == 2 and xq.size(1) == k,
@@ -448,14 +499,14 @@ def _gemm_impl(xq, xscale, wpack, wmeta, bias, workspace, out_dtype):
     m = xq.size(0)
     _require(xscale.dtype == torch.float32 and xscale.numel() == m, f"xscale must be float32 [{m}]")
     _same_device("xscale", xscale, dev)
-    return _gemm_launch(xq.contiguous(), xscale.contiguous(), wpack, wmeta, bias, workspace, out_dtype, m, n, k, dev)
+    return _gemm_launch(xq.contiguous(), xscale.contiguous(), wpack, wmeta, bias, out_dtype, m, n, k, dev)
 
 
 _pq_lib.impl("w4a8_gemm", _gemm_impl, "CUDA")
 
 
 @torch.library.register_fake("paroquant::w4a8_gemm")
-def _gemm_fake(xq, xscale, wpack, wmeta, bias, workspace, out_dtype):
+def _gemm_fake(xq, xscale, wpack, wmeta, bias, out_dtype):
     return xq.new_empty((xq.size(0), wpack.size(0) * 16), dtype=out_dtype)
 
 
@@ -515,8 +566,7 @@ def _prepack_fake(awq_qweight, awq_scales, awq_qzeros):
             awq_qweight.new_empty((n // 16, k // 128, 16), dtype=torch.int32))
 
 
-def _linear_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16, materialize_fp16,
-                 out_dtype):
+def _linear_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, input_fp16, materialize_fp16, out_dtype):
     dev = x.device
     n, k = _check_weights(wpack, wmeta, dev)
     _require(x.size(-1) == k, f"x has {x.size(-1)} features, the weights expect {k}")
@@ -531,15 +581,7 @@ def _linear_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace
         bias = bias.contiguous()
     lib = _lib.load()
     need = int(lib.pq_w4a8_linear_workspace_size(m, n, k, krot))
-    scratch = None
-    if need > 0:
-        # a caller's buffer is used when it fits; otherwise scratch comes from the caching allocator
-        if (workspace is not None and workspace.dtype == torch.uint8 and workspace.is_contiguous()
-                and workspace.numel() >= need and workspace.data_ptr() % 256 == 0):
-            _same_device("workspace", workspace, dev)
-            scratch = workspace
-        else:
-            scratch = torch.empty(need, dtype=torch.uint8, device=dev)
+    scratch = torch.empty(need, dtype=torch.uint8, device=dev) if need > 0 else None
     flags = (_lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0) | (_lib.PQ_RQ_MATERIALIZE_FP16 if materialize_fp16 else 0)
     idx, cs = rot_idx.contiguous(), rot_cs.contiguous()
     sc = scales.contiguous() if scales is not None else None
@@ -592,25 +634,21 @@ def _group_members(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, out_dty
     return members, outs, keep, bias_dt, m, k
 
 
-def _group_scratch(workspace, m, k, count, dev):
+def _group_scratch(m, k, count, dev):
+    """Scratch of a group launch from torch's caching allocator (inside a graph capture: the graph's pool,
+    at fixed addresses across replays)."""
     need = int(_lib.load().pq_w4a8_linear_group_workspace_size(m, k, count))
-    if need <= 0:
-        return None
-    if (workspace is not None and workspace.dtype == torch.uint8 and workspace.is_contiguous()
-            and workspace.numel() >= need and workspace.data_ptr() % 256 == 0):
-        _same_device("workspace", workspace, dev)
-        return workspace
-    return torch.empty(need, dtype=torch.uint8, device=dev)
+    return torch.empty(need, dtype=torch.uint8, device=dev) if need > 0 else None
 
 
-def _linear_group_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16,
-                       materialize_fp16, out_dtype):
+def _linear_group_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, input_fp16, materialize_fp16,
+                       out_dtype):
     dev = x.device
     xc = x.contiguous()
     members, outs, keep, bias_dt, m, k = _group_members(xc, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
                                                         out_dtype)
     count = len(outs)
-    scratch = _group_scratch(workspace, m, k, count, dev)
+    scratch = _group_scratch(m, k, count, dev)
     flags = (_lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0) | (_lib.PQ_RQ_MATERIALIZE_FP16 if materialize_fp16 else 0)
     lib = _lib.load()
     with _DeviceGuard(dev):
@@ -622,7 +660,7 @@ def _linear_group_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, wor
 
 
 def _linear_group_fused_impl(x, x2, norm_weight, eps, mode, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
-                             workspace, input_fp16, materialize_fp16, out_dtype, return_h, return_sum):
+                             input_fp16, materialize_fp16, out_dtype, return_h, return_sum):
     dev = x.device
     _require(x.dtype in _DT, f"x must be float32/float16/bfloat16, got {x.dtype}")
     _require(mode in (_lib.PQ_PRO_RMSNORM, _lib.PQ_PRO_ADD, _lib.PQ_PRO_SWIGLU), f"unknown prologue mode {mode}")
@@ -649,7 +687,7 @@ def _linear_group_fused_impl(x, x2, norm_weight, eps, mode, rot_idx, rot_cs, sca
     count = len(outs)
     h = torch.empty_like(xc) if return_h else None
     sm = torch.empty_like(xc) if return_sum else None
-    scratch = _group_scratch(workspace, m, k, count, dev)
+    scratch = _group_scratch(m, k, count, dev)
     flags = (_lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0) | (_lib.PQ_RQ_MATERIALIZE_FP16 if materialize_fp16 else 0)
     lib = _lib.load()
     with _DeviceGuard(dev):
@@ -673,20 +711,20 @@ _pq_lib.impl("w4a8_linear_group_fused", _linear_group_fused_impl, "CUDA")
 
 @torch.library.register_fake("paroquant::w4a8_linear_group_fused")
 def _linear_group_fused_fake(x, x2, norm_weight, eps, mode, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
-                             workspace, input_fp16, materialize_fp16, out_dtype, return_h, return_sum):
+                             input_fp16, materialize_fp16, out_dtype, return_h, return_sum):
     outs = [x.new_empty((*x.shape[:-1], w.size(0) * 16), dtype=out_dtype) for w in wpack]
     if return_h:
-        outs.append(torch.empty_like(x))
+        outs.append(x.new_empty(x.shape))
     if return_sum:
-        outs.append(torch.empty_like(x))
+        outs.append(x.new_empty(x.shape))
     return outs
 
 
 def _linear_group_rmsnorm_impl(x, residual, norm_weight, eps, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
-                               workspace, input_fp16, materialize_fp16, out_dtype, return_normed, return_sum):
+                               input_fp16, materialize_fp16, out_dtype, return_normed, return_sum):
     return _linear_group_fused_impl(x, residual, norm_weight, eps, _lib.PQ_PRO_RMSNORM, rot_idx, rot_cs, scales, krot,
-                                    wpack, wmeta, bias, workspace, input_fp16, materialize_fp16, out_dtype,
-                                    return_normed, return_sum)
+                                    wpack, wmeta, bias, input_fp16, materialize_fp16, out_dtype, return_normed,
+                                    return_sum)
 
 
 _pq_lib.impl("w4a8_linear_group_rmsnorm", _linear_group_rmsnorm_impl, "CUDA")
@@ -694,12 +732,12 @@ _pq_lib.impl("w4a8_linear_group_rmsnorm", _linear_group_rmsnorm_impl, "CUDA")
 
 @torch.library.register_fake("paroquant::w4a8_linear_group_rmsnorm")
 def _linear_group_rmsnorm_fake(x, residual, norm_weight, eps, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
-                               workspace, input_fp16, materialize_fp16, out_dtype, return_normed, return_sum):
+                               input_fp16, materialize_fp16, out_dtype, return_normed, return_sum):
     outs = [x.new_empty((*x.shape[:-1], w.size(0) * 16), dtype=out_dtype) for w in wpack]
     if return_normed:
-        outs.append(torch.empty_like(x))
+        outs.append(x.new_empty(x.shape))
     if return_sum:
-        outs.append(torch.empty_like(x))
+        outs.append(x.new_empty(x.shape))
     return outs
 
 
@@ -707,14 +745,21 @@ _pq_lib.impl("w4a8_linear_group", _linear_group_impl, "CUDA")
 
 
 @torch.library.register_fake("paroquant::w4a8_linear_group")
-def _linear_group_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16,
-                       materialize_fp16, out_dtype):
+def _linear_group_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, input_fp16, materialize_fp16,
+                       out_dtype):
     return [x.new_empty((*x.shape[:-1], w.size(0) * 16), dtype=out_dtype) for w in wpack]
 
 
-def split_path(m: int, k: int) -> bool:
-    """True when the linear entry points run m tokens of k features on the split-rotation kernel pair."""
-    return bool(_lib.load().pq_w4a8_linear_split_path(m, k))
+def split_path(m, k) -> bool:
+    """True when the linear entry points run m tokens of k features on the split-rotation kernels: the rule of
+    pq_w4a8_linear_split_path, restated in Python so that torch.compile can guard on it when m is a symbolic
+    size (tests check the two agree).  Split pair: m * k <= 12288, or k >= 8192 and m <= 4, as long as the
+    GEMM's LDS image of A fits (m <= 16, m * (k + 16) <= 80 KiB); three-launch long rows: otherwise
+    k in [8192, 16384] and m <= 16."""
+    if m < 1 or k % 128 or k > 16384:
+        return False
+    split = (m * k <= 12288 or (k >= 8192 and m <= 4)) and m <= 16 and m * (k + 16) <= 80 * 1024
+    return bool(split or (m <= 16 and k >= 8192))
 
 
 def linear_group_workspace_bytes(m: int, k: int, count: int) -> int:
@@ -723,8 +768,7 @@ def linear_group_workspace_bytes(m: int, k: int, count: int) -> int:
 
 
 @torch.library.register_fake("paroquant::w4a8_linear")
-def _linear_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16, materialize_fp16,
-                 out_dtype):
+def _linear_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, input_fp16, materialize_fp16, out_dtype):
     return x.new_empty((*x.shape[:-1], wpack.size(0) * 16), dtype=out_dtype)
 
 
@@ -803,7 +847,7 @@ def w4a16_linear_workspace_bytes(m: int, k: int) -> int:
     return int(_lib.load().pq_w4a16_linear_workspace_size(m, k))
 
 
-def _w16_linear_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16, out_dtype):
+def _w16_linear_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, input_fp16, out_dtype):
     dev = x.device
     n, k = _check_weights(wpack, wmeta, dev)
     _require(x.size(-1) == k, f"x has {x.size(-1)} features, the weights expect {k}")
@@ -815,14 +859,7 @@ def _w16_linear_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, works
     bias = _w16_bias(bias, n, dev)
     lib = _lib.load()
     need = int(lib.pq_w4a16_linear_workspace_size(m, k))
-    scratch = None
-    if need > 0:
-        if (workspace is not None and workspace.dtype == torch.uint8 and workspace.is_contiguous()
-                and workspace.numel() >= need and workspace.data_ptr() % 256 == 0):
-            _same_device("workspace", workspace, dev)
-            scratch = workspace
-        else:
-            scratch = torch.empty(need, dtype=torch.uint8, device=dev)
+    scratch = torch.empty(need, dtype=torch.uint8, device=dev) if need > 0 else None
     flags = _lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0
     idx, cs = rot_idx.contiguous(), rot_cs.contiguous()
     sc = scales.contiguous() if scales is not None else None
@@ -840,7 +877,7 @@ def _w16_linear_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, works
 _pq_lib.impl("w4a16_linear", _w16_linear_impl, "CUDA")
 
 
-def _w16_linear_group_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16, out_dtype):
+def _w16_linear_group_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, input_fp16, out_dtype):
     """paroquant::w4a16_linear for linears that read the same x, in one rotation launch and (m <= 16) one GEMM."""
     dev = x.device
     _require(x.dtype in _DT, f"x must be float32/float16/bfloat16, got {x.dtype}")
@@ -850,14 +887,7 @@ def _w16_linear_group_impl(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
     count = len(outs)
     lib = _lib.load()
     need = int(lib.pq_w4a16_linear_group_workspace_size(m, k, count))
-    scratch = None
-    if need > 0:
-        if (workspace is not None and workspace.dtype == torch.uint8 and workspace.is_contiguous()
-                and workspace.numel() >= need and workspace.data_ptr() % 256 == 0):
-            _same_device("workspace", workspace, dev)
-            scratch = workspace
-        else:
-            scratch = torch.empty(need, dtype=torch.uint8, device=dev)
+    scratch = torch.empty(need, dtype=torch.uint8, device=dev) if need > 0 else None
     flags = _lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0
     with _DeviceGuard(dev):
         st = lib.pq_w4a16_linear_group(xc.data_ptr(), _DT[x.dtype], members, count, bias_dt, _DT[out_dtype], m, k,
@@ -871,10 +901,10 @@ _pq_lib.impl("w4a16_linear_group", _w16_linear_group_impl, "CUDA")
 
 
 @torch.library.register_fake("paroquant::w4a16_linear_group")
-def _w16_linear_group_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16, out_dtype):
+def _w16_linear_group_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, input_fp16, out_dtype):
     return [x.new_empty((*x.shape[:-1], w.size(0) * 16), dtype=out_dtype) for w in wpack]
 
 
 @torch.library.register_fake("paroquant::w4a16_linear")
-def _w16_linear_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, workspace, input_fp16, out_dtype):
+def _w16_linear_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, input_fp16, out_dtype):
     return x.new_empty((*x.shape[:-1], wpack.size(0) * 16), dtype=out_dtype)

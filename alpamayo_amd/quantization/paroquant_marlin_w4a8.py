@@ -31,8 +31,7 @@ addresses, as in the reference 262-271):
   qweight    uint8 [N/16, K/128, 64, 16]   packed int4 codes
   scales     int32 [N/16, K/128, 16]       fp16 group scale | zero point << 16
   qzeros     empty (zero points live in ``scales``)
-  workspace  uint8                          scratch of paroquant::w4a8_linear for M <= 16
-                                            (int8 codes and scales between its two kernels)
+  workspace  empty uint8 (the ops take their scratch from torch's allocator), kept for API parity
   g_idx, g_idx_sort_indices   empty int32 (no act-order), kept for API parity
   input_global_scale          float32 [1] = 1 (the fp16 scales are used as is)
 """
@@ -50,9 +49,6 @@ from .qmodule import WQLinear, unpack_intweight
 from .rotation_linear import RotateLinearInt4, Rotation
 
 logger = logging.getLogger(__name__)
-
-_WORKSPACE_MAX_M = 16
-
 
 # ---------------------------------------------------------------------------
 # bf16 wrapper
@@ -87,19 +83,29 @@ class BF16RotateLinearWrapper(nn.Module):
             return getattr(self.rotate_linear, name)
 
 
+def _rmsnorm_like_module(s: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """Qwen3VLTextRMSNorm.forward (modeling_qwen3_vl.py:354-359) with torch ops: float32 mean square and
+    rsqrt, the normalized row rounded to s's dtype, then times the weight in that dtype."""
+    sf = s.float()
+    normed = (sf * torch.rsqrt(sf.pow(2).mean(-1, keepdim=True) + eps)).to(s.dtype)
+    return weight.to(s.dtype) * normed
+
+
 class SharedInputRotateLinears(nn.Module):
     """Linears that read the same activation -- q/k/v, or gate/up -- run as one group.
 
     Each member keeps its own rotation and weights; forward(x) returns the
-    members' outputs, equal to calling each member on x.  The group runs
-    paroquant::w4a8_linear_group: one rotation (+ quant) launch for all
-    members and one GEMM launch over their concatenated output columns,
-    where separate calls take two launches per linear.  Members are
-    BF16RotateLinearWrapper or RotateLinearInt4 modules holding a
-    MarlinW4A8Linear, all of one kind, with one in_features and one number
-    of rotation layers.  The reference keeps these linears separate once
-    ParoQuant is loaded (paroquant_marlin_w4a8.py:455-460); its unquantised
-    counterparts are QKVLinear / MergedColumnLinear (patches.py:144-263).
+    members' outputs, equal to calling each member on x.  Members are
+    BF16RotateLinearWrapper or RotateLinearInt4 modules (all of one kind)
+    with one in_features and one number of rotation layers, holding
+    MarlinW4A8Linear weights (W4A8: paroquant::w4a8_linear_group, one
+    rotation + quant launch for all members and one GEMM launch over their
+    concatenated output columns, where separate calls take two launches per
+    linear) or all WQLinear weights (W4A16: paroquant::w4a16_linear_group,
+    one rotation launch and, up to 16 tokens, one GEMM launch).  The reference
+    keeps these linears separate once ParoQuant is loaded
+    (paroquant_marlin_w4a8.py:455-460); its unquantised counterparts are
+    QKVLinear / MergedColumnLinear (patches.py:144-263).
     """
 
     def __init__(self, members):
@@ -111,89 +117,108 @@ class SharedInputRotateLinears(nn.Module):
         if len(kinds) != 1 or not kinds <= {BF16RotateLinearWrapper, RotateLinearInt4}:
             raise TypeError("members must all be BF16RotateLinearWrapper or all RotateLinearInt4")
         rls = [m.rotate_linear if isinstance(m, BF16RotateLinearWrapper) else m for m in members]
-        for rl in rls:
-            if not isinstance(rl.qlinear, MarlinW4A8Linear):
-                raise TypeError("every member must hold a MarlinW4A8Linear (convert_model_to_marlin_w4a8)")
+        weight_kinds = {type(rl.qlinear) for rl in rls}
+        if weight_kinds not in ({MarlinW4A8Linear}, {WQLinear}):
+            raise TypeError("members must all hold MarlinW4A8Linear (convert_model_to_marlin_w4a8) or all WQLinear")
         if len({rl.qlinear.in_features for rl in rls}) != 1 or len({rl.rotation.krot for rl in rls}) != 1:
             raise ValueError("members must share in_features and the number of rotation layers")
         self.members = nn.ModuleList(members)
         self.bf16_inputs = isinstance(members[0], BF16RotateLinearWrapper)
-        self.register_buffer("workspace", torch.empty(0, dtype=torch.uint8), persistent=False)
+        self.w4a16 = weight_kinds == {WQLinear}
 
     def _rotate_linears(self):
         return [m.rotate_linear if self.bf16_inputs else m for m in self.members]
 
     def _args(self, x):
         rls = self._rotate_linears()
-        for rl in rls:
-            rl.qlinear._check_loaded()
-            if not rl.rotation.prepared:
-                rl.rotation.prepare()
-        k = x.size(-1)
-        need = _ops.linear_group_workspace_bytes(x.numel() // k, k, len(rls))
-        if self.workspace.numel() < need or self.workspace.device != x.device:
-            self.workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
-        return ([rl.rotation.rot_idx for rl in rls], [rl.rotation.rot_cs for rl in rls],
-                [rl.rotation.scales_f32 for rl in rls], rls[0].rotation.krot, [rl.qlinear.qweight for rl in rls],
-                [rl.qlinear.scales for rl in rls], [rl.qlinear.bias for rl in rls], self.workspace,
-                self.bf16_inputs, True, x.dtype)
+        if not torch.compiler.is_compiling():
+            # Host-side checks run eagerly only: under torch.compile the members must have been prepared
+            # (prepare(), or one eager call).
+            for rl in rls:
+                if self.w4a16:
+                    if not rl.qlinear.prepared:
+                        rl.qlinear.prepare()
+                else:
+                    rl.qlinear._check_loaded()
+                if not rl.rotation.prepared:
+                    rl.rotation.prepare()
+        rot = ([rl.rotation.rot_idx for rl in rls], [rl.rotation.rot_cs for rl in rls],
+               [rl.rotation.scales_f32 for rl in rls], rls[0].rotation.krot)
+        if self.w4a16:
+            return rot + ([rl.qlinear.w16_pack for rl in rls], [rl.qlinear.w16_meta for rl in rls],
+                          [rl.qlinear.bias for rl in rls], self.bf16_inputs, x.dtype)
+        return rot + ([rl.qlinear.qweight for rl in rls], [rl.qlinear.scales for rl in rls],
+                      [rl.qlinear.bias for rl in rls], self.bf16_inputs, True, x.dtype)
+
+    def _plain(self, x):
+        if self.w4a16:
+            return list(torch.ops.paroquant.w4a16_linear_group(x, *self._args(x)))
+        return list(torch.ops.paroquant.w4a8_linear_group(x, *self._args(x)))
 
     def forward(self, x: torch.Tensor, norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
                 residual: torch.Tensor | None = None, return_normed: bool = False, return_sum: bool = False):
         """The members' outputs on x; with ``norm_weight``, on the decoder layer's RMSNorm of
         x (+ residual): h = weight * (s * rsqrt(mean(s^2) + eps)) with s = x + residual, in x's dtype
         (Qwen3VLTextRMSNorm.forward, modeling_qwen3_vl.py:354-359); with only ``residual``, on
-        s = x + residual (a decoder layer's residual add).  The norm runs inside the group's rotation
-        launch; the add does where the group runs the split rotation (decode sizes), and as a
-        separate torch add otherwise, which measured faster there.  ``return_normed`` /
-        ``return_sum`` append h / s to the outputs."""
-        args = self._args(x)
+        s = x + residual (a decoder layer's residual add).  With W4A8 members the norm runs inside the
+        group's rotation launch, and so does the add where the group runs the split rotation (decode
+        sizes; a separate torch add measured faster otherwise); with W4A16 members both are torch ops.
+        ``return_normed`` / ``return_sum`` append h / s to the outputs."""
+        if return_normed and norm_weight is None:
+            raise ValueError("return_normed needs norm_weight (the add alone returns its sum: return_sum)")
+        if return_sum and residual is None:
+            raise ValueError("return_sum needs a residual")
+        k = x.size(-1)
+        if self.w4a16:
+            s = x + residual if residual is not None else x
+            h = _rmsnorm_like_module(s, norm_weight, eps) if norm_weight is not None else s
+            return tuple(self._plain(h) + ([h] if return_normed else []) + ([s] if return_sum else []))
         if norm_weight is not None:
             outs = torch.ops.paroquant.w4a8_linear_group_fused(x, residual, norm_weight.to(x.dtype), float(eps),
-                                                               _ops._lib.PQ_PRO_RMSNORM, *args, return_normed,
-                                                               return_sum)
+                                                               _ops._lib.PQ_PRO_RMSNORM, *self._args(x),
+                                                               return_normed, return_sum)
         elif residual is not None:
-            if return_normed:
-                raise ValueError("return_normed needs norm_weight (the add alone returns its sum: return_sum)")
-            if _ops.split_path(x.numel() // x.size(-1), x.size(-1)):
+            if _ops.split_path(x.numel() // k, k):
                 outs = torch.ops.paroquant.w4a8_linear_group_fused(x, residual, None, 0.0, _ops._lib.PQ_PRO_ADD,
-                                                                   *args, False, return_sum)
+                                                                   *self._args(x), False, return_sum)
             else:   # the row kernel: a separate add is cheaper (same result bit for bit)
                 s = x + residual
-                outs = list(torch.ops.paroquant.w4a8_linear_group(s, *args)) + ([s] if return_sum else [])
+                outs = self._plain(s) + ([s] if return_sum else [])
         else:
-            if return_normed or return_sum:
-                raise ValueError("return_normed / return_sum need norm_weight or residual")
-            outs = torch.ops.paroquant.w4a8_linear_group(x, *args)
+            outs = self._plain(x)
         return tuple(outs)
 
     def forward_swiglu(self, gate: torch.Tensor, up: torch.Tensor, return_act: bool = False):
         """The members' outputs on act = silu(gate) * up in the inputs' dtype (a gated MLP's down_proj
         input, patches.py:541-548: silu in float32, rounded, times up, rounded), formed inside the
-        group's rotation launch where the group runs the split rotation (decode sizes), by torch's
+        group's rotation launch where W4A8 members run the split rotation (decode sizes), by torch's
         silu and mul otherwise (measured faster there).  ``return_act`` appends act."""
-        args = self._args(gate)
-        if _ops.split_path(gate.numel() // gate.size(-1), gate.size(-1)):
-            outs = torch.ops.paroquant.w4a8_linear_group_fused(gate, up, None, 0.0, _ops._lib.PQ_PRO_SWIGLU, *args,
-                                                               return_act, False)
-        else:   # the row kernel: separate elementwise kernels are cheaper (same rows, up to silu's last bit)
+        k = gate.size(-1)
+        if not self.w4a16 and _ops.split_path(gate.numel() // k, k):
+            outs = torch.ops.paroquant.w4a8_linear_group_fused(gate, up, None, 0.0, _ops._lib.PQ_PRO_SWIGLU,
+                                                               *self._args(gate), return_act, False)
+        else:   # separate elementwise kernels (same rows, up to silu's last bit)
             act = torch.nn.functional.silu(gate) * up
-            outs = list(torch.ops.paroquant.w4a8_linear_group(act, *args)) + ([act] if return_act else [])
+            outs = self._plain(act) + ([act] if return_act else [])
         return tuple(outs)
 
 
 def _get_alpamayo_layers(model, target="vlm"):
-    if target == "expert":
-        return model.expert.layers
-    return model.vlm.model.language_model.layers
+    """The decoder layers whose linears ParoQuant replaces: the language model's (target "vlm") or the action
+    expert's ("expert"), at the module paths of AlpamayoR1 (paroquant_marlin_w4a8.py:74-80)."""
+    root = model.expert if target == "expert" else model.vlm.model.language_model
+    return root.layers
 
 
-def _iter_linears(module, prefix=""):
-    for name, child in module.named_children():
-        full = f"{prefix}.{name}" if prefix else name
-        if isinstance(child, nn.Linear):
-            yield full, module, name, child
-        yield from _iter_linears(child, full)
+def _modules_with_parent(root: nn.Module, kind):
+    """(parent, attribute name, module) for every submodule of `kind` below `root`, collected before any
+    replacement so the caller may swap them in place."""
+    found = []
+    for parent in root.modules():
+        for name, child in parent.named_children():
+            if isinstance(child, kind):
+                found.append((parent, name, child))
+    return found
 
 
 # ---------------------------------------------------------------------------
@@ -206,27 +231,31 @@ def unpack_wqlinear_qweight(qweight: torch.Tensor, out_features: int, in_feature
     return unpack_intweight(qweight, out_features, in_features, interleave, kstride)
 
 
+# AWQ's int32 word c of a row holds the 8 columns 8c .. 8c+7; nibble i (bits 4i .. 4i+3) holds column
+# 8c + _AWQ_ORDER[i].  _AWQ_NIBBLE_OF is the inverse: the nibble that holds column 8c + j.
 _AWQ_ORDER = [0, 2, 4, 6, 1, 3, 5, 7]
+_AWQ_NIBBLE_OF = [_AWQ_ORDER.index(j) for j in range(8)]
+
+
+def _nibble_shifts(device) -> torch.Tensor:
+    return torch.arange(0, 32, 4, dtype=torch.int64, device=device)
 
 
 def pack_awq_int32(values: torch.Tensor) -> torch.Tensor:
-    """[rows, cols] int4 -> [rows, cols/8] int32; nibble i holds column 8c + _AWQ_ORDER[i]."""
+    """[rows, cols] int4 -> [rows, cols/8] int32 in AWQ's nibble order."""
     rows, cols = values.shape
-    assert cols % 8 == 0, f"cols={cols} must be divisible by 8"
-    v = values.to(torch.int32).reshape(rows, cols // 8, 8)
-    packed = torch.zeros(rows, cols // 8, dtype=torch.int32, device=values.device)
-    for i, src in enumerate(_AWQ_ORDER):
-        packed |= (v[:, :, src] & 0xF) << (4 * i)
-    return packed
+    if cols % 8:
+        raise ValueError(f"cols={cols} must be divisible by 8")
+    nib = (values.to(torch.int64) & 0xF).reshape(rows, cols // 8, 8)[:, :, _AWQ_ORDER]
+    word = (nib << _nibble_shifts(values.device)).sum(dim=-1)          # disjoint nibbles: sum == or
+    return torch.where(word >= 2 ** 31, word - 2 ** 32, word).to(torch.int32)
 
 
 def unpack_awq_int32(packed: torch.Tensor, cols: int) -> torch.Tensor:
     """Inverse of pack_awq_int32 -> [rows, cols] int32."""
     rows = packed.shape[0]
-    out = torch.empty(rows, cols // 8, 8, dtype=torch.int32, device=packed.device)
-    for i, dst in enumerate(_AWQ_ORDER):
-        out[:, :, dst] = (packed >> (4 * i)) & 0xF
-    return out.reshape(rows, cols)
+    nib = (packed.to(torch.int64).unsqueeze(-1) >> _nibble_shifts(packed.device)) & 0xF
+    return nib[:, :, _AWQ_NIBBLE_OF].reshape(rows, cols).to(torch.int32)
 
 
 class AWQBuffers(NamedTuple):
@@ -238,34 +267,42 @@ class AWQBuffers(NamedTuple):
 
 
 def wqlinear_to_awq(qweight_i16, scales, scaled_zeros, out_features, in_features, group_size) -> AWQBuffers:
-    """WQLinear buffers -> AWQ buffers; zeros recovered as round(-scaled_zeros / scales) in [0, 15]."""
-    N, K = out_features, in_features
-    G = K // group_size
-    int4 = unpack_wqlinear_qweight(qweight_i16, N, K)
-    awq_qweight = pack_awq_int32(int4.t().contiguous())
-    awq_scales = scales[:G, :N].contiguous().to(torch.float16)
-    safe = awq_scales.float().clone()
-    safe[safe.abs() < 1e-10] = 1.0
-    zeros = (-scaled_zeros[:G, :N].float() / safe).round().clamp(0, 15).to(torch.int32)
-    return AWQBuffers(awq_qweight, awq_scales, pack_awq_int32(zeros), int4, zeros)
+    """WQLinear buffers -> AWQ buffers (paroquant_marlin_w4a8.py:179-209).
+
+    WQLinear keeps the zero point only as scaled_zeros = -(s * z) in fp16 (qmodule.py:199-203); the integer
+    zero point comes back as round(-scaled_zeros / s), clamped to the 4-bit range, with a zero scale (an
+    unused group) read as 1.  Only the first K / group_size rows of WQLinear's padded scale buffers are used.
+    """
+    n_groups = in_features // group_size
+    codes = unpack_wqlinear_qweight(qweight_i16, out_features, in_features)             # [N, K]
+    s16 = scales[:n_groups, :out_features].to(torch.float16).contiguous()
+    s32 = s16.float()
+    denom = torch.where(s32.abs() < 1e-10, torch.ones_like(s32), s32)
+    zeros = torch.clamp(torch.round(-scaled_zeros[:n_groups, :out_features].float() / denom), 0, 15)
+    zeros = zeros.to(torch.int32)
+    return AWQBuffers(qweight=pack_awq_int32(codes.t().contiguous()), scales=s16, qzeros=pack_awq_int32(zeros),
+                      int4_values=codes, zeros=zeros)
+
+
+def _per_group(t: torch.Tensor, n_out: int, n_groups: int) -> torch.Tensor:
+    """[groups(+padding), N] -> float32 [N, groups, 1], to broadcast over a group's channels."""
+    return t[:n_groups, :n_out].float().t().unsqueeze(-1)
 
 
 def dequant_wqlinear(int4_NK, scales, scaled_zeros, group_size):
-    """w = q * s + sz."""
+    """WQLinear's weights w = q * s + sz in float32, [N, K] (paroquant_marlin_w4a8.py:216-224)."""
     N, K = int4_NK.shape
     G = K // group_size
-    sc = scales[:G, :N].float().repeat_interleave(group_size, dim=0).t()
-    sz = scaled_zeros[:G, :N].float().repeat_interleave(group_size, dim=0).t()
-    return int4_NK.float() * sc + sz
+    q = int4_NK.float().reshape(N, G, group_size)
+    return (q * _per_group(scales, N, G) + _per_group(scaled_zeros, N, G)).reshape(N, K)
 
 
 def dequant_awq(int4_NK, zeros, scales, group_size):
-    """w = (q - z) * s."""
+    """AWQ's weights w = (q - z) * s in float32, [N, K] (paroquant_marlin_w4a8.py:227-235)."""
     N, K = int4_NK.shape
     G = K // group_size
-    sc = scales[:G, :N].float().repeat_interleave(group_size, dim=0).t()
-    zp = zeros[:G, :N].float().repeat_interleave(group_size, dim=0).t()
-    return (int4_NK.float() - zp) * sc
+    q = int4_NK.float().reshape(N, G, group_size)
+    return ((q - _per_group(zeros, N, G)) * _per_group(scales, N, G)).reshape(N, K)
 
 
 # ---------------------------------------------------------------------------
@@ -311,9 +348,7 @@ class MarlinW4A8Linear(nn.Module):
         self.g_idx = torch.empty(0, dtype=torch.int32, device=dev)
         self.g_idx_sort_indices = torch.empty(0, dtype=torch.int32, device=dev)
         self.input_global_scale = torch.ones(1, dtype=torch.float32, device=dev)
-        ws = max(max(_ops.workspace_bytes(m, N, K), _ops.linear_workspace_bytes(m, N, K, 16))
-                 for m in range(1, _WORKSPACE_MAX_M + 1))
-        self.workspace = torch.zeros(max(ws, 1), dtype=torch.uint8, device=dev)
+        self.workspace = torch.empty(0, dtype=torch.uint8, device=dev)
         self.bias = bias.to(dev).contiguous() if bias is not None else None
 
     def _check_loaded(self):
@@ -323,115 +358,171 @@ class MarlinW4A8Linear(nn.Module):
     @torch.no_grad()
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """x: already-rotated activations [..., K]; returns x.dtype [..., N]."""
-        self._check_loaded()
+        if not torch.compiler.is_compiling():
+            self._check_loaded()
         shape = x.shape
         xq, xs = torch.ops.paroquant.quant_i8(x.reshape(-1, shape[-1]))
-        y = torch.ops.paroquant.w4a8_gemm(xq, xs, self.qweight, self.scales, self.bias, self.workspace, x.dtype)
+        y = torch.ops.paroquant.w4a8_gemm(xq, xs, self.qweight, self.scales, self.bias, x.dtype)
         return y.view(*shape[:-1], self.out_features)
 
     @torch.no_grad()
     def forward_rotated(self, x: torch.Tensor, rotation: Rotation, input_fp16: bool, out_dtype: torch.dtype,
                         materialize_fp16: bool = True) -> torch.Tensor:
-        """Rotation + int8 quant + GEMM on un-rotated activations x [..., K]."""
-        self._check_loaded()
-        if not rotation.prepared:
-            rotation.prepare()
+        """Rotation + int8 quant + GEMM on un-rotated activations x [..., K].  Eagerly it checks that the
+        weights are loaded and (re)prepares the rotation's operands when they are stale; under torch.compile
+        it expects a prepared rotation (prepare(), or one eager call)."""
+        if not torch.compiler.is_compiling():
+            self._check_loaded()
+            if not rotation.prepared:
+                rotation.prepare()
         return torch.ops.paroquant.w4a8_linear(
             x, rotation.rot_idx, rotation.rot_cs, rotation.scales_f32, rotation.krot, self.qweight, self.scales,
-            self.bias, self.workspace, input_fp16, materialize_fp16, out_dtype)
+            self.bias, input_fp16, materialize_fp16, out_dtype)
 
     def extra_repr(self) -> str:
         return f"in_features={self.in_features}, out_features={self.out_features}, group_size={self.group_size}"
 
 
 # ---------------------------------------------------------------------------
-# converters
+# converters and checkpoint loading
 # ---------------------------------------------------------------------------
 
 def convert_wqlinear_layer(qweight_i16, scales, scaled_zeros, out_features, in_features, group_size, bias=None,
                            device="cuda"):
-    """WQLinear buffers -> (MarlinW4A8Linear on `device`, AWQBuffers)."""
+    """One WQLinear's buffers -> (a loaded MarlinW4A8Linear on `device`, the intermediate AWQBuffers)
+    (paroquant_marlin_w4a8.py:340-353)."""
     awq = wqlinear_to_awq(qweight_i16, scales, scaled_zeros, out_features, in_features, group_size)
-    mod = MarlinW4A8Linear(in_features, out_features, group_size)
-    mod.load_from_awq(awq.qweight.to(device), awq.scales.to(device), awq.qzeros.to(device),
-                      bias=bias.to(device) if bias is not None else None)
-    return mod, awq
+    layer = MarlinW4A8Linear(in_features, out_features, group_size)
+    on_dev = [t.to(device) for t in (awq.qweight, awq.scales, awq.qzeros)]
+    layer.load_from_awq(*on_dev, bias=None if bias is None else bias.to(device))
+    return layer, awq
 
 
 def _wrap_rotate_linears(model, target="vlm"):
+    """Put every RotateLinearInt4 of the target layers behind a BF16RotateLinearWrapper (bf16 model,
+    fp16 kernels; paroquant_marlin_w4a8.py:356-363)."""
     for layer in _get_alpamayo_layers(model, target):
-        for _, child in layer.named_children():
-            for sub_name, sub_child in child.named_children():
-                if isinstance(sub_child, RotateLinearInt4):
-                    setattr(child, sub_name, BF16RotateLinearWrapper(sub_child))
+        for parent, name, rl in _modules_with_parent(layer, RotateLinearInt4):
+            if not isinstance(parent, BF16RotateLinearWrapper):
+                setattr(parent, name, BF16RotateLinearWrapper(rl))
 
 
 def replace_linears_with_rotate_linear(model, target="vlm", init_only: bool = True,
                                        ignore_suffix: tuple[str, ...] = ("lm_head",)):
-    """Replace every nn.Linear of the target layers by an empty RotateLinearInt4 shell."""
+    """Swap each nn.Linear of the target layers (except those named in ignore_suffix) for an empty fp16
+    RotateLinearInt4 of the same shape, to be filled by load_state_dict (paroquant_marlin_w4a8.py:366-387)."""
     for layer in _get_alpamayo_layers(model, target):
-        for _, parent, child_name, linear in list(_iter_linears(layer)):
-            if child_name in ignore_suffix:
+        for parent, name, lin in _modules_with_parent(layer, nn.Linear):
+            if name in ignore_suffix:
                 continue
-            setattr(parent, child_name, RotateLinearInt4(
-                in_feat=linear.in_features, out_feat=linear.out_features, bias=linear.bias is not None,
-                dtype=torch.float16))
+            shell = RotateLinearInt4(in_feat=lin.in_features, out_feat=lin.out_features, bias=lin.bias is not None,
+                                     dtype=torch.float16)
+            setattr(parent, name, shell)
+
+
+# An fp16 rotation multiplies activations (typically |x| < 100) by the channel scale: above this bound the
+# product can leave the fp16 range (65504) and turn into inf, then NaN.
+_FP16_SAFE_SCALE = 65504.0 / 128.0
 
 
 def _sanitise_channel_scales(model):
-    """Clamp inf/NaN/|s| > 65504/128 channel scales (fp16 overflow guard)."""
-    safe_max = 65504.0 / 128.0
-    n_fixed = 0
-    for name, mod in model.named_modules():
-        if not isinstance(mod, RotateLinearInt4):
+    """Clip every RotateLinearInt4's channel scales to +-65504/128 in place (inf included) and report the
+    modules touched (paroquant_marlin_w4a8.py:390-423).  As in the reference, the clip leaves NaN entries
+    NaN; they are reported separately because no clip can repair them.  Returns the number of modules whose
+    scales were out of range."""
+    touched = 0
+    for name, rl in model.named_modules():
+        if not isinstance(rl, RotateLinearInt4):
             continue
-        cs = mod.rotation.channel_scales
-        bad = torch.isinf(cs) | torch.isnan(cs) | (cs.abs() > safe_max)
-        n_bad = int(bad.sum().item())
-        if n_bad:
-            with torch.no_grad():
-                cs.clamp_(-safe_max, safe_max)   # like the reference, NaN entries stay NaN
-            n_fixed += 1
-            logger.warning("  Clamped %d/%d channel_scales in %s (had INF/NaN/overflow values)", n_bad,
-                           cs.numel(), name)
-    if n_fixed:
-        logger.warning("Sanitised channel_scales in %d RotateLinearInt4 modules", n_fixed)
-    return n_fixed
+        cs = rl.rotation.channel_scales
+        nan = torch.isnan(cs)
+        out_of_range = torch.isinf(cs) | (cs.abs() > _FP16_SAFE_SCALE)
+        n_nan, n_big = int(nan.sum()), int(out_of_range.sum())
+        if n_nan + n_big == 0:
+            continue
+        touched += 1
+        with torch.no_grad():
+            cs.clamp_(min=-_FP16_SAFE_SCALE, max=_FP16_SAFE_SCALE)
+        logger.warning("%s: %d of %d channel scales beyond +-%.0f (or infinite) clipped; %d NaN left as they are",
+                       name, n_big, cs.numel(), _FP16_SAFE_SCALE, n_nan)
+    if touched:
+        logger.warning("channel scales clipped in %d RotateLinearInt4 module(s)", touched)
+    else:
+        logger.info("channel scales: every value within the fp16-safe range")
+    return touched
+
+
+class LoadReport(NamedTuple):
+    """What load_paroquant_checkpoint found (the reference logs the same diagnostics,
+    paroquant_marlin_w4a8.py:466-502)."""
+    missing: list            # model keys the checkpoint lacks
+    unexpected: list         # checkpoint keys the model lacks
+    quant_missing: list      # missing keys of quantized modules (rotation / qlinear buffers)
+    zero_scales: list        # names of non-empty "scales" tensors that are all zero after loading
+    sanitised: int           # modules whose channel scales were clipped
+
+
+_QUANT_KEY_PARTS = ("qlinear", "rotation", "qweight", "scales", "scaled_zeros")
+
+
+def _all_zero_scale_tensors(model) -> list:
+    """Names of non-empty parameters or buffers with "scales" in their name that hold only zeros: a
+    quantized layer whose checkpoint entries did not load (its outputs would be all zero)."""
+    named = list(model.named_parameters()) + list(model.named_buffers())
+    return [n for n, t in named if "scales" in n and t.numel() > 0 and not bool(t.detach().ne(0).any())]
 
 
 def load_paroquant_checkpoint(model, paro_checkpoint, *, target="vlm", device="cuda", wrap_bf16=True):
-    """Put a ParoQuant state dict into an already-built model (load_paroquant_model 462-510)."""
+    """Load a ParoQuant state dict into an already-built model: the checkpoint half of the reference's
+    load_paroquant_model (paroquant_marlin_w4a8.py:426-510), whose first half builds the AlpamayoR1 model.
+
+    Replaces the target layers' linears by RotateLinearInt4 shells, reads the state dict
+    (``torch.load(..., weights_only=True)`` for a path; a dict is used as is), loads it non-strictly, reports
+    key overlap, missing and unexpected keys and quantized layers whose scales stayed all zero, clips
+    out-of-range channel scales, wraps the shells for bf16 activations, and moves the model to `device` in
+    eval mode.  Returns (model, LoadReport).
+    """
     replace_linears_with_rotate_linear(model, target=target, init_only=True)
-    sd = torch.load(paro_checkpoint, map_location="cpu", weights_only=True) if isinstance(paro_checkpoint, str) \
-        else paro_checkpoint
-    missing, unexpected = model.load_state_dict(sd, strict=False)
-    quant_missing = [k for k in missing if any(s in k for s in ("qlinear", "rotation", "qweight", "scales",
-                                                               "scaled_zeros"))]
+    if isinstance(paro_checkpoint, (str, bytes)) or hasattr(paro_checkpoint, "__fspath__"):
+        state = torch.load(paro_checkpoint, map_location="cpu", weights_only=True)
+    else:
+        state = paro_checkpoint
+    have, given = set(model.state_dict()), set(state)
+    logger.info("ParoQuant checkpoint: %d tensors, model: %d, shared: %d", len(given), len(have), len(have & given))
+    missing, unexpected = model.load_state_dict(state, strict=False)
+    quant_missing = [k for k in missing if any(part in k for part in _QUANT_KEY_PARTS)]
     if quant_missing:
-        logger.warning("CRITICAL quant missing: %s", quant_missing[:10])
+        logger.warning("%d missing keys, %d of them quantization buffers, e.g. %s", len(missing),
+                       len(quant_missing), quant_missing[:10])
+    elif missing:
+        logger.info("%d missing keys (no quantization buffer among them), e.g. %s", len(missing), missing[:5])
     if unexpected:
-        logger.warning("Unexpected keys (%d): %s", len(unexpected), unexpected[:20])
-    _sanitise_channel_scales(model)
+        logger.warning("%d checkpoint keys the model does not have, e.g. %s", len(unexpected), unexpected[:20])
+    del state
+    zero = _all_zero_scale_tensors(model)
+    if zero:
+        logger.error("%d quantized scale tensors are all zero after loading (checkpoint keys probably do not "
+                     "match the model), e.g. %s", len(zero), zero[:3])
+    else:
+        logger.info("every quantized scale tensor holds non-zero values")
+    fixed = _sanitise_channel_scales(model)
     if wrap_bf16:
         _wrap_rotate_linears(model, target=target)
     model.to(device)
     model.eval()
-    return model, missing, unexpected
+    return model, LoadReport(list(missing), list(unexpected), quant_missing, zero, fixed)
 
 
 def convert_model_to_marlin_w4a8(model):
-    """Replace the WQLinear of every RotateLinearInt4 by a MarlinW4A8Linear; returns the count."""
-    n = 0
-    for _, mod in model.named_modules():
-        if not isinstance(mod, RotateLinearInt4):
-            continue
-        wq = mod.qlinear
-        if not isinstance(wq, WQLinear):
-            continue
-        marlin, _ = convert_wqlinear_layer(wq.qweight.data, wq.scales.data, wq.scaled_zeros.data, wq.out_features,
-                                           wq.in_features, wq.group_size, bias=wq.bias, device=wq.qweight.device)
-        mod.qlinear = marlin
-        mod.rotation.prepare()
-        n += 1
-    logger.info("Converted %d WQLinear -> MarlinW4A8Linear", n)
-    return n
+    """Give every RotateLinearInt4 that holds a WQLinear a MarlinW4A8Linear with the same weights, on the
+    WQLinear's device, and derive its rotation's packed operands; returns how many were converted
+    (paroquant_marlin_w4a8.py:513-529)."""
+    todo = [rl for rl in model.modules() if isinstance(rl, RotateLinearInt4) and isinstance(rl.qlinear, WQLinear)]
+    for rl in todo:
+        wq = rl.qlinear
+        rl.qlinear, _ = convert_wqlinear_layer(wq.qweight.data, wq.scales.data, wq.scaled_zeros.data,
+                                               wq.out_features, wq.in_features, wq.group_size, bias=wq.bias,
+                                               device=wq.qweight.device)
+        rl.rotation.prepare()
+    logger.info("%d RotateLinearInt4 layer(s) now run the W4A8 kernels", len(todo))
+    return len(todo)

@@ -137,7 +137,9 @@ class WQLinear(nn.Module):
         return q
 
     def _w16_source(self):
-        return tuple((t.data_ptr(), t._version, t.device) for t in (self.qweight, self.scales, self.scaled_zeros))
+        from ..ops import tensor_state
+
+        return tuple(tensor_state(t) for t in (self.qweight, self.scales, self.scaled_zeros))
 
     @property
     def prepared(self) -> bool:
@@ -161,7 +163,7 @@ class WQLinear(nn.Module):
     @torch.no_grad()
     def forward(self, inputs):
         """inputs: fp16 [..., K] -> fp16 [..., N] (qmodule.py:207-232)."""
-        if not self.prepared:
+        if not torch.compiler.is_compiling() and not self.prepared:
             self.prepare()
         return torch.ops.paroquant.w4a16_gemm(inputs, self.w16_pack, self.w16_meta, self.bias, inputs.dtype)
 

@@ -72,14 +72,17 @@ class Rotation(nn.Module):
         self.register_buffer("rot_cs", torch.empty(0, dtype=torch.float32), persistent=False)
         self.register_buffer("scales_f32", torch.empty(0, dtype=torch.float32), persistent=False)
         self.group_size = group_size
+        self._prep_src = None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return torch.ops.rotation.rotate(x, self.pairs, self.theta, self.channel_scales, 128)
 
     @torch.no_grad()
     def prepare(self) -> None:
-        """(Re)derive the fused kernel's operands from theta/pairs/channel_scales."""
-        from ..ops import pack_rotation
+        """(Re)derive the fused kernel's operands from theta/pairs/channel_scales (host work: call it before
+        graph capture; the forward paths call it when ``prepared`` is False) and register them for
+        rotation::rotate on these buffers."""
+        from ..ops import pack_rotation, register_packed_rotation
 
         dev = self.theta.device
         check_rotation_pairs(self.pairs, self.group_size)
@@ -87,6 +90,14 @@ class Rotation(nn.Module):
         self.rot_idx = rot_idx.to(dev)
         self.rot_cs = rot_cs.to(dev)
         self.scales_f32 = self.channel_scales.detach().reshape(-1).to(dev, torch.float32).contiguous()
+        self._prep_src = self._param_source()
+        register_packed_rotation(self.pairs, self.theta, self.channel_scales, self.rot_idx, self.rot_cs,
+                                 self.scales_f32)
+
+    def _param_source(self):
+        from ..ops import tensor_state
+
+        return tuple(tensor_state(t) for t in (self.theta, self.pairs, self.channel_scales))
 
     def cos_sin_table(self) -> torch.Tensor:
         """float32 [KROT, K/2, 2] (cos, sin) of theta, evaluated in float64 on the host."""
@@ -99,7 +110,9 @@ class Rotation(nn.Module):
 
     @property
     def prepared(self) -> bool:
-        return self.rot_cs.numel() > 0 and self.rot_cs.device == self.theta.device
+        """True while the packed operands were derived from the current theta / pairs / channel_scales:
+        False again after load_state_dict, an in-place update or a move of any of them."""
+        return self.rot_cs.numel() > 0 and self._prep_src == self._param_source()
 
 
 class RotateLinearInt4(nn.Module):
@@ -144,12 +157,13 @@ class RotateLinearInt4(nn.Module):
         if isinstance(self.qlinear, WQLinear):
             # rotation (fp16 result) -> W4A16 GEMM behind one entry point.
             q, rot = self.qlinear, self.rotation
-            if not q.prepared:
-                q.prepare()
-            if not rot.prepared:
-                rot.prepare()
+            if not torch.compiler.is_compiling():
+                if not q.prepared:
+                    q.prepare()
+                if not rot.prepared:
+                    rot.prepare()
             return torch.ops.paroquant.w4a16_linear(x, rot.rot_idx, rot.rot_cs, rot.scales_f32, rot.krot, q.w16_pack,
-                                                    q.w16_meta, q.bias, None, False, x.dtype)
+                                                    q.w16_meta, q.bias, False, x.dtype)
         x = self.rotation(x)
         return self.qlinear(x)
 

@@ -247,11 +247,11 @@ def main() -> int:
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         for q, xq, xs in gemm_launches:
-            torch.ops.paroquant.w4a8_gemm(xq, xs, q.qweight, q.scales, None, q.workspace, torch.bfloat16)
+            torch.ops.paroquant.w4a8_gemm(xq, xs, q.qweight, q.scales, None, torch.bfloat16)
     torch.cuda.current_stream().wait_stream(s)
     with torch.cuda.graph(gg):
         for q, xq, xs in gemm_launches:
-            torch.ops.paroquant.w4a8_gemm(xq, xs, q.qweight, q.scales, None, q.workspace, torch.bfloat16)
+            torch.ops.paroquant.w4a8_gemm(xq, xs, q.qweight, q.scales, None, torch.bfloat16)
     gemm_ms = time_graphs([gg], max(10, args.steps // 10), 3)
     gemm_bytes = sum(gemm_kernel_bytes(1, q.out_features, q.in_features) for q, _, _ in gemm_launches)
     achieved = gemm_bytes / (gemm_ms * 1e-3) / 1e9
@@ -287,7 +287,7 @@ def main() -> int:
         with torch.cuda.graph(gg):
             for m, (q8, s8) in zip(L, xq):
                 q = m.rotate_linear.qlinear
-                torch.ops.paroquant.w4a8_gemm(q8, s8, q.qweight, q.scales, None, q.workspace, torch.bfloat16)
+                torch.ops.paroquant.w4a8_gemm(q8, s8, q.qweight, q.scales, None, torch.bfloat16)
         gms = time_graphs([gg], args.prefill_steps, 3)
         gtops = ops / (gms * 1e-3) / 1e12
         # each shape's GEMM alone (q, k, gate, down; o, v, up repeat a shape)
@@ -298,7 +298,7 @@ def main() -> int:
             q8, s8 = xq[idx]
             g1 = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g1):
-                torch.ops.paroquant.w4a8_gemm(q8, s8, q.qweight, q.scales, None, q.workspace, torch.bfloat16)
+                torch.ops.paroquant.w4a8_gemm(q8, s8, q.qweight, q.scales, None, torch.bfloat16)
             sms = time_graphs([g1], args.prefill_steps, 3)
             sops = 2 * M * q.out_features * q.in_features
             per_shape[f"{q.out_features}x{q.in_features}"] = {
@@ -442,7 +442,7 @@ def main() -> int:
             rs = [m[0] for m in members]
             return torch.ops.paroquant.w4a16_linear_group(
                 x, [r.rot_idx for r in rs], [r.rot_cs for r in rs], [r.scales_f32 for r in rs], rs[0].krot,
-                [m[1] for m in members], [m[2] for m in members], [None] * len(members), None, False, f16)
+                [m[1] for m in members], [m[2] for m in members], [None] * len(members), False, f16)
 
         def run16(li, X, gemm_only=False, grouped=False):
             xa, xo, xm, xd = X
@@ -456,7 +456,7 @@ def main() -> int:
                     outs.append(torch.ops.paroquant.w4a16_gemm(x, wp, wm16, None, f16))
                 else:
                     outs.append(torch.ops.paroquant.w4a16_linear(x, rot.rot_idx, rot.rot_cs, rot.scales_f32,
-                                                                 rot.krot, wp, wm16, None, None, False, f16))
+                                                                 rot.krot, wp, wm16, None, False, f16))
             return outs
 
         def capture16(xs, gemm_only, layers, grouped=False):
@@ -534,12 +534,17 @@ def main() -> int:
         K = 4096
         g = workloads.generator(6300, device=dev)
         pairs, theta, cs = workloads.rotation_params(K, g, device=dev)
-        th16, cs16 = theta.to(torch.bfloat16), cs.to(torch.bfloat16)
+        from alpamayo_amd.quantization import Rotation
+        # a prepared Rotation (bf16 buffers): the ops find its packed operands, as Rotation.forward's call does
+        rot = Rotation(K, rotation_angles=theta.to(torch.bfloat16), rotation_pairs=pairs,
+                       channel_scales=cs.to(torch.bfloat16)).to(dev)
+        rot.prepare()
         for M in (16, 3072):
             xm = workloads.activations(M, K, g, device=dev)
             res = {}
-            for name, fn in (("mxfp4", lambda: torch.ops.rotation.rotate_and_quant_mxfp4(xm, pairs, th16, cs16, 128)),
-                             ("rotate", lambda: torch.ops.rotation.rotate(xm, pairs, th16, cs16, 128))):
+            for name, fn in (("mxfp4", lambda: torch.ops.rotation.rotate_and_quant_mxfp4(
+                                 xm, rot.pairs, rot.theta, rot.channel_scales, 128)),
+                             ("rotate", lambda: rot(xm))):
                 fn()
                 gr = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(gr):

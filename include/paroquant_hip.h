@@ -29,6 +29,8 @@
  *                        rotation::rotate -> MarlinW4A8Linear.forward
  *                        (paroquant_marlin_w4a8.py:59-65, 314-333;
  *                        rotation_linear.py:120-124)
+ *   pq_rotate_backward   RotateTensorFunc.backward
+ *                        kernels/paroquant_kernels/interface.py:30-93
  *   pq_rotate_mxfp4      rotation::rotate_and_quant (rotation.cu:62-111),
  *                        in the OCP MXFP4 format instead of NVFP4
  *   pq_w4a16_gemm        torch.ops.awq.gemv / torch.ops.awq.gemm behind
@@ -84,6 +86,28 @@ const char* pq_last_error(void);
 int pq_rotate(const void* x, void* y, const int16_t* idx_ij, const void* theta,
               const void* scales, int64_t rows, int64_t h, int krot, int group_size,
               int dtype, void* stream);
+
+/* Bytes of workspace pq_rotate_backward needs: per-workgroup partial sums,
+ * min(ceil(rows / 16), 64) * (krot * h/2 + h) * 4 bytes (0 for rows = 0). */
+size_t pq_rotate_backward_workspace_size(int64_t rows, int64_t h, int krot);
+
+/* Gradients of pq_rotate's y = R_{krot-1} ... R_0 (scales * x) given grad_y:
+ * grad_x [rows, h], grad_theta [krot, h/2] (summed over rows) and, when
+ * scales is not NULL, grad_scales [h] (summed over rows), all of `dtype`
+ * like x, grad_y, theta and scales; arguments and rules as for pq_rotate.
+ * The layers are recomputed from x in float32 (each layer's outputs kept),
+ * then walked backwards: the angle gradient of a pair is
+ * sum_rows g_a' * b' - g_b' * a' at the layer's outputs (a', b') and
+ * gradients (g_a', g_b'), and the gradient passes through the transposed
+ * rotation; grad_x = scales * g_t and grad_scales = sum_rows x * g_t at
+ * t = scales * x.  Sums are float32 in a fixed order (deterministic).
+ * workspace: pq_rotate_backward_workspace_size bytes, 16-byte aligned.
+ * Reference: RotateTensorFunc.backward (kernels/paroquant_kernels/
+ * interface.py:30-93), which gives the same gradients by inverting y one
+ * layer at a time with rotation::rotate. */
+int pq_rotate_backward(const void* x, const void* grad_y, void* grad_x, void* grad_theta, void* grad_scales,
+                       const int16_t* idx_ij, const void* theta, const void* scales, int64_t rows, int64_t h,
+                       int krot, int group_size, int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Fused rotation + OCP MXFP4 quantization: the rotation of pq_rotate (same
  * arguments and rules), then, per row and per block of 32 channels of the

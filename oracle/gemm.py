@@ -8,9 +8,10 @@ AWQ weight semantics ``w = (q - z) * s`` (dequant_awq, 227-235):
   P[m, g, n] = sum_{k in group g} (q[n, k] - z[g, n]) * xq[m, k]      (int32)
   y[m, n]    = xscale[m] * sum_g s[g, n] * P[m, g, n]  (+ bias[n])
 
-Every partial is an integer of magnitude <= 128*15*128 < 2^24, so a float64
-(or even float32) matmul over one group is exact regardless of summation
-order; the oracle uses float64.
+Every partial is an integer of magnitude <= 128*15*127 < 2^24, so a float32
+matmul over one group is exact regardless of summation order (every
+intermediate sum is an integer below 2^24); the partials are exact, and the
+epilogue runs in float64.
 
 Marlin additionally recodes the fp16 group scales as int16 plus a global
 factor (marlin_act_int8_process_scales, paroquant_marlin_w4a8.py:296-302);
@@ -61,14 +62,13 @@ def w4a8_linear(xq: np.ndarray, xscale: np.ndarray, codes_nk: np.ndarray, scales
     N = codes_nk.shape[0]
     G = K // group_size
     s = np.asarray(scales_gn).astype(np.float64)
-    z = np.asarray(zeros_gn).astype(np.float64)
-    xf = xq.astype(np.float64)
-    qf = np.asarray(codes_nk).astype(np.float64)
+    z = np.asarray(zeros_gn).astype(np.float32)
+    xf = xq.astype(np.float32)
+    w = np.asarray(codes_nk).astype(np.float32).reshape(N, G, group_size) - z.T[:, :, None]   # q - z, exact
     acc = np.zeros((M, N), dtype=np.float64)
     for g in range(G):
-        ks = slice(g * group_size, (g + 1) * group_size)
-        P = xf[:, ks] @ (qf[:, ks] - z[g][:, None]).T          # exact integers
-        acc += P * s[g][None, :]
+        P = xf[:, g * group_size:(g + 1) * group_size] @ w[:, g, :].T      # exact integers (< 2^24)
+        acc += P.astype(np.float64) * s[g][None, :]
     y = acc * np.asarray(xscale, np.float64)[:, None]
     if bias is not None:
         y = y + np.asarray(bias, np.float64)[None, :]

@@ -180,3 +180,46 @@ def rotate_f32_packed(xs: np.ndarray, rot_idx: np.ndarray, rot_cs: np.ndarray, k
     y[:, gi, Af] = a
     y[:, gi, Bf] = b
     return y.reshape(rows, G * 128)
+
+
+def rotate_backward(x: np.ndarray, pairs: np.ndarray, theta: np.ndarray, scales: np.ndarray | None,
+                    grad_y: np.ndarray, group_size: int):
+    """Gradients of y = R_{K-1} ... R_0 (s * x) with respect to x, theta and s, in float64.
+
+    Layer r maps a pair (a, b) to (a', b') = (c a + s b, c b - s a), so
+    d(a', b')/d theta = (b', -a'): the angle's gradient is
+    sum_rows (g_a' b' - g_b' a'), with (g_a', g_b') the gradient at the layer's
+    output, and the gradient at its input is the transposed rotation
+    (c g_a' - s g_b', s g_a' + c g_b').  The layers' outputs are recomputed
+    forward from x (not recovered by inverting y).  Below layer 0 the gradient
+    g_t is taken at t = s * x: d x = s * g_t and d s = sum_rows x * g_t.
+    cos / sin are those of cos_sin_table (the float32 values the kernels use).
+    Returns (grad_x [rows, h], grad_theta [krot, h/2], grad_scales [h] or None).
+    The values are those of the reference's RotateTensorFunc.backward
+    (kernels/paroquant_kernels/interface.py:30-93), which reaches them another way.
+    """
+    x = np.asarray(x, np.float64)
+    h = x.shape[-1]
+    xr = x.reshape(-1, h)
+    c32, s32 = cos_sin_table(theta)
+    c, s = c32.astype(np.float64), s32.astype(np.float64)
+    gi, gj = pair_index_arrays(pairs, group_size)
+    krot = gi.shape[0]
+    sc = None if scales is None else np.asarray(scales, np.float64).reshape(-1)
+    t = xr * sc[None, :] if sc is not None else xr.copy()
+    outs = []
+    for r in range(krot):
+        a, b = t[:, gi[r]], t[:, gj[r]]
+        na, nb = c[r] * a + s[r] * b, c[r] * b - s[r] * a
+        t[:, gi[r]], t[:, gj[r]] = na, nb
+        outs.append((na, nb))
+    g = np.asarray(grad_y, np.float64).reshape(-1, h).copy()
+    g_theta = np.zeros((krot, h // 2))
+    for r in range(krot - 1, -1, -1):
+        na, nb = outs[r]
+        ga, gb = g[:, gi[r]], g[:, gj[r]]
+        g_theta[r] = (ga * nb - gb * na).sum(axis=0)
+        g[:, gi[r]], g[:, gj[r]] = c[r] * ga - s[r] * gb, s[r] * ga + c[r] * gb
+    if sc is None:
+        return g, g_theta, None
+    return g * sc[None, :], g_theta, (xr * g).sum(axis=0)

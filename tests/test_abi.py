@@ -288,3 +288,59 @@ def test_rotate_rows_argument_checks():
     assert call(mode=1) == 1 and "null" in _err(lib)              # MXFP4 needs the scale buffer
     assert call(x=ctypes.c_void_p(264)) == 1 and "aligned" in _err(lib)
     assert call(rows=0) == 0
+
+
+def test_w4a16_linear_group_argument_checks():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    mem = (_lib.LinearMember * 5)()
+    for i in range(5):
+        mem[i] = _lib.LinearMember(256, 256, None, 256, 256, None, 256, 64)
+    call = lambda members, count, m=2, k=1024, ws=p, wsb=1 << 20: lib.pq_w4a16_linear_group(  # noqa: E731
+        p, 1, members, count, 0, 1, m, k, 8, 1, ws, wsb, None)
+    assert call(mem, 0) == 1 and "count" in _err(lib)
+    assert call(mem, 5) == 1
+    assert call(None, 2) == 1 and "member table" in _err(lib)
+    mem[1].n = 40
+    assert call(mem, 2) == 1
+    mem[1].n = 64
+    assert call(mem, 2, k=1000) == 1
+    assert call(mem, 2, m=0) == 0                                  # empty input: nothing to do
+    mem[0].rot_idx = None
+    assert call(mem, 2) == 1 and "member 0: null pointer" in _err(lib)
+    mem[0].rot_idx = 256
+    mem[1].wpack = 264                                             # 8-byte aligned only
+    assert call(mem, 2) == 1 and "member 1: misaligned" in _err(lib)
+    mem[1].wpack = 256
+    assert call(mem, 2, wsb=16) == 4 and "workspace" in _err(lib)  # workspace too small
+    assert call(mem, 2, ws=ctypes.c_void_p(272)) == 4              # workspace not 256-byte aligned
+
+
+def test_rotate_backward_argument_checks():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    ws = lib.pq_rotate_backward_workspace_size(100, 256, 8)
+    assert ws == 7 * (8 * 128 + 256) * 4                                 # ceil(100 / 16) row tiles
+    assert lib.pq_rotate_backward_workspace_size(10 ** 6, 256, 8) == 64 * (8 * 128 + 256) * 4   # capped at 64
+    assert lib.pq_rotate_backward_workspace_size(0, 256, 8) == 0
+    call = lambda rows=4, h=256, krot=8, gs=128, dt=1, sc=None, gsc=None, w=p, wb=1 << 20: lib.pq_rotate_backward(  # noqa: E731
+        p, p, p, p, gsc, p, p, sc, rows, h, krot, gs, dt, w, wb, None)
+    assert call(gs=32) == 2 and "group_size" in _err(lib)
+    assert call(krot=3) == 2 and "KROT" in _err(lib)
+    assert call(h=200) == 1 and "divisible" in _err(lib)
+    assert call(dt=7) == 2
+    assert call(sc=p) == 1 and "grad_scales" in _err(lib)
+    assert call(gsc=p) == 1 and "grad_scales" in _err(lib)
+    assert call(wb=16) == 4 and "workspace" in _err(lib)
+    assert call(w=None) == 4
+
+
+def test_split_path_python_rule_matches_library():
+    """ops.split_path (the Python form torch.compile traces) agrees with pq_w4a8_linear_split_path."""
+    from alpamayo_amd import ops
+
+    lib = _lib.load()
+    for k in range(128, 16384 + 1, 128):
+        for m in list(range(0, 40)) + [63, 64, 96, 1000, 3072]:
+            assert ops.split_path(m, k) == bool(lib.pq_w4a8_linear_split_path(m, k)), (m, k)
+    assert ops.split_path(1, 16384 + 128) == bool(lib.pq_w4a8_linear_split_path(1, 16384 + 128))

@@ -11,7 +11,6 @@ import pytest
 import torch
 
 import alpamayo_amd  # noqa: F401
-from alpamayo_amd import ops as pqops
 from alpamayo_amd import workloads
 from oracle import gemm as ogemm
 from oracle import packing as opack
@@ -64,12 +63,10 @@ def test_gemm_matches_oracle(M, N, K, out_dtype):
     print(f"gemm M={M} N={N} K={K} {out_dtype}", flush=True)
     w, xq, xs = _case(M, N, K, zlib.crc32(f"g{M}-{N}-{K}".encode()))
     wp, wm = _prepack(w)
-    ws = torch.zeros(max(pqops.workspace_bytes(M, N, K), 1), dtype=torch.uint8, device="cuda")
-    y = torch.ops.paroquant.w4a8_gemm(xq.cuda(), xs.cuda(), wp, wm, None, ws, out_dtype)
+    y = torch.ops.paroquant.w4a8_gemm(xq.cuda(), xs.cuda(), wp, wm, None, out_dtype)
     ref = ogemm.w4a8_linear(xq.numpy(), xs.numpy(), w.codes.numpy(), w.awq_scales.numpy(), w.zeros.numpy())
     assert y.dtype == out_dtype and y.shape == (M, N)
     assert_bf16_close(to_np(y), ref)
-    assert int(ws[:4096].count_nonzero()) == 0      # split-K counters re-armed
 
 
 def test_gemm_bias_and_repeatability():
@@ -77,10 +74,9 @@ def test_gemm_bias_and_repeatability():
     w, xq, xs = _case(M, N, K, 99)
     wp, wm = _prepack(w)
     bias = torch.randn(N).to(torch.bfloat16)
-    ws = torch.zeros(pqops.workspace_bytes(M, N, K), dtype=torch.uint8, device="cuda")
-    y1 = torch.ops.paroquant.w4a8_gemm(xq.cuda(), xs.cuda(), wp, wm, bias.cuda(), ws, torch.bfloat16)
-    y2 = torch.ops.paroquant.w4a8_gemm(xq.cuda(), xs.cuda(), wp, wm, bias.cuda(), ws, torch.bfloat16)
-    assert torch.equal(y1, y2)                       # deterministic split-K reduction
+    y1 = torch.ops.paroquant.w4a8_gemm(xq.cuda(), xs.cuda(), wp, wm, bias.cuda(), torch.bfloat16)
+    y2 = torch.ops.paroquant.w4a8_gemm(xq.cuda(), xs.cuda(), wp, wm, bias.cuda(), torch.bfloat16)
+    assert torch.equal(y1, y2)                       # fixed-order sums: repeatable bit for bit
     ref = ogemm.w4a8_linear(xq.numpy(), xs.numpy(), w.codes.numpy(), w.awq_scales.numpy(), w.zeros.numpy(),
                             bias.float().numpy())
     assert_bf16_close(to_np(y1), ref)
@@ -91,8 +87,7 @@ def test_gemm_bias_f32_out(M, N, K):
     w, xq, xs = _case(M, N, K, 7 + M)
     wp, wm = _prepack(w)
     bias = torch.randn(N).half()
-    ws = torch.zeros(max(pqops.workspace_bytes(M, N, K), 1), dtype=torch.uint8, device="cuda")
-    y = torch.ops.paroquant.w4a8_gemm(xq.cuda(), xs.cuda(), wp, wm, bias.cuda(), ws, torch.float32)
+    y = torch.ops.paroquant.w4a8_gemm(xq.cuda(), xs.cuda(), wp, wm, bias.cuda(), torch.float32)
     ref = ogemm.w4a8_linear(xq.numpy(), xs.numpy(), w.codes.numpy(), w.awq_scales.numpy(), w.zeros.numpy(),
                             bias.float().numpy())
     assert_bf16_close(to_np(y), ref)
@@ -119,9 +114,28 @@ def test_gemm_extreme_operands_exact():
 def test_gemm_empty_and_errors():
     w, xq, xs = _case(4, 64, 256, 5)
     wp, wm = _prepack(w)
-    y = torch.ops.paroquant.w4a8_gemm(xq[:0].cuda(), xs[:0].cuda(), wp, wm, None, None, torch.bfloat16)
+    y = torch.ops.paroquant.w4a8_gemm(xq[:0].cuda(), xs[:0].cuda(), wp, wm, None, torch.bfloat16)
     assert y.shape == (0, 64)
     with pytest.raises(RuntimeError, match="xq must be int8"):
-        torch.ops.paroquant.w4a8_gemm(xq[:, :128].cuda(), xs.cuda(), wp, wm, None, None, torch.bfloat16)
+        torch.ops.paroquant.w4a8_gemm(xq[:, :128].cuda(), xs.cuda(), wp, wm, None, torch.bfloat16)
     with pytest.raises(RuntimeError, match="awq_scales"):
         torch.ops.paroquant.w4a8_prepack(w.awq_qweight.cuda(), w.awq_scales.float().cuda(), w.awq_qzeros.cuda())
+
+
+# The prefill GEMM at the full Qwen3-8B depths with 192 x 256 tiles (>= 256 tiles): q/o (4096 x 4096), the
+# q/k/v group's concatenated columns (6144 x 4096), gate/up's (24576 x 4096 would need 9.6 GB of partials;
+# 12288 x 4096 has the same tiling per column block) and down (4096 x 12288); partials checked bit for bit on
+# rows spread over every row tile position.
+@pytest.mark.parametrize("N,K", [(4096, 4096), (6144, 4096), (12288, 4096), (4096, 12288)])
+def test_partials_full_depth_big_tiles_row_subset(N, K):
+    M = 3072
+    print(f"partials full depth M={M} N={N} K={K}", flush=True)
+    w, xq, _ = _case(M, N, K, zlib.crc32(f"fd{N}-{K}".encode()))
+    wp, wm = _prepack(w)
+    rng = np.random.default_rng(N + K)
+    rows = np.unique(np.concatenate([[0, 1, 191, 192, 383, 1535, 3071], rng.integers(0, M, 9)]))
+    P = torch.ops.paroquant.w4a8_gemm_partials(xq.cuda(), wp, wm)
+    got = to_np(P[torch.from_numpy(rows).cuda()])
+    del P
+    ref = ogemm.group_partials(xq.numpy()[rows], w.codes.numpy(), w.zeros.numpy())
+    np.testing.assert_array_equal(got, ref)

@@ -72,7 +72,7 @@ def test_group_matches_oracle_and_single_calls(M, K, ns, krot, flags):
     xc = x.cuda()
     outs = torch.ops.paroquant.w4a8_linear_group(
         xc, [m["rot_idx"] for m in mbs], [m["rot_cs"] for m in mbs], [m["scales"] for m in mbs], krot,
-        [m["wp"] for m in mbs], [m["wm"] for m in mbs], [m["bias"] for m in mbs], None, flags[0], flags[1],
+        [m["wp"] for m in mbs], [m["wm"] for m in mbs], [m["bias"] for m in mbs], flags[0], flags[1],
         torch.bfloat16)
     assert len(outs) == len(ns)
     x_np = to_np(x)
@@ -80,7 +80,7 @@ def test_group_matches_oracle_and_single_calls(M, K, ns, krot, flags):
         assert y.shape == (M, N) and y.dtype == torch.bfloat16
         assert_bf16_close(to_np(y), _oracle(mb, x_np, flags))
         single = torch.ops.paroquant.w4a8_linear(xc, mb["rot_idx"], mb["rot_cs"], mb["scales"], krot, mb["wp"],
-                                                 mb["wm"], mb["bias"], None, flags[0], flags[1], torch.bfloat16)
+                                                 mb["wm"], mb["bias"], flags[0], flags[1], torch.bfloat16)
         if M > 16:
             # same rotate+quant rows, and the prefill tiles accumulate every output element in the same order
             assert torch.equal(y, single)
@@ -95,7 +95,7 @@ def test_group_output_dtypes_and_leading_dims():
     for dt in (torch.float32, torch.float16):
         outs = torch.ops.paroquant.w4a8_linear_group(
             x.cuda().to(dt), [m["rot_idx"] for m in mbs], [m["rot_cs"] for m in mbs], [m["scales"] for m in mbs],
-            8, [m["wp"] for m in mbs], [m["wm"] for m in mbs], [None, None], None, False, True, dt)
+            8, [m["wp"] for m in mbs], [m["wm"] for m in mbs], [None, None], False, True, dt)
         assert [tuple(o.shape) for o in outs] == [(2, 3, 64), (2, 3, 128)] and all(o.dtype == dt for o in outs)
         for mb, y in zip(mbs, outs):
             assert_bf16_close(to_np(y.reshape(6, -1)), _oracle(mb, to_np(x.reshape(6, 1024).to(dt)), (False, True)))
@@ -138,10 +138,10 @@ def test_group_rejects_bad_members():
     mbs = _members((64, 128), 1024, 8, 5, with_bias=False)
     x = workloads.activations(2, 1024, workloads.generator(6)).cuda()
     with pytest.raises(Exception, match="1..4"):
-        torch.ops.paroquant.w4a8_linear_group(x, [], [], [], 8, [], [], [], None, True, True, torch.bfloat16)
+        torch.ops.paroquant.w4a8_linear_group(x, [], [], [], 8, [], [], [], True, True, torch.bfloat16)
     other = _members((64,), 2048, 8, 7, with_bias=False)[0]
     with pytest.raises(Exception, match="features"):
         torch.ops.paroquant.w4a8_linear_group(
             x, [mbs[0]["rot_idx"], other["rot_idx"]], [mbs[0]["rot_cs"], other["rot_cs"]],
             [mbs[0]["scales"], other["scales"]], 8, [mbs[0]["wp"], other["wp"]], [mbs[0]["wm"], other["wm"]],
-            [None, None], None, True, True, torch.bfloat16)
+            [None, None], True, True, torch.bfloat16)

@@ -55,7 +55,7 @@ def test_rmsnorm_group(M, K, ns, with_res):
     res = workloads.activations(M, K, g) if with_res else None
     w = (0.8 + 0.4 * torch.rand(K, generator=g)).to(torch.bfloat16)
     args = ([m["rot_idx"] for m in mbs], [m["rot_cs"] for m in mbs], [m["scales"] for m in mbs], krot,
-            [m["wp"] for m in mbs], [m["wm"] for m in mbs], [m["bias"] for m in mbs], None, flags[0], flags[1],
+            [m["wp"] for m in mbs], [m["wm"] for m in mbs], [m["bias"] for m in mbs], flags[0], flags[1],
             torch.bfloat16)
     outs = torch.ops.paroquant.w4a8_linear_group_rmsnorm(x.cuda(), res.cuda() if with_res else None, w.cuda(), 1e-6,
                                                          *args, True, with_res)

@@ -121,3 +121,75 @@ def test_autograd_backward_matches_float64():
     assert rel_fro(to_np(xg.grad), x64.grad.numpy()) < 1e-4
     assert rel_fro(to_np(thg.grad), th64.grad.numpy()) < 1e-4
     assert rel_fro(to_np(scg.grad), sc64.grad.numpy()) < 1e-4
+
+
+_BWD_TOL = {"f32": 2e-6, "f16": 2e-3, "bf16": 1.6e-2}
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("gs,krot,h,rows", [(128, 8, 4096, 5), (128, 1, 256, 1), (64, 4, 192, 33),
+                                            (128, 16, 384, 9), (64, 8, 64, 3), (128, 2, 1024, 3000),
+                                            (128, 8, 12288, 17), (64, 16, 320, 1030), (128, 8, 256, 0)])
+@pytest.mark.parametrize("with_scale", [True, False])
+def test_rotate_backward_matches_oracle(dt, gs, krot, h, rows, with_scale):
+    """paroquant::rotate_backward (one kernel pass + a fixed-order reduction) against the float64 oracle on
+    the same dtype-rounded inputs; 3000 rows exercise the grid-stride row tiles, 0 rows the zero sums."""
+    print(f"rotate_backward dt={dt} gs={gs} krot={krot} h={h} rows={rows} scale={with_scale}", flush=True)
+    rng = np.random.default_rng(zlib.crc32(f"bwd{dt}{gs}{krot}{h}{rows}".encode()))
+    pairs, theta, scales = _params(rng, krot, h, gs)
+    tdt = DT[dt]
+    x = torch.from_numpy(rng.standard_normal((rows, h)).astype(np.float32) * 3).to(tdt)
+    gy = torch.from_numpy(rng.standard_normal((rows, h)).astype(np.float32)).to(tdt)
+    th = torch.from_numpy(theta).to(tdt)
+    sc = torch.from_numpy(scales).to(tdt).reshape(1, h) if with_scale else None
+    idx = torch.from_numpy(pairs)
+    gx, gt, gs_ = torch.ops.paroquant.rotate_backward(gy.cuda(), x.cuda(), idx.cuda(), th.cuda(),
+                                                      sc.cuda() if sc is not None else None, gs)
+    again = torch.ops.paroquant.rotate_backward(gy.cuda(), x.cuda(), idx.cuda(), th.cuda(),
+                                                sc.cuda() if sc is not None else None, gs)
+    torch.cuda.synchronize()
+    assert gx.dtype == tdt and gx.shape == x.shape and gt.dtype == tdt and gt.shape == th.shape
+    for a, b in zip((gx, gt, gs_), again):
+        assert torch.equal(a, b), "the backward is deterministic"
+    rx, rt, rs = orot.rotate_backward(to_np(x).astype(np.float64), pairs, to_np(th),
+                                      to_np(sc).reshape(-1) if sc is not None else None,
+                                      to_np(gy).astype(np.float64), gs)
+    tol = _BWD_TOL[dt]
+    if rows == 0:
+        assert gx.numel() == 0 and not gt.abs().any()
+        if with_scale:
+            assert gs_.shape == sc.shape and not gs_.abs().any()
+        return
+    assert rel_fro(to_np(gx), rx.reshape(x.shape)) < tol
+    assert rel_fro(to_np(gt), rt) < tol
+    if with_scale:
+        assert gs_.shape == sc.shape
+        assert rel_fro(to_np(gs_).reshape(-1), rs) < tol
+    else:
+        assert gs_.numel() == 0
+
+
+def test_autograd_backward_half_precision_and_no_scale():
+    """scaled_pairwise_rotation in fp16 with and without channel scales: gradients against float64 autograd."""
+    rng = np.random.default_rng(4)
+    h, krot, rows = 512, 8, 40
+    pairs, theta, scales = _params(rng, krot, h, 128)
+    for with_scale in (True, False):
+        x16 = torch.from_numpy(rng.standard_normal((rows, h)).astype(np.float32)).half()
+        th16 = torch.from_numpy(theta).half()
+        sc16 = torch.from_numpy(scales).half()
+        w = torch.from_numpy(rng.standard_normal((rows, h)).astype(np.float32)).half()
+        x64 = x16.double().requires_grad_(True)
+        th64 = th16.double().requires_grad_(True)
+        sc64 = sc16.double().requires_grad_(True)
+        (_givens_f64(x64, torch.from_numpy(pairs), th64, sc64 if with_scale else None, 128) * w.double()).sum() \
+            .backward()
+        xg = x16.cuda().requires_grad_(True)
+        thg = th16.cuda().requires_grad_(True)
+        scg = sc16.cuda().requires_grad_(True) if with_scale else None
+        y = scaled_pairwise_rotation(xg, torch.from_numpy(pairs).cuda(), thg, scg, 128)
+        (y * w.cuda()).sum().backward()
+        assert rel_fro(to_np(xg.grad), x64.grad.numpy()) < 2e-3
+        assert rel_fro(to_np(thg.grad), th64.grad.numpy()) < 2e-3
+        if with_scale:
+            assert rel_fro(to_np(scg.grad), sc64.grad.numpy()) < 2e-3

@@ -80,38 +80,51 @@ def test_packed_kernel_equals_tile_kernel(dt, krot, h, rows, with_scale):
     assert rel_fro(to_np(y_rows), ref) < (1e-5 if dt == "f32" else 1e-2)
 
 
-def test_ops_use_the_packed_kernel_from_1024_rows_and_in_graphs():
+def test_ops_use_registered_packed_operands_from_1024_rows_and_in_graphs():
+    """rotation::rotate / rotate_and_quant_mxfp4 on a prepared Rotation's own buffers run the packed-operand
+    kernel from 1024 rows (the operands Rotation.prepare() registered; the op never packs); the same values
+    in other tensors run the tile kernel; both give the same bits.  An in-place update of the angles lapses
+    the registration until the next prepare()."""
+    from alpamayo_amd.quantization import Rotation
+
     rng = np.random.default_rng(99)
     h, krot = 4096, 8
     pairs, theta, scales = _params(rng, krot, h)
     p = torch.from_numpy(pairs).cuda()
     th = torch.from_numpy(theta).bfloat16().cuda()
-    sc = torch.from_numpy(scales).bfloat16().cuda()
+    sc = torch.from_numpy(scales).bfloat16().cuda().reshape(1, h)
+    rot = Rotation(h, rotation_angles=th, rotation_pairs=p, channel_scales=sc).cuda()
+    rot.prepare()
     x = torch.randn(2048, h, device="cuda").bfloat16()
-    ops._PACK_CACHE.clear()
-    y = torch.ops.rotation.rotate(x, p, th, sc, 128)
-    q, s = torch.ops.rotation.rotate_and_quant_mxfp4(x, p, th, sc, 128)
-    assert len(ops._PACK_CACHE) == 1                      # one packing serves both ops
-    small = torch.ops.rotation.rotate(x[:16], p, th, sc, 128)   # tile kernel below 1024 rows
-    assert torch.equal(small, y[:16])
+    assert ops._packed_for(rot.pairs, rot.theta, rot.channel_scales, 128) is not None
+    y = rot(x)                                                      # packed kernel
+    y_tile = torch.ops.rotation.rotate(x, p.clone(), th.clone(), sc.clone(), 128)   # unregistered: tile kernel
+    assert ops._packed_for(p, th, sc, 128) is None
+    assert torch.equal(y, y_tile)
+    q, s = torch.ops.rotation.rotate_and_quant_mxfp4(x, rot.pairs, rot.theta, rot.channel_scales, 128)
     y32 = torch.ops.rotation.rotate(x.float(), p, th.float(), sc.float(), 128)
     rq, rs = omx.quantize(to_np(y32))
     assert np.array_equal(q.cpu().numpy(), rq) and np.array_equal(s.cpu().numpy(), rs)
-    # graph capture replays the packed kernel (operands already cached)
+    small = rot(x[:16])                                             # tile kernel below 1024 rows
+    assert torch.equal(small, y[:16])
+    # graph capture replays the packed kernel
     st = torch.cuda.Stream()
     st.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(st):
-        torch.ops.rotation.rotate(x, p, th, sc, 128)
+        rot(x)
     torch.cuda.current_stream().wait_stream(st)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        yc = torch.ops.rotation.rotate(x, p, th, sc, 128)
+        yc = rot(x)
     for _ in range(3):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(yc, y)
-    # new angles (in-place update) are packed again
-    th.mul_(0.5)
-    y2 = torch.ops.rotation.rotate(x, p, th, sc, 128)
-    ref2 = orot.rotate(to_np(x), pairs, to_np(th), to_np(sc), 128, out_dtype=np.float32)
+    # new angles (in-place update): the registration lapses (tile kernel, new values) until prepare()
+    rot.theta.mul_(0.5)
+    assert not rot.prepared and ops._packed_for(rot.pairs, rot.theta, rot.channel_scales, 128) is None
+    y2 = rot(x)
+    ref2 = orot.rotate(to_np(x), pairs, to_np(rot.theta), to_np(sc), 128, out_dtype=np.float32)
     assert rel_fro(to_np(y2), ref2) < 1e-2 and not torch.equal(y2, y)
+    rot.prepare()
+    assert torch.equal(rot(x), y2)

@@ -154,7 +154,7 @@ def test_linear_rotation_then_gemm(m, x_dtype, input_fp16):
     wpack, wmeta = _prepack(spec.w, s, sz)
     scales = spec.channel_scales.float().reshape(-1)
     y = torch.ops.paroquant.w4a16_linear(x.cuda(), rot_idx.cuda(), rot_cs.cuda(), scales.cuda(), 8, wpack, wmeta,
-                                         None, None, input_fp16, torch.float32)
+                                         None, input_fp16, torch.float32)
     torch.cuda.synchronize()
     ref, _ = ow.rotate_linear_w16(to_np(x).astype(np.float32), spec.pairs.numpy(), c, sn, scales.numpy(),
                                   spec.w.codes.numpy(), s.numpy(), sz.numpy(), input_fp16=input_fp16)
@@ -268,10 +268,10 @@ def test_linear_group_matches_single_linears(m, ns):
         args.append((rot_idx.cuda(), rot_cs.cuda(), scales, wpack, wmeta, bias))
     outs = torch.ops.paroquant.w4a16_linear_group(x, [a[0] for a in args], [a[1] for a in args],
                                                   [a[2] for a in args], 8, [a[3] for a in args],
-                                                  [a[4] for a in args], [a[5] for a in args], None, True,
+                                                  [a[4] for a in args], [a[5] for a in args], True,
                                                   torch.bfloat16)
     for (ri, rc, sc, wp, wm, b), y, n in zip(args, outs, ns):
-        ref = torch.ops.paroquant.w4a16_linear(x, ri, rc, sc, 8, wp, wm, b, None, True, torch.bfloat16)
+        ref = torch.ops.paroquant.w4a16_linear(x, ri, rc, sc, 8, wp, wm, b, True, torch.bfloat16)
         torch.cuda.synchronize()
         assert y.shape == (m, n)
         yf, rf = y.float(), ref.float()
@@ -301,9 +301,9 @@ def test_linear_group_member_blocks_aligned_small_k(m, k):
     assert need % (256 * len(ns)) == 0
     outs = torch.ops.paroquant.w4a16_linear_group(x, [a[0] for a in args], [a[1] for a in args],
                                                   [a[2] for a in args], 8, [a[3] for a in args],
-                                                  [a[4] for a in args], [None] * len(ns), None, True, torch.bfloat16)
+                                                  [a[4] for a in args], [None] * len(ns), True, torch.bfloat16)
     for (ri, rc, sc, wp, wm), y, n in zip(args, outs, ns):
-        ref = torch.ops.paroquant.w4a16_linear(x, ri, rc, sc, 8, wp, wm, None, None, True, torch.bfloat16)
+        ref = torch.ops.paroquant.w4a16_linear(x, ri, rc, sc, 8, wp, wm, None, True, torch.bfloat16)
         torch.cuda.synchronize()
         assert y.shape == (m, n)
         yf, rf = y.float(), ref.float()

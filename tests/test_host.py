@@ -41,10 +41,10 @@ def test_meta_kernels_propagate_shapes():
     assert xq.shape == (6, 256) and xq.dtype == torch.int8 and xs.shape == (6,)
     wp = torch.empty(64, 2, 64, 16, device=m, dtype=torch.uint8)
     wm = torch.empty(64, 2, 16, device=m, dtype=torch.int32)
-    out = torch.ops.paroquant.w4a8_gemm(xq, xs, wp, wm, None, None, torch.bfloat16)
+    out = torch.ops.paroquant.w4a8_gemm(xq, xs, wp, wm, None, torch.bfloat16)
     assert out.shape == (6, 1024) and out.dtype == torch.bfloat16
     lin = torch.ops.paroquant.w4a8_linear(x, torch.empty(2, 64, 4, device=m, dtype=torch.int32),
-                                          torch.empty(2, 64, 8, 2, device=m), None, 8, wp, wm, None, None, True, True,
+                                          torch.empty(2, 64, 8, 2, device=m), None, 8, wp, wm, None, True, True,
                                           torch.bfloat16)
     assert lin.shape == (2, 3, 1024)
     part = torch.ops.paroquant.w4a8_gemm_partials(xq, wp, wm)
@@ -129,6 +129,77 @@ def test_rotation_prepare_builds_fused_operands():
     bad[0, 1] = bad[0, 0]
     with pytest.raises(ValueError):
         check_rotation_pairs(bad)
+
+
+def test_rotation_prepared_tracks_its_parameters():
+    """prepared turns False after load_state_dict, an in-place update or a replacement of theta / pairs /
+    channel_scales, so the fused paths re-derive their operands instead of using stale ones."""
+    g = workloads.generator(6)
+    pairs, theta, cs = workloads.rotation_params(256, g)
+    rot = Rotation(256, rotation_angles=theta, rotation_pairs=pairs, channel_scales=cs)
+    assert not rot.prepared
+    rot.prepare()
+    assert rot.prepared
+    old_cs = rot.rot_cs.clone()
+    pairs2, theta2, cs2 = workloads.rotation_params(256, workloads.generator(7))
+    rot.load_state_dict({"theta": theta2, "pairs": pairs2, "channel_scales": cs2})
+    assert not rot.prepared
+    rot.prepare()
+    assert rot.prepared and not torch.equal(rot.rot_cs, old_cs)
+    rot.channel_scales.mul_(2)
+    assert not rot.prepared
+    rot.prepare()
+    np.testing.assert_array_equal(rot.scales_f32.numpy(), (cs2.float() * 2).reshape(-1).numpy())
+    rot.theta = rot.theta.clone()
+    assert not rot.prepared
+
+
+def test_rotate_op_only_looks_up_registered_operands():
+    """rotation::rotate never packs: it finds the operands Rotation.prepare() registered for exactly its
+    tensors, and the entry lapses when any of them changes."""
+    from alpamayo_amd import ops
+
+    g = workloads.generator(8)
+    pairs, theta, cs = workloads.rotation_params(256, g)
+    rot = Rotation(256, rotation_angles=theta, rotation_pairs=pairs, channel_scales=cs)
+    assert ops._packed_for(rot.pairs, rot.theta, rot.channel_scales, 128) is None
+    rot.prepare()
+    got = ops._packed_for(rot.pairs, rot.theta, rot.channel_scales, 128)
+    assert got is not None and got[0] is rot.rot_idx and got[1] is rot.rot_cs
+    assert ops._packed_for(rot.pairs.clone(), rot.theta, rot.channel_scales, 128) is None   # other tensor
+    assert ops._packed_for(rot.pairs, rot.theta, rot.channel_scales, 64) is None
+    th_grad = rot.theta.float().requires_grad_(True)
+    assert ops._packed_for(rot.pairs, th_grad, rot.channel_scales, 128) is None
+    rot.theta.add_(0.5)
+    assert ops._packed_for(rot.pairs, rot.theta, rot.channel_scales, 128) is None
+
+
+def test_rotate_backward_fake_kernel():
+    m = "meta"
+    x = torch.empty(3, 5, 256, device=m, dtype=torch.bfloat16)
+    idx = torch.empty(8, 256, device=m, dtype=torch.int16)
+    th = torch.empty(8, 128, device=m, dtype=torch.bfloat16)
+    sc = torch.empty(1, 256, device=m, dtype=torch.bfloat16)
+    gx, gt, gs = torch.ops.paroquant.rotate_backward(x, x, idx, th, sc, 128)
+    assert gx.shape == x.shape and gt.shape == th.shape and gs.shape == sc.shape and gs.dtype == torch.bfloat16
+    gx, gt, gs = torch.ops.paroquant.rotate_backward(x, x, idx, th, None, 128)
+    assert gs.numel() == 0
+
+
+def test_op_implementations_reach_no_host_copy():
+    """No op implementation copies to the host or synchronizes (the reference op only enqueues,
+    rotation.cu:137): the source of every registered CUDA implementation is free of such calls."""
+    import inspect
+
+    from alpamayo_amd import ops
+
+    impls = [v for k, v in vars(ops).items() if k.startswith("_") and k.endswith("_impl") and callable(v)]
+    impls += [ops._packed_for, ops._rotate_rows, ops._rotate_args]
+    assert len(impls) >= 15
+    for fn in impls:
+        src = inspect.getsource(fn)
+        for bad in ('.to("cpu"', ".cpu()", ".item()", ".tolist()", "synchronize", "pack_rotation(", ".numpy()"):
+            assert bad not in src, f"{fn.__name__} contains {bad}"
 
 
 def test_workloads_are_seeded_and_distributed_as_specified():

@@ -162,3 +162,108 @@ def test_rotate_rejects_bad_shapes():
     with pytest.raises(ValueError):
         rotation.rotate(np.zeros((1, 128), np.float32), np.zeros((8, 128), np.int16),
                         np.zeros((4, 64), np.float32), None, 128)
+
+
+def _dense_autograd_grads(x, pairs, theta, scales, gy, gs):
+    """dL/d(x, theta, scales) of L = sum(gy * y) by torch float64 autograd through an explicit dense product
+    of block-diagonal Givens matrices built from (pairs, theta) with torch.cos / torch.sin."""
+    import torch
+
+    krot, h = pairs.shape
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    tt = torch.tensor(theta.astype(np.float32).astype(np.float64), requires_grad=True)
+    st = torch.tensor(scales.astype(np.float64), requires_grad=True) if scales is not None else None
+    v = xt * st if st is not None else xt
+    for r in range(krot):
+        rows_i, cols_i, vals = [], [], []
+        L = torch.zeros(h, h, dtype=torch.float64)
+        for g in range(h // gs):
+            for t in range(gs // 2):
+                i = g * gs + int(pairs[r, g * gs + 2 * t])
+                j = g * gs + int(pairs[r, g * gs + 2 * t + 1])
+                a = tt[r, g * gs // 2 + t]
+                L = L.index_put((torch.tensor([i, i, j, j]), torch.tensor([i, j, i, j])),
+                                torch.stack([torch.cos(a), torch.sin(a), -torch.sin(a), torch.cos(a)]))
+        v = v @ L.T
+    (v * torch.tensor(gy, dtype=torch.float64)).sum().backward()
+    return xt.grad.numpy(), tt.grad.numpy(), (st.grad.numpy() if st is not None else None)
+
+
+@pytest.mark.parametrize("gs,krot,scaled", [(128, 8, True), (64, 4, True), (128, 2, False), (128, 16, True)])
+def test_backward_matches_float64_autograd(gs, krot, scaled):
+    """rotate_backward against autograd of the dense product (a library routine over a different form)."""
+    rng = np.random.default_rng(10 + krot)
+    h, rows = 128 if gs == 128 else 192, 5
+    pairs = _random_pairs(rng, krot, h, gs)
+    theta = rng.uniform(-np.pi, np.pi, (krot, h // 2)).astype(np.float16)
+    scales = rng.uniform(0.5, 2, h).astype(np.float16) if scaled else None
+    x = rng.standard_normal((rows, h))
+    gy = rng.standard_normal((rows, h))
+    gx, gt, gsc = rotation.rotate_backward(x, pairs, theta, scales, gy, gs)
+    rx, rt, rs = _dense_autograd_grads(x, pairs, theta, scales, gy, gs)
+    # the oracle uses cos/sin rounded to float32, autograd exact ones: agreement to ~1e-7
+    assert np.linalg.norm(gx - rx) / np.linalg.norm(rx) < 1e-6
+    assert np.linalg.norm(gt - rt) / np.linalg.norm(rt) < 1e-6
+    if scaled:
+        assert np.linalg.norm(gsc - rs) / np.linalg.norm(rs) < 1e-6
+    else:
+        assert gsc is None
+
+
+def test_backward_angle_gradient_by_finite_differences():
+    """d L / d theta[r, p] by central differences of the forward oracle (float64 angles)."""
+    rng = np.random.default_rng(21)
+    h, krot, rows = 128, 3, 4
+    pairs = _random_pairs(rng, krot, h)
+    theta = rng.uniform(-np.pi, np.pi, (krot, h // 2)).astype(np.float32)
+    x = rng.standard_normal((rows, h))
+    gy = rng.standard_normal((rows, h))
+    _, gt, _ = rotation.rotate_backward(x, pairs, theta, None, gy, 128)
+    gi, gj = rotation.pair_index_arrays(pairs, 128)
+
+    def loss(th):
+        t = x.copy()
+        for r in range(krot):
+            c, s = np.cos(th[r]), np.sin(th[r])
+            a, b = t[:, gi[r]], t[:, gj[r]]
+            t[:, gi[r]], t[:, gj[r]] = c * a + s * b, c * b - s * a
+        return float((t * gy).sum())
+
+    eps = 1e-6
+    th64 = theta.astype(np.float64)
+    for r, p in ((0, 0), (1, 17), (2, 63)):
+        tp, tm = th64.copy(), th64.copy()
+        tp[r, p] += eps
+        tm[r, p] -= eps
+        fd = (loss(tp) - loss(tm)) / (2 * eps)
+        assert abs(fd - gt[r, p]) < 1e-5 * max(1.0, abs(fd)), (r, p, fd, gt[r, p])
+
+
+def test_backward_check_catches_a_sign_mistake():
+    """A plausible mistake in the angle gradient (g_a' a' + g_b' b' instead of g_a' b' - g_b' a') must fail the
+    autograd comparison above."""
+    rng = np.random.default_rng(22)
+    h, krot, rows = 128, 2, 3
+    pairs = _random_pairs(rng, krot, h)
+    theta = rng.uniform(-np.pi, np.pi, (krot, h // 2)).astype(np.float16)
+    x = rng.standard_normal((rows, h))
+    gy = rng.standard_normal((rows, h))
+    _, rt, _ = _dense_autograd_grads(x, pairs, theta, None, gy, 128)
+    # wrong form, planted on the CPU
+    c32, s32 = rotation.cos_sin_table(theta)
+    gi, gj = rotation.pair_index_arrays(pairs, 128)
+    t = x.copy()
+    outs = []
+    for r in range(krot):
+        a, b = t[:, gi[r]], t[:, gj[r]]
+        na, nb = c32[r] * a + s32[r] * b, c32[r] * b - s32[r] * a
+        t[:, gi[r]], t[:, gj[r]] = na, nb
+        outs.append((na, nb))
+    g = gy.copy()
+    wrong = np.zeros((krot, h // 2))
+    for r in range(krot - 1, -1, -1):
+        na, nb = outs[r]
+        ga, gb = g[:, gi[r]], g[:, gj[r]]
+        wrong[r] = (ga * na + gb * nb).sum(axis=0)
+        g[:, gi[r]], g[:, gj[r]] = c32[r] * ga - s32[r] * gb, s32[r] * ga + c32[r] * gb
+    assert np.linalg.norm(wrong - rt) / np.linalg.norm(rt) > 0.1
