@@ -279,9 +279,11 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
 #pragma unroll
   for (int r = 0; r < RB; ++r) rmax[r] = 0.0f;
 
-  pqd::RotLane<KP> cur, nxt;
-  uint32_t xa[RB], xb[RB], xan[RB], xbn[RB];
-  float sa = 1.0f, sb = 1.0f, san = 1.0f, sbn = 1.0f;
+  // Two register sets, used alternately (the group loop is unrolled twice): the set of group g is
+  // computed while the loads of group g + kRQWaves land in the other one, with no copies between them.
+  pqd::RotLane<KP> rl[2];
+  uint32_t xa[2][RB], xb[2][RB];
+  float sa[2] = {1.0f, 1.0f}, sb[2] = {1.0f, 1.0f};
   auto load_inputs = [&](int g, uint32_t (&va)[RB], uint32_t (&vb)[RB], float& s0, float& s1) {
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
@@ -300,8 +302,8 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
   const bool pro_glu = NORM && nm.mode == PQ_PRO_SWIGLU;
   const void* nres = NORM && nm.res != nullptr ? nm.res : x;
   const void* nwp = pro_norm ? nm.w : x;
-  uint32_t ra[RB], rb[RB], ran[RB], rbn[RB];
-  uint32_t wa = 0, wb = 0, wan = 0, wbn = 0;
+  uint32_t ra[2][RB], rb[2][RB];
+  uint32_t wa[2] = {0, 0}, wb[2] = {0, 0};
   auto load_norm = [&](int g, uint32_t (&va)[RB], uint32_t (&vb)[RB], uint32_t& w0, uint32_t& w1) {
     if constexpr (NORM) {
 #pragma unroll
@@ -323,82 +325,77 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
   const bool write_norm = NORM && blockIdx.y == 0;   // the same for every member: member 0 writes
 
   if (w < G) {
-    pqd::load_rot_lane<KP>(rot_idx, rot_cs, w, lane, cur);
-    load_inputs(w, xa, xb, sa, sb);
-    load_norm(w, ra, rb, wa, wb);
+    pqd::load_rot_lane<KP>(rot_idx, rot_cs, w, lane, rl[0]);
+    load_inputs(w, xa[0], xb[0], sa[0], sb[0]);
+    load_norm(w, ra[0], rb[0], wa[0], wb[0]);
   }
-  for (int g = w; g < G; g += kRQWaves) {
-    const int gn = (g + kRQWaves < G) ? g + kRQWaves : g;   // clamped: the loads stay unconditional
-    pqd::load_rot_lane<KP>(rot_idx, rot_cs, gn, lane, nxt);
-    load_inputs(gn, xan, xbn, san, sbn);
-    load_norm(gn, ran, rbn, wan, wbn);
+  for (int g0 = w; g0 < G; g0 += 2 * kRQWaves) {
+#pragma unroll
+    for (int ph = 0; ph < 2; ++ph) {
+      const int g = g0 + ph * kRQWaves;
+      if (g >= G) break;   // wave-uniform
+      const int nx = ph ^ 1;
+      const int gn = (g + kRQWaves < G) ? g + kRQWaves : g;   // clamped: the loads stay unconditional
+      pqd::load_rot_lane<KP>(rot_idx, rot_cs, gn, lane, rl[nx]);
+      load_inputs(gn, xa[nx], xb[nx], sa[nx], sb[nx]);
+      load_norm(gn, ra[nx], rb[nx], wa[nx], wb[nx]);
 
-    const bool sw = pqd::rot_init_swapped(cur);
-    const float s0 = has_scales ? sa : 1.0f, s1 = has_scales ? sb : 1.0f;
-    float a[RB], b[RB];
+      const pqd::RotLane<KP>& cur = rl[ph];
+      const bool sw = pqd::rot_init_swapped(cur);
+      const float s0 = has_scales ? sa[ph] : 1.0f, s1 = has_scales ? sb[ph] : 1.0f;
+      float a[RB], b[RB];
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      float lo = pq_raw_to_f32<DT>(xa[r]), hi = pq_raw_to_f32<DT>(xb[r]);
-      if constexpr (NORM) {
-        const int64_t ro = (row0 + r) * h + g * 128 + lane;
-        if (pro_glu) {
-          lo = pqd::swiglu<DT>(lo, pq_raw_to_f32<DT>(ra[r]));
-          hi = pqd::swiglu<DT>(hi, pq_raw_to_f32<DT>(rb[r]));
+      for (int r = 0; r < RB; ++r) {
+        float lo = pq_raw_to_f32<DT>(xa[ph][r]), hi = pq_raw_to_f32<DT>(xb[ph][r]);
+        if constexpr (NORM) {
+          const int64_t ro = (row0 + r) * h + g * 128 + lane;
+          if (pro_glu) {
+            lo = pqd::swiglu<DT>(lo, pq_raw_to_f32<DT>(ra[ph][r]));
+            hi = pqd::swiglu<DT>(hi, pq_raw_to_f32<DT>(rb[ph][r]));
+          } else {
+            if (nm.res != nullptr) {
+              lo = pqd::round_to_dt<DT>(lo + pq_raw_to_f32<DT>(ra[ph][r]));
+              hi = pqd::round_to_dt<DT>(hi + pq_raw_to_f32<DT>(rb[ph][r]));
+            }
+            if (write_norm && nm.s_out != nullptr) {
+              pq_store_from_f32<DT>(nm.s_out, ro, lo);
+              pq_store_from_f32<DT>(nm.s_out, ro + 64, hi);
+            }
+            if (pro_norm) {
+              lo = pqd::rms_apply<DT>(lo, s_rinv[r], pq_raw_to_f32<DT>(wa[ph]));
+              hi = pqd::rms_apply<DT>(hi, s_rinv[r], pq_raw_to_f32<DT>(wb[ph]));
+            }
+          }
+          if ((pro_norm || pro_glu) && write_norm && nm.h_out != nullptr) {
+            pq_store_from_f32<DT>(nm.h_out, ro, lo);
+            pq_store_from_f32<DT>(nm.h_out, ro + 64, hi);
+          }
+        }
+        lo = (in16 ? pq_round_f16(lo) : lo) * s0;
+        hi = (in16 ? pq_round_f16(hi) : hi) * s1;
+        a[r] = sw ? hi : lo;
+        b[r] = sw ? lo : hi;
+      }
+#pragma unroll
+      for (int k = 0; k < KP; ++k)
+        if (k < krot) pqd::rot_layer<KP, RB>(cur, k, a, b);
+      const int fa = g * 128 + pqd::rot_final_a(cur), fb = g * 128 + pqd::rot_final_b(cur);
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        float vi = a[r], vj = b[r];
+        if constexpr (MAT16) {
+          const uint16_t hi = pq_f32_to_f16(vi), hj = pq_f32_to_f16(vj);
+          rowbuf[r * h + fa] = hi;
+          rowbuf[r * h + fb] = hj;
+          vi = pq_f16_to_f32(hi);
+          vj = pq_f16_to_f32(hj);
         } else {
-          if (nm.res != nullptr) {
-            lo = pqd::round_to_dt<DT>(lo + pq_raw_to_f32<DT>(ra[r]));
-            hi = pqd::round_to_dt<DT>(hi + pq_raw_to_f32<DT>(rb[r]));
-          }
-          if (write_norm && nm.s_out != nullptr) {
-            pq_store_from_f32<DT>(nm.s_out, ro, lo);
-            pq_store_from_f32<DT>(nm.s_out, ro + 64, hi);
-          }
-          if (pro_norm) {
-            lo = pqd::rms_apply<DT>(lo, s_rinv[r], pq_raw_to_f32<DT>(wa));
-            hi = pqd::rms_apply<DT>(hi, s_rinv[r], pq_raw_to_f32<DT>(wb));
-          }
+          rowbuf[r * h + fa] = vi;
+          rowbuf[r * h + fb] = vj;
         }
-        if ((pro_norm || pro_glu) && write_norm && nm.h_out != nullptr) {
-          pq_store_from_f32<DT>(nm.h_out, ro, lo);
-          pq_store_from_f32<DT>(nm.h_out, ro + 64, hi);
-        }
+        rmax[r] = fmaxf(rmax[r], fmaxf(fabsf(vi), fabsf(vj)));
       }
-      lo = (in16 ? pq_round_f16(lo) : lo) * s0;
-      hi = (in16 ? pq_round_f16(hi) : hi) * s1;
-      a[r] = sw ? hi : lo;
-      b[r] = sw ? lo : hi;
     }
-#pragma unroll
-    for (int k = 0; k < KP; ++k)
-      if (k < krot) pqd::rot_layer<KP, RB>(cur, k, a, b);
-    const int fa = g * 128 + pqd::rot_final_a(cur), fb = g * 128 + pqd::rot_final_b(cur);
-#pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      float vi = a[r], vj = b[r];
-      if constexpr (MAT16) {
-        const uint16_t hi = pq_f32_to_f16(vi), hj = pq_f32_to_f16(vj);
-        rowbuf[r * h + fa] = hi;
-        rowbuf[r * h + fb] = hj;
-        vi = pq_f16_to_f32(hi);
-        vj = pq_f16_to_f32(hj);
-      } else {
-        rowbuf[r * h + fa] = vi;
-        rowbuf[r * h + fb] = vj;
-      }
-      rmax[r] = fmaxf(rmax[r], fmaxf(fabsf(vi), fabsf(vj)));
-    }
-    cur = nxt;
-#pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      xa[r] = xan[r];
-      xb[r] = xbn[r];
-      ra[r] = ran[r];
-      rb[r] = rbn[r];
-    }
-    sa = san;
-    sb = sbn;
-    wa = wan;
-    wb = wbn;
   }
 
   if constexpr (OUT == kRqRows) {
@@ -477,16 +474,24 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
     if (lane == 0) red[w][r] = v;
   }
   __syncthreads();
+  // Each row's absmax and 127 / absmax, once per row.
+  __shared__ float s_am[RB], s_inv[RB];
+  if (t < RB) {
+    float am = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < kRQWaves; ++ww) am = fmaxf(am, red[ww][t]);
+    s_am[t] = am;
+    s_inv[t] = pqd::inv_scale(am);
+  }
+  __syncthreads();
 
   // Quantize the row buffer: 8 elements per thread per step.
   const int per_row = h >> 3;
   for (int e = t; e < RB * per_row; e += kRQWaves * 64) {
     const int r = e / per_row;
     const int c8 = (e - r * per_row) * 8;
-    float am = 0.0f;
-#pragma unroll
-    for (int ww = 0; ww < kRQWaves; ++ww) am = fmaxf(am, red[ww][r]);
-    const float inv = pqd::inv_scale(am);
+    const float am = s_am[r];
+    const float inv = s_inv[r];
     float f[8];
     if constexpr (MAT16) {
       const uint4 u = *reinterpret_cast<const uint4*>(rowbuf + r * h + c8);

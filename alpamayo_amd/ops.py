@@ -37,6 +37,7 @@ explicit workspace argument instead.
 
 from __future__ import annotations
 
+import ctypes
 import weakref
 from collections import OrderedDict
 
@@ -908,3 +909,32 @@ def _w16_linear_group_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
 @torch.library.register_fake("paroquant::w4a16_linear")
 def _w16_linear_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, input_fp16, out_dtype):
     return x.new_empty((*x.shape[:-1], wpack.size(0) * 16), dtype=out_dtype)
+
+
+# ---------------------------------------------------------------------------
+# weight prefetch (decode): pq_prefetch
+# ---------------------------------------------------------------------------
+
+_PREFETCH_MAX = 16
+
+
+def prefetch(tensors, blocks: int = 0) -> None:
+    """Reads the tensors' device memory once (one load per 128-byte line) on the current stream so that a later
+    kernel finds it in L2 / the Infinity Cache.  Run it on a second stream (same priority) over the weights of
+    the next linears while the current ones compute; it writes nothing and needs no synchronization for
+    correctness.  blocks: workgroups per tensor (0 = the library's default)."""
+    ts = [t for t in tensors if t is not None and t.numel() > 0]
+    if not ts:
+        return
+    dev = ts[0].device
+    lib = _lib.load()
+    for i in range(0, len(ts), _PREFETCH_MAX):
+        chunk = ts[i:i + _PREFETCH_MAX]
+        for t in chunk:
+            _same_device("prefetch tensor", t, dev)
+            _require(t.is_contiguous(), "prefetch: tensors must be contiguous")
+        ptrs = (ctypes.c_void_p * len(chunk))(*[t.data_ptr() for t in chunk])
+        sizes = (ctypes.c_size_t * len(chunk))(*[(t.numel() * t.element_size()) // 4 * 4 for t in chunk])
+        with _DeviceGuard(dev):
+            st = lib.pq_prefetch(ptrs, sizes, len(chunk), int(blocks), _stream(dev))
+        _lib.check(st, "prefetch")

@@ -50,6 +50,9 @@ from .rotation_linear import RotateLinearInt4, Rotation
 
 logger = logging.getLogger(__name__)
 
+# The longest rows the fused linear kernels take; longer ones run rotate -> quant -> GEMM as three ops.
+_FUSED_MAX_K = 16384
+
 # ---------------------------------------------------------------------------
 # bf16 wrapper
 # ---------------------------------------------------------------------------
@@ -371,6 +374,8 @@ class MarlinW4A8Linear(nn.Module):
         """Rotation + int8 quant + GEMM on un-rotated activations x [..., K].  Eagerly it checks that the
         weights are loaded and (re)prepares the rotation's operands when they are stale; under torch.compile
         it expects a prepared rotation (prepare(), or one eager call)."""
+        if self.in_features > _FUSED_MAX_K:
+            return self._forward_unfused(x, rotation, input_fp16, out_dtype, materialize_fp16)
         if not torch.compiler.is_compiling():
             self._check_loaded()
             if not rotation.prepared:
@@ -378,6 +383,21 @@ class MarlinW4A8Linear(nn.Module):
         return torch.ops.paroquant.w4a8_linear(
             x, rotation.rot_idx, rotation.rot_cs, rotation.scales_f32, rotation.krot, self.qweight, self.scales,
             self.bias, input_fp16, materialize_fp16, out_dtype)
+
+    def _forward_unfused(self, x, rotation, input_fp16, out_dtype, materialize_fp16):
+        """The same computation as paroquant::w4a8_linear in three ops, for rows longer than its kernels take
+        (K > 16384): rotation::rotate in float32 (from x rounded to fp16 when input_fp16), the result rounded
+        to fp16 when materialize_fp16, per-token int8 quantization, the GEMM."""
+        if not torch.compiler.is_compiling():
+            self._check_loaded()
+        xin = x.to(torch.float16) if input_fp16 else x
+        xr = torch.ops.rotation.rotate(xin.float(), rotation.pairs, rotation.theta.float(),
+                                       rotation.channel_scales.float(), rotation.group_size)
+        if materialize_fp16:
+            xr = xr.to(torch.float16)
+        xq, xs = torch.ops.paroquant.quant_i8(xr.reshape(-1, self.in_features))
+        y = torch.ops.paroquant.w4a8_gemm(xq, xs, self.qweight, self.scales, self.bias, out_dtype)
+        return y.view(*x.shape[:-1], self.out_features)
 
     def extra_repr(self) -> str:
         return f"in_features={self.in_features}, out_features={self.out_features}, group_size={self.group_size}"

@@ -12,8 +12,9 @@ The same layer with all seven linears called separately is reported next to
 it.  A pool of distinct layers (8 by
 default, 772 MB of weights, so the 256 MB Infinity Cache cannot serve them)
 is captured as ONE HIP graph, the way a model's decode step is captured
-whole; a replay is as many steps as the pool has layers, and --steps is
-rounded up to a whole number of replays.  value = algorithmic bytes
+whole; a replay is as many steps as the pool has layers, and exactly
+--steps steps are timed (whole replays plus a graph of the remaining
+layers) after exactly --warmup untimed ones.  value = algorithmic bytes
 of the layer / time per step, in GB/s, where per linear
   B = N*K/2 + 2*N*K/128 + N*K/256 + 3*8*K + 2*K + 2*M*K + 2*M*N.
 Also reported: M = 4 and 16 decode, M = 3072 prefill in int8 TOPS and % of
@@ -123,8 +124,6 @@ def main() -> int:
                     help="comma-separated decode token counts to time (M = 1 gives value)")
     args = ap.parse_args()
 
-    if args.steps % args.pool_layers:
-        args.steps += args.pool_layers - args.steps % args.pool_layers   # whole replays of the pool graph
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)",
               file=sys.stderr)
@@ -178,10 +177,10 @@ def main() -> int:
             return [*qkv(xa), L[3](xo), *gu(xm), L[6](xd)]
         return [L[0](xa), L[1](xa), L[2](xa), L[3](xo), L[4](xm), L[5](xm), L[6](xd)]
 
-    def capture_layers(M, seed, grouped):
-        """One HIP graph holding the whole pool of layers in sequence, as a
-        model's decode step is captured whole: a replay is len(pool) steps."""
-        xs = make_inputs(M, seed)
+    def capture_layers(M, seed, grouped, n_layers=None):
+        """One HIP graph holding the pool's layers (the first n_layers of them) in sequence, as a
+        model's decode step is captured whole: a replay is that many steps."""
+        xs = make_inputs(M, seed)[:n_layers]
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -192,6 +191,30 @@ def main() -> int:
         with torch.cuda.graph(gr):
             outs = [run_layer(li, X, grouped) for li, X in enumerate(xs)]
         return gr, outs, xs
+
+    def time_exact_steps(M, seed, grouped, steps, warmup):
+        """Exactly `warmup` untimed then exactly `steps` timed layer steps: whole replays of the pool graph plus
+        one replay of a graph of the first (steps mod pool) layers.  Returns ms per step."""
+        P = len(pool)
+        full, _, _ = capture_layers(M, seed, grouped)
+        parts = {}
+        for r in {steps % P, warmup % P} - {0}:
+            parts[r], _, _ = capture_layers(M, seed, grouped, r)
+
+        def run(n):
+            for _ in range(n // P):
+                full.replay()
+            if n % P:
+                parts[n % P].replay()
+
+        run(warmup)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        run(steps)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
 
     def time_graphs(graphs, steps, warmup, warm_s=None):
         # warm up for at least warm_s (default --warm-seconds) of wall time as well as `warmup`
@@ -224,13 +247,10 @@ def main() -> int:
     for M in decode_ms:
         b = sum(linear_bytes(M, N, K) for N, K in shapes)
         for grouped, table in ((True, decode), (False, decode_sep)):
-            gr, _, _ = capture_layers(M, 5000 + M, grouped)
-            # K steps = K / P replays of the pool graph (steps is a multiple of P)
-            ms = time_graphs([gr], args.steps // P, -(-args.warmup // P), warm_s=0.0) / P
+            ms = time_exact_steps(M, 5000 + M, grouped, args.steps, args.warmup)
             table[M] = (ms, b / (ms * 1e-3) / 1e9)
             log(f"decode M={M} {'grouped ' if grouped else 'separate'}: {ms * 1e3:.1f} us/layer, "
                 f"{table[M][1]:.0f} GB/s")
-            del gr
     ms_per_step, value = decode[1]
 
     # ---- roofline of the dominant kernel: the decode GEMM at M = 1 --------
@@ -469,11 +489,11 @@ def main() -> int:
 
         x16 = [tuple(a.to(f16) for a in X) for X in make_inputs(1, 8001)]
         gr, _ = capture16(x16, False, range(P))
-        d_ms = time_graphs([gr], args.steps // P, -(-args.warmup // P)) / P
+        d_ms = time_graphs([gr], -(-args.steps // P), -(-args.warmup // P)) / P
         d_b = sum(w16_linear_bytes(1, N, K) for N, K in shapes)
         del gr
         gr, _ = capture16(x16, False, range(P), grouped=True)
-        dgr_ms = time_graphs([gr], args.steps // P, -(-args.warmup // P)) / P
+        dgr_ms = time_graphs([gr], -(-args.steps // P), -(-args.warmup // P)) / P
         del gr
         gr, _ = capture16(x16, True, range(P))
         dg_ms = time_graphs([gr], max(10, args.steps // 10), 3) / P

@@ -307,6 +307,16 @@ int pq_w4a8_linear_group_rmsnorm(const void* x, const void* residual, const void
                                  int count, int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot,
                                  unsigned flags, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Reads count (0..16) byte ranges of device memory once, one 4-byte load per
+ * 128-byte line, so that a kernel launched later finds those lines in the
+ * GPU's caches (L2 and the Infinity Cache in front of HBM).  For decode, where
+ * each linear's rotation launch leaves HBM idle: run it on a second stream of
+ * the same priority over the next linears' wpack / wmeta.  Each range
+ * pointer 4-byte aligned, each size a multiple of 4 (0 = skipped); blocks =
+ * workgroups per range (0 = 64).  Writes nothing.  No counterpart in the
+ * reference. */
+int pq_prefetch(const void* const* ptrs, const size_t* bytes, int count, int blocks, void* stream);
+
 /* ---- W4A16 (fp16 activations, no activation quant) ---- */
 
 /* Repack WQLinear weights for pq_w4a16_gemm: awq_qweight int32 [k, n/8] (the

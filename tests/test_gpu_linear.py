@@ -206,3 +206,17 @@ def test_linear_op_input_dtypes(M, dtype):
     q, sx = oquant.quant_int8_per_token(v)
     ref = ogemm.w4a8_linear(q, sx, spec.w.codes.numpy(), spec.w.awq_scales.numpy(), spec.w.zeros.numpy(), None)
     assert_bf16_close(to_np(y), ref)
+
+
+@pytest.mark.parametrize("M", [1, 20])
+def test_rows_longer_than_the_fused_kernels(M):
+    """K = 16512 (> 16384, the fused kernels' limit) runs rotate -> quant -> GEMM as three ops with the same
+    semantics; against the oracle."""
+    N, K = 64, 16384 + 128
+    spec = workloads.linear_spec("long", N, K, workloads.generator(1300 + M), keep_codes=True)
+    mod = workloads.build_module(spec, "cuda")
+    x = workloads.activations(M, K, workloads.generator(1400 + M))
+    y = mod(x.cuda())
+    ref, _, _ = _oracle_linear(spec, to_np(x))
+    assert y.shape == (M, N) and y.dtype == torch.bfloat16
+    assert_bf16_close(to_np(y), ref)
