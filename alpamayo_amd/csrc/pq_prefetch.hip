@@ -4,10 +4,11 @@
 //
 // Decode-size linears are latency-bound launch chains: the rotation kernel of
 // a linear moves almost no bytes, and the GEMM streams its weights at about
-// half of HBM's bandwidth.  The weights of the next linears are known in
-// advance, so a caller can run this kernel on a second stream of the same
-// priority while the current linears compute, moving the next weights out of
-// HBM while it would otherwise idle.  No counterpart in the reference.
+// half of HBM's bandwidth.  This kernel reads a linear's weights ahead of its
+// GEMM.  Measured at one token on the Qwen3-8B layer: the GEMM then runs
+// 0.4-1.4 us faster, but the reads take about 6 us per linear, so the linear
+// path does not use it; it stays as a measurement option.  No counterpart in
+// the reference.
 #include "pq_common.h"
 
 namespace {

@@ -920,9 +920,10 @@ _PREFETCH_MAX = 16
 
 def prefetch(tensors, blocks: int = 0) -> None:
     """Reads the tensors' device memory once (one load per 128-byte line) on the current stream so that a later
-    kernel finds it in L2 / the Infinity Cache.  Run it on a second stream (same priority) over the weights of
-    the next linears while the current ones compute; it writes nothing and needs no synchronization for
-    correctness.  blocks: workgroups per tensor (0 = the library's default)."""
+    kernel finds it in L2 / the Infinity Cache.  It writes nothing and needs no synchronization for
+    correctness.  A measurement option (bench.py --decode-prefetch): at one decode token the reads cost more
+    than the GEMM saves, so the linear path does not call it.  blocks: workgroups per tensor (0 = the
+    library's default)."""
     ts = [t for t in tensors if t is not None and t.numel() > 0]
     if not ts:
         return

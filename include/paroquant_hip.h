@@ -309,12 +309,14 @@ int pq_w4a8_linear_group_rmsnorm(const void* x, const void* residual, const void
 
 /* Reads count (0..16) byte ranges of device memory once, one 4-byte load per
  * 128-byte line, so that a kernel launched later finds those lines in the
- * GPU's caches (L2 and the Infinity Cache in front of HBM).  For decode, where
- * each linear's rotation launch leaves HBM idle: run it on a second stream of
- * the same priority over the next linears' wpack / wmeta.  Each range
- * pointer 4-byte aligned, each size a multiple of 4 (0 = skipped); blocks =
- * workgroups per range (0 = 64).  Writes nothing.  No counterpart in the
- * reference. */
+ * GPU's caches (L2 and the Infinity Cache in front of HBM).  A measurement
+ * option, not part of the linear path: at one decode token a GEMM whose
+ * weights were read ahead runs 0.4-1.4 us faster, but reading them costs
+ * about 6 us per linear on the same stream, and on a second stream of the
+ * same priority the two branches of a captured graph compete for HBM.  Each
+ * range pointer 4-byte aligned, each size a multiple of 4 (0 = skipped);
+ * blocks = workgroups per range (0 = 64).  Writes nothing.  No counterpart in
+ * the reference. */
 int pq_prefetch(const void* const* ptrs, const size_t* bytes, int count, int blocks, void* stream);
 
 /* ---- W4A16 (fp16 activations, no activation quant) ---- */
