@@ -206,7 +206,11 @@ __device__ __forceinline__ float row_sumsq(const void* __restrict__ x, const voi
   // The loads of kB chunks are issued together (indices clamped into the row,
   // so they stay unconditional); the sum then runs over the chunks in the
   // same order as one chunk at a time, so the result does not change.
+  // The residual loads are unconditional too (from x when there is none): a
+  // load under a branch made the compiler wait for every load at the join,
+  // one round trip per chunk.
   constexpr int kB = 4;
+  const void* rs = res != nullptr ? res : x;
   float acc = 0.0f;
   for (int c0 = lane * 8; c0 < h; c0 += 512 * kB) {
     float f[kB][8], r[kB][8];
@@ -214,7 +218,7 @@ __device__ __forceinline__ float row_sumsq(const void* __restrict__ x, const voi
     for (int b = 0; b < kB; ++b) {
       const int c8 = min(c0 + 512 * b, h - 8);
       load8_as_f32<DT>(x, row_off + c8, f[b]);
-      if (res != nullptr) load8_as_f32<DT>(res, row_off + c8, r[b]);
+      load8_as_f32<DT>(rs, row_off + c8, r[b]);
     }
 #pragma unroll
     for (int b = 0; b < kB; ++b) {
@@ -301,13 +305,25 @@ __device__ __forceinline__ void rotate_group_rows(const void* __restrict__ x, co
     xhi[m] = pq_raw_to_f32<DT>(xb[m]);
   }
   if constexpr (NORM) {
+    // the second operand of the group (residual or up projection), loaded
+    // unconditionally (from x when there is none) so that no load waits
+    // behind a branch
+    const void* np = nres != nullptr ? nres : x;
+    float nlo[MR], nhi[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const int mm = m < M ? m : M - 1;
+      const int64_t ro = static_cast<int64_t>(mm) * h;
+      nlo[m] = pq_load_as_f32<DT>(np, ro + g * 128 + lane);
+      nhi[m] = pq_load_as_f32<DT>(np, ro + g * 128 + 64 + lane);
+    }
     if (mode == PQ_PRO_SWIGLU) {
 #pragma unroll
       for (int m = 0; m < MR; ++m) {
         const int mm = m < M ? m : M - 1;
         const int64_t ro = static_cast<int64_t>(mm) * h;
-        xlo[m] = swiglu<DT>(xlo[m], pq_load_as_f32<DT>(nres, ro + g * 128 + lane));
-        xhi[m] = swiglu<DT>(xhi[m], pq_load_as_f32<DT>(nres, ro + g * 128 + 64 + lane));
+        xlo[m] = swiglu<DT>(xlo[m], nlo[m]);
+        xhi[m] = swiglu<DT>(xhi[m], nhi[m]);
         if (m < M && h_out != nullptr) {
           pq_store_from_f32<DT>(h_out, ro + g * 128 + lane, xlo[m]);
           pq_store_from_f32<DT>(h_out, ro + g * 128 + 64 + lane, xhi[m]);
@@ -323,8 +339,8 @@ __device__ __forceinline__ void rotate_group_rows(const void* __restrict__ x, co
         const int64_t ro = static_cast<int64_t>(mm) * h;
         const float r = norm ? rms_inv(row_sumsq<DT>(x, nres, ro, h, lane), h, eps) : 1.0f;
         if (nres != nullptr) {
-          xlo[m] = round_to_dt<DT>(xlo[m] + pq_load_as_f32<DT>(nres, ro + g * 128 + lane));
-          xhi[m] = round_to_dt<DT>(xhi[m] + pq_load_as_f32<DT>(nres, ro + g * 128 + 64 + lane));
+          xlo[m] = round_to_dt<DT>(xlo[m] + nlo[m]);
+          xhi[m] = round_to_dt<DT>(xhi[m] + nhi[m]);
         }
         if (m < M && s_out != nullptr) {
           pq_store_from_f32<DT>(s_out, ro + g * 128 + lane, xlo[m]);

@@ -315,20 +315,22 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
       w1 = pq_load_raw<DT>(nwp, g * 128 + 64 + lane);
     }
   };
-  if (pro_norm) {
-    if (w < RB) {
-      const float r = pqd::rms_inv(pqd::row_sumsq<DT>(x, nm.res, (row0 + w) * h, h, lane), h, nm.eps);
-      if (lane == 0) s_rinv[w] = r;
-    }
-    __syncthreads();
-  }
-  const bool write_norm = NORM && blockIdx.y == 0;   // the same for every member: member 0 writes
-
+  // the first group's loads go out before the RMSNorm factor is reduced, so
+  // they are in flight while waves 0..RB-1 sum their rows
   if (w < G) {
     pqd::load_rot_lane<KP>(rot_idx, rot_cs, w, lane, rl[0]);
     load_inputs(w, xa[0], xb[0], sa[0], sb[0]);
     load_norm(w, ra[0], rb[0], wa[0], wb[0]);
   }
+  if (pro_norm) {
+    if (w < RB) {
+      const float r = pqd::rms_inv(pqd::row_sumsq<DT>(x, nm.res, (row0 + w) * h, h, lane), h, nm.eps);
+      if (lane == 0) s_rinv[w] = r;
+    }
+    pqd::lds_barrier();   // s_rinv is written (LDS only: the loads above stay in flight)
+  }
+  const bool write_norm = NORM && blockIdx.y == 0;   // the same for every member: member 0 writes
+
   for (int g0 = w; g0 < G; g0 += 2 * kRQWaves) {
 #pragma unroll
     for (int ph = 0; ph < 2; ++ph) {
