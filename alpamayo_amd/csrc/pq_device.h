@@ -200,7 +200,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 // wave: lane l sums the 8-element chunks 8l, 8l + 512, ... in order (each
 // square rounded, then added), then the butterfly.  Every wave that calls it
 // on the same row gets the same bits.
-template <int DT>
+template <int DT, int kB = 4>
 __device__ __forceinline__ float row_sumsq(const void* __restrict__ x, const void* __restrict__ res, int64_t row_off,
                                            int h, int lane) {
   // The loads of kB chunks are issued together (indices clamped into the row,
@@ -209,7 +209,6 @@ __device__ __forceinline__ float row_sumsq(const void* __restrict__ x, const voi
   // The residual loads are unconditional too (from x when there is none): a
   // load under a branch made the compiler wait for every load at the join,
   // one round trip per chunk.
-  constexpr int kB = 4;
   const void* rs = res != nullptr ? res : x;
   float acc = 0.0f;
   for (int c0 = lane * 8; c0 < h; c0 += 512 * kB) {
@@ -337,7 +336,7 @@ __device__ __forceinline__ void rotate_group_rows(const void* __restrict__ x, co
       for (int m = 0; m < MR; ++m) {
         const int mm = m < M ? m : M - 1;
         const int64_t ro = static_cast<int64_t>(mm) * h;
-        const float r = norm ? rms_inv(row_sumsq<DT>(x, nres, ro, h, lane), h, eps) : 1.0f;
+        const float r = norm ? rms_inv(row_sumsq<DT, MR <= 4 ? 8 : 4>(x, nres, ro, h, lane), h, eps) : 1.0f;
         if (nres != nullptr) {
           xlo[m] = round_to_dt<DT>(xlo[m] + nlo[m]);
           xhi[m] = round_to_dt<DT>(xhi[m] + nhi[m]);

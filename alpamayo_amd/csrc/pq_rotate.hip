@@ -324,7 +324,7 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
   }
   if (pro_norm) {
     if (w < RB) {
-      const float r = pqd::rms_inv(pqd::row_sumsq<DT>(x, nm.res, (row0 + w) * h, h, lane), h, nm.eps);
+      const float r = pqd::rms_inv(pqd::row_sumsq<DT, 8>(x, nm.res, (row0 + w) * h, h, lane), h, nm.eps);
       if (lane == 0) s_rinv[w] = r;
     }
     pqd::lds_barrier();   // s_rinv is written (LDS only: the loads above stay in flight)
