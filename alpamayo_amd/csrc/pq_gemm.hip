@@ -117,30 +117,27 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
   float gm[kPreMax];
   uint4 pre[kPre][AQ == 2 ? 2 : 1];
   bool preloaded = false;
+  // All of these loads are unconditional, with clamped indices (their values
+  // are used only where the index is in range): behind a branch, the
+  // compiler's wait before their first use also waited for the weight
+  // blocks issued after them, which put the whole prologue behind the
+  // weights' round trip.
   if constexpr (AQ != 0) {
 #pragma unroll
-    for (int q = 0; q < kPreMax; ++q) {
-      const int i = threadIdx.x + q * nthr;
-      gm[q] = i < M * G ? gmax[i] : 0.0f;
-    }
+    for (int q = 0; q < kPreMax; ++q) gm[q] = gmax[min(static_cast<int>(threadIdx.x) + q * nthr, M * G - 1)];
     preloaded = M * k8 <= kPre * nthr;
-    if (preloaded) {
 #pragma unroll
-      for (int q = 0; q < kPre; ++q) {
-        const int e = threadIdx.x + q * nthr;
-        if (e < M * k8) {
-          const int r = e / k8;
-          const int c8 = (e - r * k8) * 8;
-          if constexpr (AQ == 1) {
-            pre[q][0] =
-                *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(xr) + static_cast<int64_t>(r) * K + c8);
-          } else {
-            const uint4* src =
-                reinterpret_cast<const uint4*>(static_cast<const float*>(xr) + static_cast<int64_t>(r) * K + c8);
-            pre[q][0] = src[0];
-            pre[q][AQ == 2 ? 1 : 0] = src[1];
-          }
-        }
+    for (int q = 0; q < kPre; ++q) {
+      const int e = min(static_cast<int>(threadIdx.x) + q * nthr, M * k8 - 1);
+      const int r = e / k8;
+      const int c8 = (e - r * k8) * 8;
+      if constexpr (AQ == 1) {
+        pre[q][0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(xr) + static_cast<int64_t>(r) * K + c8);
+      } else {
+        const uint4* src =
+            reinterpret_cast<const uint4*>(static_cast<const float*>(xr) + static_cast<int64_t>(r) * K + c8);
+        pre[q][0] = src[0];
+        pre[q][AQ == 2 ? 1 : 0] = src[1];
       }
     }
   }
@@ -158,8 +155,11 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
     v4i a0[U], a1[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int g = g0 + W * u;
-      if (g < G) {
+      // with the AQ prologue, a group past G loads group G-1 (unused) rather
+      // than branching around the loads (see the prologue); without it the
+      // branch measured faster
+      const int g = AQ != 0 ? min(g0 + W * u, G - 1) : g0 + W * u;
+      if (AQ != 0 || g < G) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const int64_t blk = static_cast<int64_t>(tile0 + nt) * G + g;
