@@ -127,6 +127,17 @@ __device__ __forceinline__ void load_rot_lane(const uint32_t* __restrict__ rot_i
   }
 }
 
+// Ties the lane's operands to this point of the program: the compiler
+// otherwise sinks the load of a layer's cos/sin into that layer's
+// `layer < krot` branch, where it costs a round trip of its own.
+template <int KP>
+__device__ __forceinline__ void pin_rot_lane(RotLane<KP>& p) {
+#pragma unroll
+  for (int i = 0; i < 2 * KP; ++i) asm volatile("" : "+v"(p.cs[i]));
+#pragma unroll
+  for (int i = 0; i < KP / 2; ++i) asm volatile("" : "+v"(p.w[i]));
+}
+
 template <int KP>
 __device__ __forceinline__ bool rot_init_swapped(const RotLane<KP>& p) { return (p.w[0] >> 16) & 1u; }
 template <int KP>
@@ -295,6 +306,7 @@ __device__ __forceinline__ void rotate_group_rows(const void* __restrict__ x, co
   const float s0r = sp[(g * 128 + lane) & smask];
   const float s1r = sp[(g * 128 + 64 + lane) & smask];
   const float s0 = has_scales ? s0r : 1.0f, s1 = has_scales ? s1r : 1.0f;
+  pin_rot_lane<KP>(p);
   const bool sw = rot_init_swapped(p);
   float a[MR], b[MR];
   float xlo[MR], xhi[MR];
