@@ -614,6 +614,20 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn)
     bv[tn] = has_bias ? pq_load_dyn(bias, bias_dtype, min(bn * BN + bcol[tn], N - 1)) : 0.0f;
+  // This lane's activation scales, all read up front: rows 8j + 4hj .. +3 of
+  // a 32-row tile are one 16-byte LDS read.  Read per value inside the slice
+  // loop, each was an LDS round trip in front of its row's conversions.
+  float xsv[TM][16];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4 x4 = *reinterpret_cast<const float4*>(xs_tile + wm * (BM / WM) + tm * 32 + 8 * j + 4 * hj);
+      xsv[tm][4 * j] = x4.x;
+      xsv[tm][4 * j + 1] = x4.y;
+      xsv[tm][4 * j + 2] = x4.z;
+      xsv[tm][4 * j + 3] = x4.w;
+    }
   auto emit = [&](auto out_dtype) {
     constexpr int DT = decltype(out_dtype)::value;
     constexpr int ESZ = DT == PQ_F32 ? 4 : 2;
@@ -625,10 +639,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int r = 8 * (v >> 2) + 4 * hj + (v & 3);
-        const float xsm = xs_tile[wm * (BM / WM) + tm * 32 + r];
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn) {
-          float val = acc[tm][tn][v] * xsm;
+          float val = acc[tm][tn][v] * xsv[tm][v];
           if (has_bias) val = val + bv[tn];
           uint8_t* dst = smem + (wm * 32 + r) * PITCH + bcol[tn] * ESZ;
           if constexpr (DT == PQ_F32) *reinterpret_cast<float*>(dst) = val;
