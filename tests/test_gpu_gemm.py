@@ -93,6 +93,20 @@ def test_gemm_bias_f32_out(M, N, K):
     assert_bf16_close(to_np(y), ref)
 
 
+@pytest.mark.parametrize("M,N,K", [(5, 1024, 4096), (200, 1552, 384), (1500, 8176, 384)])
+def test_gemm_16bit_outputs_are_rounded_f32(M, N, K):
+    """bf16 and fp16 outputs are the float32 output rounded to nearest even (torch's conversion), bit for bit,
+    on the decode kernel, the small-tile and the 192 x 256 prefill kernels: every output type computes the same
+    float32 value and converts it last (v_cvt_pk_bf16_f32 / v_cvt_f16_f32)."""
+    w, xq, xs = _case(M, N, K, 11 + M)
+    wp, wm = _prepack(w)
+    bias = torch.randn(N, generator=workloads.generator(12 + M)).half().cuda()
+    y32 = torch.ops.paroquant.w4a8_gemm(xq.cuda(), xs.cuda(), wp, wm, bias, torch.float32)
+    for dt in (torch.bfloat16, torch.float16):
+        y = torch.ops.paroquant.w4a8_gemm(xq.cuda(), xs.cuda(), wp, wm, bias, dt)
+        assert torch.equal(y.view(torch.int16), y32.to(dt).view(torch.int16)), dt
+
+
 def test_gemm_extreme_operands_exact():
     """All codes 15 vs zero 0 and activations -128/127: the largest partials are still exact."""
     M, N, K = 20, 32, 256

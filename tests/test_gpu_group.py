@@ -59,6 +59,9 @@ CASES = [
     (17, 1024, (48, 1552)),
     (300, 4096, (4096, 1024, 1024)),
     (1100, 2048, (1040, 2064, 16)),
+    # 192 x 256 tiles past one round: the leading members that fill whole rounds run as a launch of their own
+    (1536, 256, (8192, 1024, 1024)),
+    (768, 128, (8192, 8192, 2048)),
 ]
 
 

@@ -124,6 +124,22 @@ def test_gemm_bias_and_output_dtypes(m, out_dtype, bias_dtype):
     _check(y, ref, out_dtype)
 
 
+@pytest.mark.parametrize("m", [3, 300])
+def test_gemm_16bit_outputs_are_rounded_f32(m):
+    """bf16 and fp16 outputs equal the float32 output rounded to nearest even by torch, bit for bit (decode and
+    prefill kernels): the conversion is the last step."""
+    n, k = 512, 1024
+    w, s, sz = _case(n, k, 3700)
+    wpack, wmeta = _prepack(w, s, sz)
+    gen = workloads.generator(3701 + m)
+    x = torch.randn(m, k, generator=gen).to(torch.float16).cuda()
+    bias = torch.randn(n, generator=gen).to(torch.float16).cuda()
+    y32 = torch.ops.paroquant.w4a16_gemm(x, wpack, wmeta, bias, torch.float32)
+    for dt in (torch.bfloat16, torch.float16):
+        y = torch.ops.paroquant.w4a16_gemm(x, wpack, wmeta, bias, dt)
+        assert torch.equal(y.view(torch.int16), y32.to(dt).view(torch.int16)), dt
+
+
 def test_gemm_empty_and_leading_dims():
     n, k = 256, 512
     w, s, sz = _case(n, k, 3700)
