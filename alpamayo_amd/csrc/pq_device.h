@@ -168,6 +168,22 @@ __device__ __forceinline__ void rot_layer(const RotLane<KP>& p, int r, float (&a
   }
 }
 
+// All Givens layers of one group.  With krot == KP (the usual KROT) the
+// layers run as one straight-line block; with fewer, each layer sits behind
+// a uniform branch on its index, whose condition the compiler evaluates with
+// VALU instructions in every layer (6-9 % of the row kernel's time).
+template <int KP, int N>
+__device__ __forceinline__ void rot_layers(const RotLane<KP>& p, int krot, float (&a)[N], float (&b)[N]) {
+  if (krot == KP) {
+#pragma unroll
+    for (int k = 0; k < KP; ++k) rot_layer<KP, N>(p, k, a, b);
+  } else {
+#pragma unroll
+    for (int k = 0; k < KP; ++k)
+      if (k < krot) rot_layer<KP, N>(p, k, a, b);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // RMSNorm prologue (reference: Qwen3VLTextRMSNorm.forward,
 // src/alpamayo_r1/models/qwen3_vl/modeling_qwen3_vl.py:354-359):
@@ -376,9 +392,7 @@ __device__ __forceinline__ void rotate_group_rows(const void* __restrict__ x, co
     a[m] = sw ? hi : lo;
     b[m] = sw ? lo : hi;
   }
-#pragma unroll
-  for (int k = 0; k < KP; ++k)
-    if (k < krot) rot_layer<KP, MR>(p, k, a, b);
+  rot_layers<KP, MR>(p, krot, a, b);
   const int fa = g * 128 + rot_final_a(p), fb = g * 128 + rot_final_b(p);
 #pragma unroll
   for (int m = 0; m < MR; ++m) {

@@ -378,9 +378,7 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
         a[r] = sw ? hi : lo;
         b[r] = sw ? lo : hi;
       }
-#pragma unroll
-      for (int k = 0; k < KP; ++k)
-        if (k < krot) pqd::rot_layer<KP, RB>(cur, k, a, b);
+      pqd::rot_layers<KP, RB>(cur, krot, a, b);
       const int fa = g * 128 + pqd::rot_final_a(cur), fb = g * 128 + pqd::rot_final_b(cur);
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
