@@ -358,7 +358,9 @@ def main() -> int:
                 torch.ops.paroquant.w4a8_gemm(q8, s8, q.qweight, q.scales, None, torch.bfloat16)
         gms = time_graphs([gg], args.prefill_steps, 3)
         gtops = ops / (gms * 1e-3) / 1e12
-        # each shape's GEMM alone (q, k, gate, down; o, v, up repeat a shape)
+        # each shape's GEMM alone (q, k, gate, down; o, v, up repeat a shape): REP launches per graph,
+        # so that the gap between two graph replays is not charged to one kernel
+        REP = 4
         per_shape = {}
         for idx in (0, 1, 4, 6):
             m = L[idx]
@@ -366,19 +368,37 @@ def main() -> int:
             q8, s8 = xq[idx]
             g1 = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g1):
-                torch.ops.paroquant.w4a8_gemm(q8, s8, q.qweight, q.scales, None, torch.bfloat16)
-            sms = time_graphs([g1], args.prefill_steps, 3)
+                for _ in range(REP):
+                    torch.ops.paroquant.w4a8_gemm(q8, s8, q.qweight, q.scales, None, torch.bfloat16)
+            sms = time_graphs([g1], args.prefill_steps, 3) / REP
             sops = 2 * M * q.out_features * q.in_features
             per_shape[f"{q.out_features}x{q.in_features}"] = {
                 "us": round(sms * 1e3, 1), "pct_int8_peak": round(100 * sops / (sms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 2)}
             del g1
         log("prefill GEMM per shape (N x K): " + ", ".join(f"{k} {v['us']} us ({v['pct_int8_peak']}%)"
                                                            for k, v in per_shape.items()))
+        # the rotate + int8 quant launch of one linear alone (bf16 rows in, int8 codes + token scales out)
+        rq_shape = {}
+        for idx in (0, 6):
+            r = L[idx].rotate_linear.rotation
+            x = (X[0], X[0], X[0], X[1], X[2], X[2], X[3])[idx]
+            K = x.shape[-1]
+            g1 = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g1):
+                for _ in range(REP):
+                    torch.ops.paroquant.rotate_quant_i8(x, r.rot_idx, r.rot_cs, r.scales_f32, r.krot, True, True)
+            sms = time_graphs([g1], args.prefill_steps, 3) / REP
+            gbps = (2 * M * K + M * K + 4 * M) / (sms * 1e-3) / 1e9
+            rq_shape[str(K)] = {"us": round(sms * 1e3, 1), "GBps": round(gbps, 1),
+                                "frac_hbm": round(gbps / HBM_PEAK_GBS, 4)}
+            del g1
+        log("prefill rotate+quant per K: " + ", ".join(f"K={k} {v['us']} us ({v['GBps']} GB/s)"
+                                                       for k, v in rq_shape.items()))
         prefill = {"ms_per_layer": round(ms, 4), "tops": round(tops, 1),
                    "pct_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2),
                    "separate_linears_ms_per_layer": round(res[False], 4), "separate_linears_tops": round(tops_sep, 1),
                    "gemm_only_tops": round(gtops, 1), "gemm_only_pct_int8_peak": round(100 * gtops / INT8_PEAK_TOPS, 2),
-                   "gemm_per_shape": per_shape}
+                   "gemm_per_shape": per_shape, "rotate_quant_per_K": rq_shape}
         log(f"prefill M=3072: {ms:.3f} ms/layer grouped, {tops:.0f} TOPS ({prefill['pct_int8_peak']}%); "
             f"separate {res[False]:.3f} ms/layer, {tops_sep:.0f} TOPS; GEMMs alone {gtops:.0f} TOPS")
         del gg, xq, X
@@ -574,8 +594,9 @@ def main() -> int:
                 torch.ops.paroquant.w4a16_gemm(x, wp, wm16, None, f16)
                 g1 = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(g1):
-                    torch.ops.paroquant.w4a16_gemm(x, wp, wm16, None, f16)
-                sms = time_graphs([g1], args.prefill_steps, 3)
+                    for _ in range(4):
+                        torch.ops.paroquant.w4a16_gemm(x, wp, wm16, None, f16)
+                sms = time_graphs([g1], args.prefill_steps, 3) / 4
                 per_shape[f"{N}x{K}"] = {"us": round(sms * 1e3, 1),
                                          "pct_fp16_peak": round(100 * 2 * M * N * K / (sms * 1e-3) / 1e12
                                                                 / FP16_PEAK_TFLOPS, 2)}
