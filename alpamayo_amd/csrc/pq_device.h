@@ -396,20 +396,20 @@ __device__ __forceinline__ void rotate_group_rows(const void* __restrict__ x, co
   const int fa = g * 128 + rot_final_a(p), fb = g * 128 + rot_final_b(p);
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
-    float va = a[m], vb = b[m];
+    const float va = a[m], vb = b[m];
     if (m < M) {
       if constexpr (MAT16) {
-        const uint16_t ha = pq_f32_to_f16(va), hb = pq_f32_to_f16(vb);
-        static_cast<uint16_t*>(xr)[static_cast<int64_t>(m) * h + fa] = ha;
-        static_cast<uint16_t*>(xr)[static_cast<int64_t>(m) * h + fb] = hb;
-        va = pq_f16_to_f32(ha);
-        vb = pq_f16_to_f32(hb);
+        static_cast<uint16_t*>(xr)[static_cast<int64_t>(m) * h + fa] = pq_f32_to_f16(va);
+        static_cast<uint16_t*>(xr)[static_cast<int64_t>(m) * h + fb] = pq_f32_to_f16(vb);
       } else {
         static_cast<float*>(xr)[static_cast<int64_t>(m) * h + fa] = va;
         static_cast<float*>(xr)[static_cast<int64_t>(m) * h + fb] = vb;
       }
     }
-    const float mx = pq_wave_max(fmaxf(fabsf(va), fabsf(vb)));
+    // the group's absmax of the stored rows: rounding to fp16 is monotonic,
+    // so it is the float32 absmax rounded once
+    float mx = pq_wave_max(fmaxf(fabsf(va), fabsf(vb)));
+    if constexpr (MAT16) mx = pq_round_f16(mx);
     if (m < M && lane == 0) gmax[static_cast<int64_t>(m) * G + g] = mx;
   }
 }

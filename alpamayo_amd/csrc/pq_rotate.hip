@@ -382,17 +382,16 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
       const int fa = g * 128 + pqd::rot_final_a(cur), fb = g * 128 + pqd::rot_final_b(cur);
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
-        float vi = a[r], vj = b[r];
+        const float vi = a[r], vj = b[r];
         if constexpr (MAT16) {
-          const uint16_t hi = pq_f32_to_f16(vi), hj = pq_f32_to_f16(vj);
-          rowbuf[r * h + fa] = hi;
-          rowbuf[r * h + fb] = hj;
-          vi = pq_f16_to_f32(hi);
-          vj = pq_f16_to_f32(hj);
+          rowbuf[r * h + fa] = pq_f32_to_f16(vi);
+          rowbuf[r * h + fb] = pq_f32_to_f16(vj);
         } else {
           rowbuf[r * h + fa] = vi;
           rowbuf[r * h + fb] = vj;
         }
+        // the float32 values: rounding to fp16 is monotonic, so the row's
+        // fp16 absmax is its float32 absmax rounded once (below)
         rmax[r] = fmaxf(rmax[r], fmaxf(fabsf(vi), fabsf(vj)));
       }
     }
@@ -480,6 +479,7 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
     float am = 0.0f;
 #pragma unroll
     for (int ww = 0; ww < kRQWaves; ++ww) am = fmaxf(am, red[ww][t]);
+    if constexpr (MAT16) am = pq_round_f16(am);   // = the absmax of the fp16 rows
     s_am[t] = am;
     s_inv[t] = pqd::inv_scale(am);
   }
