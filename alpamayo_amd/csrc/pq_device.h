@@ -17,8 +17,35 @@ __device__ __forceinline__ uint32_t quant1(float v, float inv) {
   return static_cast<uint32_t>(static_cast<int>(r)) & 0xffu;
 }
 
+// The code as an int32 (only its low byte is used), from a product that is
+// already formed.
+__device__ __forceinline__ uint32_t quant_scaled(float p) {
+  const float r = fminf(fmaxf(__builtin_rintf(p), -128.0f), 127.0f);
+  return static_cast<uint32_t>(static_cast<int>(r));
+}
+
+// Low bytes of four codes, a in byte 0: three byte permutes.
+__device__ __forceinline__ uint32_t pack4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);
+  const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
+}
+
 __device__ __forceinline__ uint32_t quant4(float a, float b, float c, float d, float inv) {
-  return quant1(a, inv) | (quant1(b, inv) << 8) | (quant1(c, inv) << 16) | (quant1(d, inv) << 24);
+  return pack4(quant_scaled(a * inv), quant_scaled(b * inv), quant_scaled(c * inv), quant_scaled(d * inv));
+}
+
+// Four codes from two dwords of fp16 values.  fma(h, inv, +0) differs from
+// h * inv only in the sign of a zero product, which rounds to the same code;
+// the form lets the fp16 -> float32 conversion ride in v_fma_mix_f32.
+__device__ __forceinline__ float mul_f16(uint32_t w, bool hi, float inv) {
+  const _Float16 h = __builtin_bit_cast(_Float16, static_cast<uint16_t>(hi ? w >> 16 : w & 0xffffu));
+  return __builtin_fmaf(static_cast<float>(h), inv, 0.0f);
+}
+
+__device__ __forceinline__ uint32_t quant4_f16(uint32_t w01, uint32_t w23, float inv) {
+  return pack4(quant_scaled(mul_f16(w01, false, inv)), quant_scaled(mul_f16(w01, true, inv)),
+               quant_scaled(mul_f16(w23, false, inv)), quant_scaled(mul_f16(w23, true, inv)));
 }
 
 __device__ __forceinline__ float inv_scale(float absmax) { return absmax > 0.0f ? 127.0f / absmax : 0.0f; }

@@ -193,24 +193,17 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
         auto quant8 = [&](int e, const uint4* v) {
           const int r = e / k8;
           const int c8 = (e - r * k8) * 8;
-          float f[8];
-          if constexpr (AQ == 1) {
-            const uint32_t wds[4] = {v[0].x, v[0].y, v[0].z, v[0].w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              f[2 * q] = pq_f16_to_f32(static_cast<uint16_t>(wds[q] & 0xffffu));
-              f[2 * q + 1] = pq_f16_to_f32(static_cast<uint16_t>(wds[q] >> 16));
-            }
-          } else {
-            f[0] = __uint_as_float(v[0].x); f[1] = __uint_as_float(v[0].y);
-            f[2] = __uint_as_float(v[0].z); f[3] = __uint_as_float(v[0].w);
-            f[4] = __uint_as_float(v[AQ == 2 ? 1 : 0].x); f[5] = __uint_as_float(v[AQ == 2 ? 1 : 0].y);
-            f[6] = __uint_as_float(v[AQ == 2 ? 1 : 0].z); f[7] = __uint_as_float(v[AQ == 2 ? 1 : 0].w);
-          }
           const float inv = inv_scale(s_amax[r]);
           uint2 o;
-          o.x = quant4(f[0], f[1], f[2], f[3], inv);
-          o.y = quant4(f[4], f[5], f[6], f[7], inv);
+          if constexpr (AQ == 1) {
+            o.x = quant4_f16(v[0].x, v[0].y, inv);
+            o.y = quant4_f16(v[0].z, v[0].w, inv);
+          } else {
+            const uint4 b = v[AQ == 2 ? 1 : 0];
+            o.x = quant4(__uint_as_float(v[0].x), __uint_as_float(v[0].y), __uint_as_float(v[0].z),
+                         __uint_as_float(v[0].w), inv);
+            o.y = quant4(__uint_as_float(b.x), __uint_as_float(b.y), __uint_as_float(b.z), __uint_as_float(b.w), inv);
+          }
           *reinterpret_cast<uint2*>(aq + r * astride + c8) = o;
         };
         if (preloaded) {

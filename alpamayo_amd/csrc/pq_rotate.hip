@@ -493,15 +493,10 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
     const float am = s_am[r];
     const float inv = s_inv[r];
     float f[8];
+    uint4 u16{};
     if constexpr (MAT16) {
-      const uint4 u = *reinterpret_cast<const uint4*>(rowbuf + r * h + c8);
-      const uint32_t wds[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        f[2 * q] = pq_f16_to_f32(static_cast<uint16_t>(wds[q] & 0xffffu));
-        f[2 * q + 1] = pq_f16_to_f32(static_cast<uint16_t>(wds[q] >> 16));
-      }
-      if (xrot != nullptr) *reinterpret_cast<uint4*>(xrot + (row0 + r) * h + c8) = u;
+      u16 = *reinterpret_cast<const uint4*>(rowbuf + r * h + c8);
+      if (xrot != nullptr) *reinterpret_cast<uint4*>(xrot + (row0 + r) * h + c8) = u16;
     } else {
       const float4 a = *reinterpret_cast<const float4*>(rowbuf + r * h + c8);
       const float4 b = *reinterpret_cast<const float4*>(rowbuf + r * h + c8 + 4);
@@ -518,8 +513,13 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
     }
     if (xq != nullptr) {   // null: only the fp16 rows are wanted (the W4A16 linear)
       uint2 o;
-      o.x = quant4(f[0], f[1], f[2], f[3], inv);
-      o.y = quant4(f[4], f[5], f[6], f[7], inv);
+      if constexpr (MAT16) {
+        o.x = pqd::quant4_f16(u16.x, u16.y, inv);
+        o.y = pqd::quant4_f16(u16.z, u16.w, inv);
+      } else {
+        o.x = quant4(f[0], f[1], f[2], f[3], inv);
+        o.y = quant4(f[4], f[5], f[6], f[7], inv);
+      }
       *reinterpret_cast<uint2*>(xq + (row0 + r) * h + c8) = o;
       if (c8 == 0) xscale[row0 + r] = am / 127.0f;
     }
@@ -581,25 +581,18 @@ __global__ __launch_bounds__(256) void quant_split_kernel(const pq::QuantGroup g
   const int c8 = (blockIdx.x * 256 + threadIdx.x) * 8;
   if (c8 >= h) return;
   const int64_t o = static_cast<int64_t>(row) * h + c8;
-  float f[8];
+  const float inv = pqd::inv_scale(am);
+  uint2 q;
   if constexpr (MAT16) {
     const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(mb.xr) + o);
-    const uint32_t wds[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      f[2 * q] = pq_f16_to_f32(static_cast<uint16_t>(wds[q] & 0xffffu));
-      f[2 * q + 1] = pq_f16_to_f32(static_cast<uint16_t>(wds[q] >> 16));
-    }
+    q.x = pqd::quant4_f16(v.x, v.y, inv);
+    q.y = pqd::quant4_f16(v.z, v.w, inv);
   } else {
     const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(mb.xr) + o);
     const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(mb.xr) + o + 4);
-    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
-    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    q.x = pqd::quant4(a.x, a.y, a.z, a.w, inv);
+    q.y = pqd::quant4(b.x, b.y, b.z, b.w, inv);
   }
-  const float inv = pqd::inv_scale(am);
-  uint2 q;
-  q.x = pqd::quant4(f[0], f[1], f[2], f[3], inv);
-  q.y = pqd::quant4(f[4], f[5], f[6], f[7], inv);
   *reinterpret_cast<uint2*>(mb.xq + o) = q;
   if (c8 == 0) mb.xscale[row] = am / 127.0f;
 }
