@@ -670,8 +670,10 @@ void launch_prefill_t(pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* p
 }
 
 // 192 x 256 tiles (8 waves of 192 x 32) when there are enough of them to
-// fill the chip, else 128 x 128 (4 waves, several workgroups per CU) when
-// those fill it, else 64 x 128 (k/v at M = 3072: 43.4 -> 37.2 us).
+// fill the chip; else 128 x 256 (8 waves of 128 x 32) when those fill at
+// least half of it in one round; else 128 x 128 (4 waves, several
+// workgroups per CU) when those fill it; else 64 x 128 (k/v at M = 3072:
+// 43.4 -> 37.2 us).
 template <bool PARTIALS>
 void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32_t* partials, int M, int K,
                     hipStream_t stream) {
@@ -679,8 +681,34 @@ void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32
   for (int i = 0; i < grp.count; ++i) bn_tiles += (grp.mem[i].n + 255) / 256;
   int64_t bn128 = 0;
   for (int i = 0; i < grp.count; ++i) bn128 += (grp.mem[i].n + 127) / 128;
-  if (static_cast<int64_t>((M + 191) / 192) * bn_tiles >= 256)
+  // A group whose 192 x 256 tiles leave the last round of the 256 CUs part
+  // empty, but whose leading members fill whole rounds: those members run on
+  // their own, the rest in a second launch with its own tile choice (q/k/v at
+  // M = 3072: q's 256 tiles, then k and v on 192 tiles of 128 x 256, instead
+  // of 384 big tiles in 1.5 rounds).  Each member's outputs do not depend on
+  // the tiling.
+  const int64_t rows192 = (M + 191) / 192;
+  if (grp.count > 1 && rows192 * bn_tiles > 256 && (rows192 * bn_tiles) % 256 != 0) {
+    int64_t lead = 0;
+    for (int i = 1; i < grp.count; ++i) {
+      lead += rows192 * ((grp.mem[i - 1].n + 255) / 256);
+      if (lead % 256 == 0) {
+        pq::GemmGroup head{}, tail{};
+        head.count = i;
+        tail.count = grp.count - i;
+        for (int j = 0; j < i; ++j) head.mem[j] = grp.mem[j];
+        for (int j = i; j < grp.count; ++j) tail.mem[j - i] = grp.mem[j];
+        launch_prefill<PARTIALS>(head, bias_dtype, y_dtype, partials, M, K, stream);
+        launch_prefill<PARTIALS>(tail, bias_dtype, y_dtype, partials, M, K, stream);
+        return;
+      }
+    }
+  }
+  const int64_t tiles128x256 = static_cast<int64_t>((M + 127) / 128) * bn_tiles;
+  if (rows192 * bn_tiles >= 256)
     launch_prefill_t<192, 256, 1, 8, PARTIALS, kPfStages, !PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
+  else if (tiles128x256 >= 128 && tiles128x256 <= 256)
+    launch_prefill_t<128, 256, 1, 8, PARTIALS, kPfStages, !PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
   else if (static_cast<int64_t>((M + 127) / 128) * bn128 >= 256)
     launch_prefill_t<128, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
   else   // narrow outputs (k/v): twice the workgroups of 128-row tiles

@@ -62,6 +62,7 @@ CASES = [
     # 192 x 256 tiles past one round: the leading members that fill whole rounds run as a launch of their own
     (1536, 256, (8192, 1024, 1024)),
     (768, 128, (8192, 8192, 2048)),
+    (3072, 128, (4096, 1024, 1024)),   # q on 192 x 256 tiles, k/v on 128 x 256 tiles
 ]
 
 
