@@ -669,11 +669,15 @@ void launch_prefill_t(pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* p
       grp, bias_dtype, y_dtype, partials, M, K);
 }
 
-// 192 x 256 tiles (8 waves of 192 x 32) when there are enough of them to
-// fill the chip; else 128 x 256 (8 waves of 128 x 32) when those fill at
-// least half of it in one round; else 128 x 128 (4 waves, several
-// workgroups per CU) when those fill it; else 64 x 128 (k/v at M = 3072:
-// 43.4 -> 37.2 us).
+// Tile choice.  From half a round of 128 x 256 tiles up, the cheaper of
+// 192 x 256 and 128 x 256 tiles (8 waves of 192 or 128 rows x 32 columns)
+// by the measured cost of their rounds of 256 workgroups, in units of one
+// full round of 192 x 256 tiles (K = 4096): a full round of 128 x 256 tiles
+// takes 0.71, a last, partly filled round 0.77 of a full one on 192 x 256
+// tiles and 0.9 on 128 x 256 tiles (M = 4096, N = 4096: 111 us on 192 x
+// 256, 89 us expected on 128 x 256).  Below that, 128 x 128 (4 waves,
+// several workgroups per CU) when those fill the chip, else 64 x 128 (k/v
+// at M = 3072: 43.4 -> 37.2 us).
 template <bool PARTIALS>
 void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32_t* partials, int M, int K,
                     hipStream_t stream) {
@@ -704,12 +708,19 @@ void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32
       }
     }
   }
+  const int64_t tiles192 = rows192 * bn_tiles;
   const int64_t tiles128x256 = static_cast<int64_t>((M + 127) / 128) * bn_tiles;
-  if (rows192 * bn_tiles >= 256)
-    launch_prefill_t<192, 256, 1, 8, PARTIALS, kPfStages, !PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
-  else if (tiles128x256 >= 128 && tiles128x256 <= 256)
-    launch_prefill_t<128, 256, 1, 8, PARTIALS, kPfStages, !PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
-  else if (static_cast<int64_t>((M + 127) / 128) * bn128 >= 256)
+  auto rounds = [](int64_t tiles, double full, double partial) {
+    return full * static_cast<double>(tiles / 256) + (tiles % 256 != 0 ? full * partial : 0.0);
+  };
+  if (tiles192 >= 256 || tiles128x256 >= 128) {
+    if (rounds(tiles192, 1.0, 0.77) <= rounds(tiles128x256, 0.71, 0.9))
+      launch_prefill_t<192, 256, 1, 8, PARTIALS, kPfStages, !PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K,
+                                                                       stream);
+    else
+      launch_prefill_t<128, 256, 1, 8, PARTIALS, kPfStages, !PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K,
+                                                                       stream);
+  } else if (static_cast<int64_t>((M + 127) / 128) * bn128 >= 256)
     launch_prefill_t<128, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
   else   // narrow outputs (k/v): twice the workgroups of 128-row tiles
     launch_prefill_t<64, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
