@@ -383,11 +383,23 @@ void launch_w16_prefill_t(const W16Args& ar, int bias_dtype, int y_dtype, int M,
   w16_prefill<BM, BN, WM, WN><<<grid, WM * WN * 64, kW16Stages * STAGE, stream>>>(ar, bias_dtype, y_dtype, M, K);
 }
 
-// 192 x 256 tiles (8 waves of 192 x 32) when there are enough of them to
-// fill the chip, else 128 x 128 (4 waves).
+// The cheapest of 192 x 256, 128 x 256 (8 waves of 192 or 128 rows x 32
+// columns) and 128 x 128 tiles (4 waves) by the measured cost of their
+// rounds of 256 workgroups (one per CU), in units of a full round of
+// 192 x 256 tiles (K = 4096): a full round of 128 x 256 tiles takes 0.74 of
+// it and one of 128 x 128 tiles 0.45; a last, partly filled round costs 0.77
+// of a full one on 192 x 256 tiles and 0.9 on the smaller ones.  M = 4096,
+// N = 4096: 171 -> 144 us (128 x 256); M = 1024, N = 4096: 46 us on 128 x 128
+// against 57 us on 128 x 256.
 void launch_w16_prefill(const W16Args& ar, int bias_dtype, int y_dtype, int M, int K, hipStream_t stream) {
-  const int64_t big = static_cast<int64_t>((M + 191) / 192) * ((ar.n + 255) / 256);
-  if (big >= 256) launch_w16_prefill_t<192, 256, 1, 8>(ar, bias_dtype, y_dtype, M, K, stream);
+  auto rounds = [](int64_t tiles, double full, double partial) {
+    return full * static_cast<double>(tiles / 256) + (tiles % 256 != 0 ? full * partial : 0.0);
+  };
+  const double big = rounds(static_cast<int64_t>((M + 191) / 192) * ((ar.n + 255) / 256), 1.0, 0.77);
+  const double mid = rounds(static_cast<int64_t>((M + 127) / 128) * ((ar.n + 255) / 256), 0.74, 0.9);
+  const double small = rounds(static_cast<int64_t>((M + 127) / 128) * ((ar.n + 127) / 128), 0.45, 0.9);
+  if (big <= mid && big <= small) launch_w16_prefill_t<192, 256, 1, 8>(ar, bias_dtype, y_dtype, M, K, stream);
+  else if (mid <= small) launch_w16_prefill_t<128, 256, 1, 8>(ar, bias_dtype, y_dtype, M, K, stream);
   else launch_w16_prefill_t<128, 128, 1, 4>(ar, bias_dtype, y_dtype, M, K, stream);
 }
 
