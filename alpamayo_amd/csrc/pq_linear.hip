@@ -38,14 +38,16 @@ namespace {
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Measured on the Qwen3-8B shapes: the split path wins while each GEMM
-// workgroup can request all of A in its prologue at once (m * k <= 12288),
-// and for long rows up to 4 tokens: the row kernel runs each row on one CU,
-// whose VALU needs about 12 us for the 96 groups of a 12288-channel row
-// (down at m = 2: 12.8 us split against 20.0 us rows; m = 4: 16.6 / 20.8).
-// Beyond that the row kernel's whole-row quantization is faster.
+// Measured on the Qwen3-8B shapes: the split path wins up to two tokens of
+// 4096 channels (m * k <= 8192; the grouped decode layer at m = 3: 52.1 us
+// on the row kernel against 55.1 us split, m = 4: 53.7 against 59.3 us; at
+// m = 2 the row kernel loses, 49.2 against 47.0 us), and for long rows up
+// to 4 tokens: the row kernel runs each row on one CU, whose VALU needs
+// about 12 us for the 96 groups of a 12288-channel row (down at m = 2:
+// 12.8 us split against 20.0 us rows; m = 4: 16.6 / 20.8).  Beyond that the
+// row kernel's whole-row quantization is faster.
 bool use_split(int64_t m, int64_t k) {
-  return (m * k <= 12288 || (k >= 8192 && m <= 4)) && pq::gemm_rotated_supported(m, k);
+  return (m * k <= 8192 || (k >= 8192 && m <= 4)) && pq::gemm_rotated_supported(m, k);
 }
 
 // Long rows past the split pair, up to 16 tokens: the split rotation with
