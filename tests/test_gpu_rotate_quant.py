@@ -42,7 +42,9 @@ def _run(x, rot, scales_f32, input_fp16=True, materialize=True):
 
 
 @pytest.mark.parametrize("M,K", [(1, 4096), (4, 4096), (16, 4096), (16, 12288), (3, 128), (70, 1024), (300, 4096),
-                                 (7, 16384)])
+                                 (7, 16384),
+                                 # two, four and eight rows per workgroup, each with remainder rows
+                                 (1301, 512), (2501, 512), (4099, 256)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_fused_matches_oracle(M, K, dtype):
     print(f"rotate_quant M={M} K={K} dtype={dtype}", flush=True)
