@@ -739,9 +739,11 @@ struct SkinnyCfg {
 
 // About 4-6 waves per SIMD over the whole grid (more waves with fewer
 // groups each shorten every wave's serial load -> MFMA -> scale chain),
-// two column tiles per workgroup for wide outputs (768+ tiles, e.g. a
-// gate/up pair) when allowed, never more waves than K groups, and the
-// shallowest batch of at least two groups that divides the K groups (an
+// two column tiles per workgroup for wide outputs only (768+ tiles, e.g. a
+// gate/up pair) when allowed (narrower outputs keep one tile per workgroup
+// at every token count: two from 5 tokens up measured slower, the M = 8
+// layer 58.3 against 55.8 us, the 36-layer M = 16 verify block 2.45 against
+// 2.41 ms), never more waves than K groups, and the shallowest batch of at least two groups that divides the K groups (an
 // uneven last batch is masked by a scalar branch).  Measured on the
 // Qwen3-8B shapes at M = 1.  Two tiles are not allowed when a member of a
 // group has an odd tile count, nor with 16 waves behind the A-quantizing
@@ -750,7 +752,7 @@ SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k, bool two_tiles_ok = tru
   const int G = static_cast<int>(k / 128);
   const int tiles = static_cast<int>(n / 16);
   auto waves_for = [](int64_t wgs) { return wgs * 16 <= 6144 ? 16 : wgs * 8 <= 6144 ? 8 : 4; };
-  int nt = (two_tiles_ok && tiles % 2 == 0 && (tiles >= 768 || (m > 4 && tiles / 2 >= 128))) ? 2 : 1;
+  int nt = (two_tiles_ok && tiles % 2 == 0 && tiles >= 768) ? 2 : 1;
   int w = waves_for(tiles / nt);
   if (aq && nt == 2 && w == 16) {
     nt = 1;
