@@ -42,21 +42,22 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 // 4096 channels (m * k <= 8192; the grouped decode layer at m = 3: 52.1 us
 // on the row kernel against 55.1 us split, m = 4: 53.7 against 59.3 us; at
 // m = 2 the row kernel loses, 49.2 against 47.0 us), and for long rows up
-// to 4 tokens: the row kernel runs each row on one CU, whose VALU needs
-// about 12 us for the 96 groups of a 12288-channel row (down at m = 2:
-// 12.8 us split against 20.0 us rows; m = 4: 16.6 / 20.8).  Beyond that the
-// row kernel's whole-row quantization is faster.
+// to 2 tokens (from 3 the three-launch path below wins with one row per
+// wave: the layer at m = 3 51.9 -> 50.3 us, m = 4 53.6 -> 50.9 us).
 bool use_split(int64_t m, int64_t k) {
-  return (m * k <= 8192 || (k >= 8192 && m <= 4)) && pq::gemm_rotated_supported(m, k);
+  return (m * k <= 8192 || (k >= 8192 && m <= 2)) && pq::gemm_rotated_supported(m, k);
 }
 
 // Long rows past the split pair, up to 16 tokens: the split rotation with
 // its rows spread over waves (kSplitRowsPerWave rows each), a small kernel
 // for the token scales and int8 codes, then the decode GEMM on int8 A.  The
-// row kernel would run each row on one CU (down, k = 12288, at m = 6: 17.8 us
+// row kernel runs each row on one CU, whose VALU needs about 12 us for the
+// 96 groups of a 12288-channel row (down, k = 12288, at m = 6: 17.8 us
 // against 22.2 us; m = 16: 20.0 / 24.0).  At k = 4096 the third launch costs
-// more than it saves (q at m = 16: 13.3 us against 11.7 us rows).
-constexpr int kSplitRowsPerWave = 4;
+// more than it saves (the decode layers at 3-16 tokens 1-2 % slower).
+// One row per wave: the 36-layer verify block at 16 tokens 2.40 -> 2.34 ms
+// against four rows per wave (2.36 ms with two, 2.50 ms with eight).
+constexpr int kSplitRowsPerWave = 1;
 bool use_split3(int64_t m, int64_t k) {
   return !use_split(m, k) && m >= 1 && m <= pq::kSplitMaxRows && k >= 8192 && k <= 16384;
 }

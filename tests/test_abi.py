@@ -117,17 +117,18 @@ def test_workspace_size_rules():
     for m in (1, 4, 16, 3072):
         for n, k in ((1024, 4096), (4096, 4096), (12288, 4096), (4096, 12288)):
             assert lib.pq_w4a8_workspace_size(m, n, k, 128) == 0        # no inter-workgroup exchange
-    # decode (m * k <= 8192, or m <= 4 for k >= 8192): rotated rows (fp32 bound) + per-group absmax
+    # decode (m * k <= 8192, or m <= 2 for k >= 8192): rotated rows (fp32 bound) + per-group absmax
     def split(m, k):
         return (m * k * 4 + 255) // 256 * 256 + m * (k // 128) * 4
     assert lib.pq_w4a8_linear_workspace_size(1, 4096, 4096, 8) == split(1, 4096)
     assert lib.pq_w4a8_linear_workspace_size(1, 4096, 12288, 16) == split(1, 12288)
     assert lib.pq_w4a8_linear_workspace_size(2, 4096, 4096, 8) == split(2, 4096)
-    assert lib.pq_w4a8_linear_workspace_size(4, 4096, 12288, 8) == split(4, 12288)
+    assert lib.pq_w4a8_linear_workspace_size(2, 4096, 12288, 8) == split(2, 12288)
     # long rows (k >= 8192) past that, up to 16 tokens: rotated rows and int8 codes, then group
     # maxima and token scales
     def split3(m, k):
         return (m * k * 4 + 255) // 256 * 256 + (m * k + 255) // 256 * 256 + m * (k // 128) * 4 + m * 4
+    assert lib.pq_w4a8_linear_workspace_size(3, 4096, 12288, 8) == split3(3, 12288)
     assert lib.pq_w4a8_linear_workspace_size(5, 4096, 12288, 8) == split3(5, 12288)
     assert lib.pq_w4a8_linear_workspace_size(16, 4096, 12288, 8) == split3(16, 12288)
     assert lib.pq_w4a8_linear_group_workspace_size(16, 8192, 2) == 2 * split3(16, 8192)
@@ -261,7 +262,7 @@ def test_split_path_rule():
     assert lib.pq_w4a8_linear_split_path(3, 4096) == 0   # three tokens: the row kernel
     assert lib.pq_w4a8_linear_split_path(1, 12288) == 1
     assert lib.pq_w4a8_linear_split_path(4, 4096) == 0
-    # long rows: split up to 4 tokens (the row kernel runs a row on one CU)
+    # long rows: the split pair up to 2 tokens, then the three-launch split path (never the row kernel)
     assert lib.pq_w4a8_linear_split_path(2, 12288) == 1
     assert lib.pq_w4a8_linear_split_path(4, 12288) == 1
     assert lib.pq_w4a8_linear_split_path(4, 8192) == 1

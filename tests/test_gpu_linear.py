@@ -165,7 +165,8 @@ def test_graph_capture_replays_match_eager(M):
 @pytest.mark.parametrize("krot,flags", [(8, (True, True)), (1, (False, True)), (8, (True, False)), (16, (True, True))])
 def test_linear_op_decode_paths(M, N, K, krot, flags):
     """paroquant::w4a8_linear on both of its paths: split rotation + prologue-quantizing GEMM
-    (M * K <= 8192, or K >= 8192 and M <= 4) and row rotate+quant + GEMM (otherwise)."""
+    (M * K <= 8192, or K >= 8192 and M <= 2), the three-launch split path (K >= 8192 beyond) and row
+    rotate+quant + GEMM (otherwise)."""
     print(f"linear op M={M} N={N} K={K} krot={krot} flags={flags}", flush=True)
     g = workloads.generator(zlib.crc32(f"{M}{N}{K}{krot}{flags}".encode()))
     spec = workloads.linear_spec("x", N, K, g, keep_codes=True)
