@@ -2,8 +2,8 @@
 // int4 x int8 GEMM) behind one entry point, pq_w4a8_linear.  Two kernels
 // either way, chosen by the number of tokens m:
 //
-//   split (decode: m * k <= 12288, e.g. one token, or up to 4 tokens when
-//     k >= 8192): the rotation runs with
+//   split (decode: m * k <= 8192, one or two tokens of 4096 channels, or
+//     up to 2 tokens when k >= 8192): the rotation runs with
 //     one wave per 128-channel group (K/128 waves spread over the chip, each
 //     rotation parameter read once) and writes the rotated rows plus each
 //     row's absmax per group; the decode GEMM derives the token scales and
