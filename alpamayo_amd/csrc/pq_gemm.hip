@@ -747,11 +747,17 @@ struct SkinnyCfg {
 // uneven last batch is masked by a scalar branch).  Measured on the
 // Qwen3-8B shapes at M = 1.  Two tiles are not allowed when a member of a
 // group has an odd tile count, nor with 16 waves behind the A-quantizing
-// prologue (that combination spills).
+// prologue (that combination spills).  Behind that prologue, where every
+// workgroup first quantizes the whole activation row into LDS, 16 waves per
+// workgroup only up to 4 per SIMD over the grid (the q/k/v group, 384
+// workgroups, on 8 waves: the M = 1 layer 42.4 -> 41.9 us in a sweep,
+// 42.1 -> 42.0 us in an A/B run, the 36-layer decode chain 1.587 -> 1.575 ms,
+// the M = 2 layer 45.6 -> 45.2 us; the other shapes measured no better).
 SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k, bool two_tiles_ok = true, bool aq = false) {
   const int G = static_cast<int>(k / 128);
   const int tiles = static_cast<int>(n / 16);
-  auto waves_for = [](int64_t wgs) { return wgs * 16 <= 6144 ? 16 : wgs * 8 <= 6144 ? 8 : 4; };
+  const int64_t w16_max = aq ? 4096 : 6144;   // waves over the grid with 16 per workgroup
+  auto waves_for = [w16_max](int64_t wgs) { return wgs * 16 <= w16_max ? 16 : wgs * 8 <= 6144 ? 8 : 4; };
   int nt = (two_tiles_ok && tiles % 2 == 0 && tiles >= 768) ? 2 : 1;
   int w = waves_for(tiles / nt);
   if (aq && nt == 2 && w == 16) {
