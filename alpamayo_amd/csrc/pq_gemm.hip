@@ -737,28 +737,34 @@ struct SkinnyCfg {
   int u;   // groups per wave per batch (loads in flight)
 };
 
-// About 4-6 waves per SIMD over the whole grid (more waves with fewer
-// groups each shorten every wave's serial load -> MFMA -> scale chain),
-// two column tiles per workgroup for wide outputs only (768+ tiles, e.g. a
-// gate/up pair) when allowed (narrower outputs keep one tile per workgroup
-// at every token count: two from 5 tokens up measured slower, the M = 8
-// layer 58.3 against 55.8 us, the 36-layer M = 16 verify block 2.45 against
-// 2.41 ms), never more waves than K groups, and the shallowest batch of at least two groups that divides the K groups (an
-// uneven last batch is masked by a scalar branch).  Measured on the
-// Qwen3-8B shapes at M = 1.  Two tiles are not allowed when a member of a
-// group has an odd tile count, nor with 16 waves behind the A-quantizing
-// prologue (that combination spills).  Behind that prologue, where every
-// workgroup first quantizes the whole activation row into LDS, 16 waves per
-// workgroup only up to 4 per SIMD over the grid (the q/k/v group, 384
-// workgroups, on 8 waves: the M = 1 layer 42.4 -> 41.9 us in a sweep,
-// 42.1 -> 42.0 us in an A/B run, the 36-layer decode chain 1.587 -> 1.575 ms,
-// the M = 2 layer 45.6 -> 45.2 us; the other shapes measured no better).
+// Measured on the Qwen3-8B shapes at 1-16 tokens:
+// - About 4-6 waves per SIMD over the whole grid: more waves with fewer
+//   groups each shorten every wave's serial load -> MFMA -> scale chain.
+//   Never more waves than K groups.
+// - Two column tiles per workgroup for wide outputs (768+ tiles, e.g. a
+//   gate/up pair), and where one tile per workgroup would put one workgroup
+//   on some CUs and two on others (256 < tiles < 512: the q/k/v group's 384
+//   tiles on int8 A, the M = 16 layer 60.6 -> 59.9 us, M = 3 50.1 -> 49.9 us,
+//   the 36-layer verify block 2.342 -> 2.315 ms).  Other outputs keep one
+//   tile per workgroup at every token count (two from 5 tokens up measured
+//   slower there: the M = 8 layer 58.3 against 55.8 us, the verify block
+//   2.45 against 2.41 ms).  Not when a member of a group has an odd tile
+//   count, nor with 16 waves behind the A-quantizing prologue (that
+//   combination spills).
+// - Behind that prologue, where every workgroup first quantizes the whole
+//   activation row into LDS, 16 waves per workgroup only up to 4 per SIMD
+//   over the grid (the q/k/v group, 384 workgroups, on 8 waves: the M = 1
+//   layer 42.4 -> 41.9 us in a sweep, 42.1 -> 42.0 us in an A/B run, the
+//   36-layer decode chain 1.587 -> 1.575 ms, the M = 2 layer 45.6 -> 45.2
+//   us; the other shapes measured no better).
+// - The shallowest batch of at least two groups that divides the K groups
+//   (an uneven last batch is masked by a scalar branch).
 SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k, bool two_tiles_ok = true, bool aq = false) {
   const int G = static_cast<int>(k / 128);
   const int tiles = static_cast<int>(n / 16);
   const int64_t w16_max = aq ? 4096 : 6144;   // waves over the grid with 16 per workgroup
   auto waves_for = [w16_max](int64_t wgs) { return wgs * 16 <= w16_max ? 16 : wgs * 8 <= 6144 ? 8 : 4; };
-  int nt = (two_tiles_ok && tiles % 2 == 0 && tiles >= 768) ? 2 : 1;
+  int nt = (two_tiles_ok && tiles % 2 == 0 && (tiles >= 768 || (tiles > 256 && tiles < 512))) ? 2 : 1;
   int w = waves_for(tiles / nt);
   if (aq && nt == 2 && w == 16) {
     nt = 1;
