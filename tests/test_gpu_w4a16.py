@@ -262,7 +262,7 @@ def test_graph_replay(m):
 
 
 @pytest.mark.parametrize("m", [1, 5, 16, 20])
-@pytest.mark.parametrize("ns", [(1024, 1040, 64), (12288, 12288)])
+@pytest.mark.parametrize("ns", [(1024, 1040, 64), (12288, 12288), (4096, 1024, 1024)])
 def test_linear_group_matches_single_linears(m, ns):
     """paroquant::w4a16_linear_group (one rotation launch; one GEMM launch at m <= 16, tiles of every member
     in one grid) gives each member what paroquant::w4a16_linear gives it alone.  The group's launch may split
