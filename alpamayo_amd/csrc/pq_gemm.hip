@@ -762,14 +762,14 @@ struct SkinnyCfg {
 SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k, bool two_tiles_ok = true, bool aq = false) {
   const int G = static_cast<int>(k / 128);
   const int tiles = static_cast<int>(n / 16);
-  const int64_t w16_max = aq ? 4096 : 6144;   // waves over the grid with 16 per workgroup
-  auto waves_for = [w16_max](int64_t wgs) { return wgs * 16 <= w16_max ? 16 : wgs * 8 <= 6144 ? 8 : 4; };
+  auto waves_for = [](int64_t wgs) { return wgs * 16 <= 6144 ? 16 : wgs * 8 <= 6144 ? 8 : 4; };
   int nt = (two_tiles_ok && tiles % 2 == 0 && (tiles >= 768 || (tiles > 256 && tiles < 512))) ? 2 : 1;
   int w = waves_for(tiles / nt);
   if (aq && nt == 2 && w == 16) {
     nt = 1;
     w = waves_for(tiles);
   }
+  if (aq && w == 16 && static_cast<int64_t>(tiles / nt) * 16 > 4096) w = 8;
   while (w > 4 && w > G) w >>= 1;
   int u = 2;
   if (G <= w) u = 1;
