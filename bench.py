@@ -114,6 +114,9 @@ def main() -> int:
     ap.add_argument("--no-ragged", action="store_true", help="skip the ragged packed batch")
     ap.add_argument("--no-w4a16", action="store_true", help="skip the W4A16 (WQLinear) figures")
     ap.add_argument("--no-mxfp4", action="store_true", help="skip the fused rotation + MXFP4 figures")
+    ap.add_argument("--no-decode-per-shape", action="store_true",
+                    help="skip the per-shape decode GEMM timing (so that a kernel trace's int8-A decode GEMM "
+                         "launches all come from the roofline graph)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--warm-seconds", type=float, default=0.3,
                     help="minimum wall time of untimed replays before each timed region")
@@ -311,8 +314,9 @@ def main() -> int:
     log(f"decode GEMM M=1: {per_launch_us:.2f} us/launch avg, {achieved:.0f} GB/s")
     del gg
     # the same launches one shape at a time (q/o, k/v, gate/up: 16 per replay; down: 8)
-    gemm_per_shape = {}
-    for shape in sorted({(q.out_features, q.in_features) for q, _, _ in gemm_launches}):
+    gemm_per_shape = None if args.no_decode_per_shape else {}
+    for shape in ([] if args.no_decode_per_shape else sorted({(q.out_features, q.in_features)
+                                                              for q, _, _ in gemm_launches})):
         sel = [t for t in gemm_launches if (t[0].out_features, t[0].in_features) == shape]
         g1 = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g1):
@@ -324,8 +328,9 @@ def main() -> int:
                                                    "GBps": round(sb / (sus * 1e-6) / 1e9, 1),
                                                    "frac_hbm": round(sb / (sus * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
         del g1
-    log("decode GEMM M=1 per shape (N x K): " + ", ".join(f"{k} {v['us_per_launch']} us ({v['GBps']:.0f} GB/s)"
-                                                          for k, v in gemm_per_shape.items()))
+    if gemm_per_shape is not None:
+        log("decode GEMM M=1 per shape (N x K): " + ", ".join(f"{k} {v['us_per_launch']} us ({v['GBps']:.0f} GB/s)"
+                                                              for k, v in gemm_per_shape.items()))
 
     # ---- prefill M = 3072 ---------------------------------------------------
     prefill = None
