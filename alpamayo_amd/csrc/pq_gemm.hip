@@ -493,7 +493,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
   // Only two pairs of partials are live; the group's B fragments are
   // unpacked once up front.
   auto compute_tp = [&](int stage, int ig) {
-    static_assert(TM % 2 == 0, "tiles in pairs");
+    static_assert(!TP || TM % 2 == 0, "tiles in pairs");
     const uint8_t* As = smem + stage * STAGE;
     const uint8_t* Bs = As + A_BYTES;
     const uint32_t* Ms = reinterpret_cast<const uint32_t*>(Bs + B_BYTES);
@@ -676,8 +676,8 @@ void launch_prefill_t(pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* p
 // takes 0.71, a last, partly filled round 0.77 of a full one on 192 x 256
 // tiles and 0.9 on 128 x 256 tiles (M = 4096, N = 4096: 111 us on 192 x
 // 256, 89 us expected on 128 x 256).  Below that, 128 x 128 (4 waves,
-// several workgroups per CU) when those fill the chip, else 64 x 128 (k/v
-// at M = 3072: 43.4 -> 37.2 us).
+// several workgroups per CU) when those fill the chip, 32 x 128 when those
+// fit in one round, else 64 x 128 (k/v at M = 3072: 43.4 -> 37.2 us).
 template <bool PARTIALS>
 void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32_t* partials, int M, int K,
                     hipStream_t stream) {
@@ -722,6 +722,11 @@ void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32
                                                                        stream);
   } else if (static_cast<int64_t>((M + 127) / 128) * bn128 >= 256)
     launch_prefill_t<128, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
+  else if (static_cast<int64_t>((M + 31) / 32) * bn128 <= 256)
+    // at most one round of 32-row tiles (17-256 tokens at N = 4096): each
+    // workgroup walks all of K, so its time follows its rows (M = 17-256:
+    // 25 -> 19 us at K = 4096, 65 -> 49.5 us at K = 12288 against 64 x 128)
+    launch_prefill_t<32, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
   else   // narrow outputs (k/v): twice the workgroups of 128-row tiles
     launch_prefill_t<64, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
 }
