@@ -383,7 +383,8 @@ void launch_w16_prefill_t(const W16Args& ar, int bias_dtype, int y_dtype, int M,
   w16_prefill<BM, BN, WM, WN><<<grid, WM * WN * 64, kW16Stages * STAGE, stream>>>(ar, bias_dtype, y_dtype, M, K);
 }
 
-// The cheapest of 192 x 256, 128 x 256 (8 waves of 192 or 128 rows x 32
+// 32 x 128 tiles when one round of them covers the output (below); else the
+// cheapest of 192 x 256, 128 x 256 (8 waves of 192 or 128 rows x 32
 // columns) and 128 x 128 tiles (4 waves) by the measured cost of their
 // rounds of 256 workgroups (one per CU), in units of a full round of
 // 192 x 256 tiles (K = 4096): a full round of 128 x 256 tiles takes 0.74 of
@@ -400,6 +401,11 @@ void launch_w16_prefill(const W16Args& ar, int bias_dtype, int y_dtype, int M, i
   const double small = rounds(static_cast<int64_t>((M + 127) / 128) * ((ar.n + 127) / 128), 0.45, 0.9);
   if (big <= mid && big <= small) launch_w16_prefill_t<192, 256, 1, 8>(ar, bias_dtype, y_dtype, M, K, stream);
   else if (mid <= small) launch_w16_prefill_t<128, 256, 1, 8>(ar, bias_dtype, y_dtype, M, K, stream);
+  // at most one round of 32-row tiles (17-256 tokens at N = 4096): each
+  // workgroup walks all of K, so its time follows its rows (M = 64-256: 42
+  // -> 26 us at K = 4096, M = 128: 115 -> 71 us at K = 12288 against 128 x 128)
+  else if (static_cast<int64_t>((M + 31) / 32) * ((ar.n + 127) / 128) <= 256)
+    launch_w16_prefill_t<32, 128, 1, 4>(ar, bias_dtype, y_dtype, M, K, stream);
   else launch_w16_prefill_t<128, 128, 1, 4>(ar, bias_dtype, y_dtype, M, K, stream);
 }
 
