@@ -71,7 +71,7 @@ __device__ __forceinline__ int group_member(const pq::GemmGroup& grp, int unit) 
   return mi;
 }
 
-template <int NT, int W, int U, bool PARTIALS, int AQ>
+template <int NT, int W, int U, bool PARTIALS, int AQ, bool RBLK = false>
 __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) void gemm_skinny(
     const pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* __restrict__ partials, int M, int K) {
   __shared__ float red[W][NT][4][64];
@@ -79,16 +79,27 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
   extern __shared__ __attribute__((aligned(16))) int8_t aq[];
   const int mi = group_member(grp, blockIdx.x);
   const pq::GemmMember& mb = grp.mem[mi];
-  const int8_t* __restrict__ xq = mb.xq;
-  const float* __restrict__ xs = mb.xs;
+  // RBLK (int8 A, 17-32 rows): grid.y cuts the rows into blocks of 16
+  // (block b takes rows 16b .. 16b+15; every pointer below moves to the
+  // block's first row).  A separate instance, so that launches of up to 16
+  // rows keep their own code (the row-block arithmetic ahead of the first
+  // loads measured 1-3 % slower on their decode layers).
+  static_assert(!RBLK || AQ == 0, "row blocks on int8 A only");
+  const int rb = RBLK ? static_cast<int>(blockIdx.y) : 0;
+  if constexpr (RBLK) M = min(M - rb * kSkinnyRows, kSkinnyRows);
+  const int8_t* __restrict__ xq = RBLK ? mb.xq + static_cast<int64_t>(rb) * kSkinnyRows * K : mb.xq;
+  const float* __restrict__ xs = RBLK ? mb.xs + rb * kSkinnyRows : mb.xs;
   const void* __restrict__ xr = mb.xr;
   const float* __restrict__ gmax = mb.gmax;
   const uint8_t* __restrict__ wpack = mb.wpack;
   const uint32_t* __restrict__ wmeta = mb.wmeta;
   const void* __restrict__ bias = mb.bias;
-  void* __restrict__ y = mb.y;
   const int N = mb.n;
+  void* __restrict__ y = RBLK ? static_cast<void*>(static_cast<char*>(mb.y) + static_cast<int64_t>(rb) * kSkinnyRows *
+                                                                                N * (y_dtype == PQ_F32 ? 4 : 2))
+                              : mb.y;
   const int G = K >> 7;
+  if constexpr (PARTIALS && RBLK) partials += static_cast<int64_t>(rb) * kSkinnyRows * G * N;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar branches
   const int lane = threadIdx.x & 63;
   const int c = lane & 15;
@@ -723,9 +734,10 @@ void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32
   } else if (static_cast<int64_t>((M + 127) / 128) * bn128 >= 256)
     launch_prefill_t<128, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
   else if (static_cast<int64_t>((M + 31) / 32) * bn128 <= 256)
-    // at most one round of 32-row tiles (17-256 tokens at N = 4096): each
-    // workgroup walks all of K, so its time follows its rows (M = 17-256:
-    // 25 -> 19 us at K = 4096, 65 -> 49.5 us at K = 12288 against 64 x 128)
+    // at most one round of 32-row tiles (33-256 tokens at N = 4096; up to
+    // 32 the decode kernel runs them): each workgroup walks all of K, so its
+    // time follows its rows (25 -> 19 us at K = 4096, 65 -> 49.5 us at
+    // K = 12288 against 64 x 128)
     launch_prefill_t<32, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
   else   // narrow outputs (k/v): twice the workgroups of 128-row tiles
     launch_prefill_t<64, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
@@ -734,7 +746,10 @@ void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32
 // ---------------------------------------------------------------------------
 // Host-side configuration
 // ---------------------------------------------------------------------------
-constexpr int kSkinnyMaxM = 16;
+// The decode GEMM on int8 A takes up to 32 rows, in row blocks of 16 (one
+// grid row per block; the weights are read once per block): M = 17-32 at N = K = 4096 7-9 us against 24.5 us on the prefill
+// kernel's 64 x 128 tiles, M = 32 at K = 12288 17.5 against 65 us.
+constexpr int kSkinnyMaxM = 32;
 
 struct SkinnyCfg {
   int nt;  // 16-column tiles per workgroup
@@ -769,7 +784,8 @@ SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k, bool two_tiles_ok = tru
   const int tiles = static_cast<int>(n / 16);
   auto waves_for = [](int64_t wgs) { return wgs * 16 <= 6144 ? 16 : wgs * 8 <= 6144 ? 8 : 4; };
   int nt = (two_tiles_ok && tiles % 2 == 0 && (tiles >= 768 || (tiles > 256 && tiles < 512))) ? 2 : 1;
-  int w = waves_for(tiles / nt);
+  const int rblk = aq ? 1 : static_cast<int>((m + kSkinnyRows - 1) / kSkinnyRows);   // int8 A: row blocks of 16
+  int w = waves_for(static_cast<int64_t>(tiles / nt) * rblk);
   if (aq && nt == 2 && w == 16) {
     nt = 1;
     w = waves_for(tiles);
@@ -789,9 +805,16 @@ void launch_skinny_nwu(pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* 
                        hipStream_t stream) {
   grp.first[0] = 0;
   for (int i = 0; i < grp.count; ++i) grp.first[i + 1] = grp.first[i] + grp.mem[i].n / 16 / NT;
-  const unsigned grid = static_cast<unsigned>(grp.first[grp.count]);
+  const unsigned tiles = static_cast<unsigned>(grp.first[grp.count]);
   const size_t lds = AQ != 0 ? static_cast<size_t>(M) * (K + 16) : 0;
-  gemm_skinny<NT, W, U, PARTIALS, AQ><<<grid, W * 64, lds, stream>>>(grp, bias_dtype, y_dtype, partials, M, K);
+  if constexpr (AQ == 0) {
+    if (M > kSkinnyRows) {   // int8 A, 17-32 rows: one grid row per block of 16
+      const dim3 grid(tiles, static_cast<unsigned>((M + kSkinnyRows - 1) / kSkinnyRows));
+      gemm_skinny<NT, W, U, PARTIALS, AQ, true><<<grid, W * 64, 0, stream>>>(grp, bias_dtype, y_dtype, partials, M, K);
+      return;
+    }
+  }
+  gemm_skinny<NT, W, U, PARTIALS, AQ><<<tiles, W * 64, lds, stream>>>(grp, bias_dtype, y_dtype, partials, M, K);
 }
 
 template <bool PARTIALS, int AQ>
