@@ -124,18 +124,20 @@ def test_workspace_size_rules():
     assert lib.pq_w4a8_linear_workspace_size(1, 4096, 12288, 16) == split(1, 12288)
     assert lib.pq_w4a8_linear_workspace_size(2, 4096, 4096, 8) == split(2, 4096)
     assert lib.pq_w4a8_linear_workspace_size(2, 4096, 12288, 8) == split(2, 12288)
-    # long rows (k >= 8192) past that, up to 16 tokens: rotated rows and int8 codes, then group
+    # long rows (k >= 8192) past that, up to 32 tokens: rotated rows and int8 codes, then group
     # maxima and token scales
     def split3(m, k):
         return (m * k * 4 + 255) // 256 * 256 + (m * k + 255) // 256 * 256 + m * (k // 128) * 4 + m * 4
     assert lib.pq_w4a8_linear_workspace_size(3, 4096, 12288, 8) == split3(3, 12288)
     assert lib.pq_w4a8_linear_workspace_size(5, 4096, 12288, 8) == split3(5, 12288)
     assert lib.pq_w4a8_linear_workspace_size(16, 4096, 12288, 8) == split3(16, 12288)
+    assert lib.pq_w4a8_linear_workspace_size(32, 4096, 12288, 8) == split3(32, 12288)
     assert lib.pq_w4a8_linear_group_workspace_size(16, 8192, 2) == 2 * split3(16, 8192)
     # otherwise the row path holds xq and xscale
     assert lib.pq_w4a8_linear_workspace_size(4, 4096, 4096, 8) == 4 * 4096 + 16
     assert lib.pq_w4a8_linear_workspace_size(3, 4096, 4096, 8) == 3 * 4096 + 12
-    assert lib.pq_w4a8_linear_workspace_size(17, 4096, 12288, 8) == 17 * 12288 + 68
+    assert lib.pq_w4a8_linear_workspace_size(17, 4096, 12288, 8) == split3(17, 12288)
+    assert lib.pq_w4a8_linear_workspace_size(33, 4096, 12288, 8) == 33 * 12288 + 132
     assert lib.pq_w4a8_linear_workspace_size(17, 4096, 4096, 8) == 17 * 4096 + 68
     assert lib.pq_w4a8_linear_workspace_size(3, 64, 100, 8) == 0       # invalid shape -> 0
 
@@ -269,7 +271,9 @@ def test_split_path_rule():
     assert lib.pq_w4a8_linear_split_path(4, 16384) == 1
     assert lib.pq_w4a8_linear_split_path(5, 12288) == 1    # long rows: the three-launch split path
     assert lib.pq_w4a8_linear_split_path(16, 8192) == 1
-    assert lib.pq_w4a8_linear_split_path(17, 12288) == 0
+    assert lib.pq_w4a8_linear_split_path(17, 12288) == 1
+    assert lib.pq_w4a8_linear_split_path(32, 16384) == 1
+    assert lib.pq_w4a8_linear_split_path(33, 12288) == 0
     assert lib.pq_w4a8_linear_split_path(16, 4096) == 0
     assert lib.pq_w4a8_linear_split_path(2, 4096) == 1
     assert lib.pq_w4a8_linear_split_path(4, 6144) == 0
