@@ -73,7 +73,7 @@ __device__ __forceinline__ int group_member(const pq::GemmGroup& grp, int unit) 
 
 template <int NT, int W, int U, bool PARTIALS, int AQ, bool RBLK = false>
 __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) void gemm_skinny(
-    const pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* __restrict__ partials, int M, int K) {
+    const pq::GemmGroup grp, int bias_dtype, int y_dtype, int M, int K) {
   __shared__ float red[W][NT][4][64];
   __shared__ float s_amax[kSkinnyRows];
   extern __shared__ __attribute__((aligned(16))) int8_t aq[];
@@ -99,6 +99,7 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
                                                                                 N * (y_dtype == PQ_F32 ? 4 : 2))
                               : mb.y;
   const int G = K >> 7;
+  int32_t* __restrict__ partials = mb.partials;
   if constexpr (PARTIALS && RBLK) partials += static_cast<int64_t>(rb) * kSkinnyRows * G * N;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar branches
   const int lane = threadIdx.x & 63;
@@ -240,6 +241,21 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
           }
         }
         lds_barrier();
+        if constexpr (PARTIALS) {
+          // Parity form: the member's first workgroup also writes the A
+          // operand it multiplies -- the int8 image just built in LDS -- and
+          // the token scales its epilogue would apply.
+          if (blockIdx.x == static_cast<unsigned>(grp.first[mi])) {
+            const int c16s = K >> 4;
+            for (int e = threadIdx.x; e < M * c16s; e += nthr) {
+              const int r = e / c16s;
+              const int c16 = (e - r * c16s) * 16;
+              *reinterpret_cast<uint4*>(mb.a_out + static_cast<int64_t>(r) * K + c16) =
+                  *reinterpret_cast<const uint4*>(aq + r * astride + c16);
+            }
+            if (static_cast<int>(threadIdx.x) < M) mb.as_out[threadIdx.x] = s_amax[threadIdx.x] / 127.0f;
+          }
+        }
       }
     }
 #pragma unroll
@@ -344,7 +360,7 @@ __device__ __forceinline__ void wait_groups(int ahead) {
 
 template <int BM, int BN, int WM, int WN, bool PARTIALS, int ST = kPfStages, bool TP = false>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
-    const pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* __restrict__ partials, int M, int K) {
+    const pq::GemmGroup grp, int bias_dtype, int y_dtype, int M, int K) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
   constexpr int A_BYTES = BM * 128;                 // BM/8 blocks of 1 KB (8 rows each)
@@ -378,6 +394,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
   const uint32_t* __restrict__ wmeta = mb.wmeta;
   const void* __restrict__ bias = mb.bias;
   void* __restrict__ y = mb.y;
+  int32_t* __restrict__ partials = mb.partials;
   const int N = mb.n;
   const int ntiles16 = N >> 4;
   const int bn = bn_all - grp.first[mi];
@@ -502,8 +519,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
   // and scales the previous pair's partials in between, one MFMA then eight
   // VALU (four converts, four fmas), enforced with sched_group_barrier.
   // Only two pairs of partials are live; the group's B fragments are
-  // unpacked once up front.
-  auto compute_tp = [&](int stage, int ig) {
+  // unpacked once up front.  The PARTIALS instance stores each pair's int32
+  // tiles where the other scales them (same MFMA chains and fragments).
+  auto store_partials = [&](int tile, int tn, int v, int g, int32_t val) {
+    const int64_t m = static_cast<int64_t>(bm) * BM + arow[tile] - r32 + 8 * (v >> 2) + 4 * hj + (v & 3);
+    const int n = bn * BN + bcol[tn];
+    if (m < M && n < N) partials[(m * G + g) * N + n] = val;
+  };
+  auto compute_tp = [&](int stage, int g, int ig) {
     static_assert(!TP || TM % 2 == 0, "tiles in pairs");
     const uint8_t* As = smem + stage * STAGE;
     const uint8_t* Bs = As + A_BYTES;
@@ -550,9 +573,12 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
             T[cb][t2][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[t2][i], b[i][tn], T[cb][t2][tn], 0, 0, 0);
             if (p > 0) {
 #pragma unroll
-              for (int v = 4 * i; v < 4 * i + 4; ++v)
-                acc[2 * p - 2 + t2][tn][v] =
-                    fmaf(static_cast<float>(T[cb ^ 1][t2][tn][v]), sc[tn], acc[2 * p - 2 + t2][tn][v]);
+              for (int v = 4 * i; v < 4 * i + 4; ++v) {
+                if constexpr (PARTIALS) store_partials(2 * p - 2 + t2, tn, v, g, T[cb ^ 1][t2][tn][v]);
+                else
+                  acc[2 * p - 2 + t2][tn][v] =
+                      fmaf(static_cast<float>(T[cb ^ 1][t2][tn][v]), sc[tn], acc[2 * p - 2 + t2][tn][v]);
+              }
             }
           }
         if (p + 1 < TM / 2) {
@@ -560,7 +586,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
           for (int t2 = 0; t2 < 2; ++t2) a[t2][i] = load_frag(2 * p + 2 + t2, i);
         }
       }
-      if (p > 0) {
+      if (!PARTIALS && p > 0) {
 #pragma unroll
         for (int q = 0; q < 8 * TN; ++q) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
@@ -575,8 +601,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-          acc[TM - 2 + t2][tn][v] = fmaf(static_cast<float>(T[LP][t2][tn][v]), sc[tn], acc[TM - 2 + t2][tn][v]);
+        for (int v = 0; v < 16; ++v) {
+          if constexpr (PARTIALS) store_partials(TM - 2 + t2, tn, v, g, T[LP][t2][tn][v]);
+          else acc[TM - 2 + t2][tn][v] = fmaf(static_cast<float>(T[LP][t2][tn][v]), sc[tn], acc[TM - 2 + t2][tn][v]);
+        }
   };
 
   // Stage g % ST holds group g; the copies run ST-1 groups ahead.  Before
@@ -597,7 +625,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
   for (int g = 0; g < G; ++g) {
     wait_groups<LOADS, ST - 2>(min(G - 1 - g, ST - 2));
     __builtin_amdgcn_s_barrier();
-    if constexpr (TP && !PARTIALS) compute_tp(g % ST, g + ST - 1);
+    if constexpr (TP) compute_tp(g % ST, g, g + ST - 1);
     else compute(g % ST, g, g + ST - 1);
   }
   if constexpr (PARTIALS) return;
@@ -670,14 +698,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_prefill(
 }
 
 template <int BM, int BN, int WM, int WN, bool PARTIALS, int ST = kPfStages, bool TP = false>
-void launch_prefill_t(pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* partials, int M, int K,
+void launch_prefill_t(pq::GemmGroup grp, int bias_dtype, int y_dtype, int M, int K,
                       hipStream_t stream) {
   constexpr int STAGE = BM * 128 + (BN / 16) * kPfBStride + BN * 4;
   grp.first[0] = 0;
   for (int i = 0; i < grp.count; ++i) grp.first[i + 1] = grp.first[i] + (grp.mem[i].n + BN - 1) / BN;
   const unsigned grid = static_cast<unsigned>(((M + BM - 1) / BM) * grp.first[grp.count]);
   gemm_prefill<BM, BN, WM, WN, PARTIALS, ST, TP><<<grid, WM * WN * 64, ST * STAGE + BM * 4, stream>>>(
-      grp, bias_dtype, y_dtype, partials, M, K);
+      grp, bias_dtype, y_dtype, M, K);
 }
 
 // Tile choice.  From half a round of 128 x 256 tiles up, the cheaper of
@@ -690,7 +718,7 @@ void launch_prefill_t(pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* p
 // several workgroups per CU) when those fill the chip, 32 x 128 when those
 // fit in one round, else 64 x 128 (k/v at M = 3072: 43.4 -> 37.2 us).
 template <bool PARTIALS>
-void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32_t* partials, int M, int K,
+void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int M, int K,
                     hipStream_t stream) {
   int64_t bn_tiles = 0;
   for (int i = 0; i < grp.count; ++i) bn_tiles += (grp.mem[i].n + 255) / 256;
@@ -713,8 +741,8 @@ void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32
         tail.count = grp.count - i;
         for (int j = 0; j < i; ++j) head.mem[j] = grp.mem[j];
         for (int j = i; j < grp.count; ++j) tail.mem[j - i] = grp.mem[j];
-        launch_prefill<PARTIALS>(head, bias_dtype, y_dtype, partials, M, K, stream);
-        launch_prefill<PARTIALS>(tail, bias_dtype, y_dtype, partials, M, K, stream);
+        launch_prefill<PARTIALS>(head, bias_dtype, y_dtype, M, K, stream);
+        launch_prefill<PARTIALS>(tail, bias_dtype, y_dtype, M, K, stream);
         return;
       }
     }
@@ -726,21 +754,19 @@ void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32
   };
   if (tiles192 >= 256 || tiles128x256 >= 128) {
     if (rounds(tiles192, 1.0, 0.77) <= rounds(tiles128x256, 0.71, 0.9))
-      launch_prefill_t<192, 256, 1, 8, PARTIALS, kPfStages, !PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K,
-                                                                       stream);
+      launch_prefill_t<192, 256, 1, 8, PARTIALS, kPfStages, true>(grp, bias_dtype, y_dtype, M, K, stream);
     else
-      launch_prefill_t<128, 256, 1, 8, PARTIALS, kPfStages, !PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K,
-                                                                       stream);
+      launch_prefill_t<128, 256, 1, 8, PARTIALS, kPfStages, true>(grp, bias_dtype, y_dtype, M, K, stream);
   } else if (static_cast<int64_t>((M + 127) / 128) * bn128 >= 256)
-    launch_prefill_t<128, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
+    launch_prefill_t<128, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, M, K, stream);
   else if (static_cast<int64_t>((M + 31) / 32) * bn128 <= 256)
     // at most one round of 32-row tiles (33-256 tokens at N = 4096; up to
     // 32 the decode kernel runs them): each workgroup walks all of K, so its
     // time follows its rows (25 -> 19 us at K = 4096, 65 -> 49.5 us at
     // K = 12288 against 64 x 128)
-    launch_prefill_t<32, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
+    launch_prefill_t<32, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, M, K, stream);
   else   // narrow outputs (k/v): twice the workgroups of 128-row tiles
-    launch_prefill_t<64, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, partials, M, K, stream);
+    launch_prefill_t<64, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, M, K, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -801,7 +827,7 @@ SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k, bool two_tiles_ok = tru
 }
 
 template <int NT, int W, int U, bool PARTIALS, int AQ>
-void launch_skinny_nwu(pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* partials, int M, int K,
+void launch_skinny_nwu(pq::GemmGroup grp, int bias_dtype, int y_dtype, int M, int K,
                        hipStream_t stream) {
   grp.first[0] = 0;
   for (int i = 0; i < grp.count; ++i) grp.first[i + 1] = grp.first[i] + grp.mem[i].n / 16 / NT;
@@ -810,19 +836,19 @@ void launch_skinny_nwu(pq::GemmGroup grp, int bias_dtype, int y_dtype, int32_t* 
   if constexpr (AQ == 0) {
     if (M > kSkinnyRows) {   // int8 A, 17-32 rows: one grid row per block of 16
       const dim3 grid(tiles, static_cast<unsigned>((M + kSkinnyRows - 1) / kSkinnyRows));
-      gemm_skinny<NT, W, U, PARTIALS, AQ, true><<<grid, W * 64, 0, stream>>>(grp, bias_dtype, y_dtype, partials, M, K);
+      gemm_skinny<NT, W, U, PARTIALS, AQ, true><<<grid, W * 64, 0, stream>>>(grp, bias_dtype, y_dtype, M, K);
       return;
     }
   }
-  gemm_skinny<NT, W, U, PARTIALS, AQ><<<tiles, W * 64, lds, stream>>>(grp, bias_dtype, y_dtype, partials, M, K);
+  gemm_skinny<NT, W, U, PARTIALS, AQ><<<tiles, W * 64, lds, stream>>>(grp, bias_dtype, y_dtype, M, K);
 }
 
 template <bool PARTIALS, int AQ>
-void launch_skinny(const SkinnyCfg& cfg, const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int32_t* partials,
-                   int M, int K, hipStream_t stream) {
+void launch_skinny(const SkinnyCfg& cfg, const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int M, int K,
+                   hipStream_t stream) {
 #define PQ_SKINNY(NT_, W_, U_)                                                                         \
   if (cfg.nt == NT_ && cfg.w == W_ && cfg.u == U_) {                                                   \
-    launch_skinny_nwu<NT_, W_, U_, PARTIALS, AQ>(grp, bias_dtype, y_dtype, partials, M, K, stream);    \
+    launch_skinny_nwu<NT_, W_, U_, PARTIALS, AQ>(grp, bias_dtype, y_dtype, M, K, stream);              \
     return;                                                                                            \
   }
 #define PQ_SKINNY_NT(NT_)                                                                              \
@@ -835,8 +861,8 @@ void launch_skinny(const SkinnyCfg& cfg, const pq::GemmGroup& grp, int bias_dtyp
 #undef PQ_SKINNY
   // every configuration choose_skinny makes is listed above; anything else
   // runs the generic one (any G, masked batches)
-  if (cfg.nt == 2) launch_skinny_nwu<2, 4, 4, PARTIALS, AQ>(grp, bias_dtype, y_dtype, partials, M, K, stream);
-  else launch_skinny_nwu<1, 4, 4, PARTIALS, AQ>(grp, bias_dtype, y_dtype, partials, M, K, stream);
+  if (cfg.nt == 2) launch_skinny_nwu<2, 4, 4, PARTIALS, AQ>(grp, bias_dtype, y_dtype, M, K, stream);
+  else launch_skinny_nwu<1, 4, 4, PARTIALS, AQ>(grp, bias_dtype, y_dtype, M, K, stream);
 }
 
 // The decode GEMM's configuration for a group: the workgroup count is the
@@ -874,16 +900,28 @@ bool gemm_rotated_supported(int64_t m, int64_t k) {
 
 void launch_gemm_group(GemmGroup grp, int aq, int bias_dtype, int y_dtype, int m, int k, hipStream_t stream) {
   if (aq == 0 && m > kSkinnyMaxM) {
-    launch_prefill<false>(grp, bias_dtype, y_dtype, nullptr, m, k, stream);
+    launch_prefill<false>(grp, bias_dtype, y_dtype, m, k, stream);
     return;
   }
   const SkinnyCfg cfg = choose_skinny_group(grp, m, k, aq != 0);
   if (aq == 0) {
-    launch_skinny<false, 0>(cfg, grp, bias_dtype, y_dtype, nullptr, m, k, stream);
+    launch_skinny<false, 0>(cfg, grp, bias_dtype, y_dtype, m, k, stream);
     return;
   }
-  if (aq == 1) launch_skinny<false, 1>(cfg, grp, bias_dtype, y_dtype, nullptr, m, k, stream);
-  else launch_skinny<false, 2>(cfg, grp, bias_dtype, y_dtype, nullptr, m, k, stream);
+  if (aq == 1) launch_skinny<false, 1>(cfg, grp, bias_dtype, y_dtype, m, k, stream);
+  else launch_skinny<false, 2>(cfg, grp, bias_dtype, y_dtype, m, k, stream);
+}
+
+// The same choices as launch_gemm_group, with PARTIALS instances.
+void launch_gemm_group_partials(GemmGroup grp, int aq, int m, int k, hipStream_t stream) {
+  if (aq == 0 && m > kSkinnyMaxM) {
+    launch_prefill<true>(grp, 0, 0, m, k, stream);
+    return;
+  }
+  const SkinnyCfg cfg = choose_skinny_group(grp, m, k, aq != 0);
+  if (aq == 0) launch_skinny<true, 0>(cfg, grp, 0, 0, m, k, stream);
+  else if (aq == 1) launch_skinny<true, 1>(cfg, grp, 0, 0, m, k, stream);
+  else launch_skinny<true, 2>(cfg, grp, 0, 0, m, k, stream);
 }
 }  // namespace pq
 
@@ -930,8 +968,7 @@ extern "C" int pq_w4a8_gemm_partials(const int8_t* xq, const uint8_t* wpack, con
   const int M = static_cast<int>(m), K = static_cast<int>(k);
   pq::GemmGroup grp{};
   grp.count = 1;
-  grp.mem[0] = {xq, nullptr, nullptr, nullptr, wpack, wmeta, nullptr, nullptr, static_cast<int>(n)};
-  if (m <= kSkinnyMaxM) launch_skinny<true, 0>(choose_skinny(m, n, k), grp, 0, 0, partials, M, K, s);
-  else launch_prefill<true>(grp, 0, 0, partials, M, K, s);
+  grp.mem[0] = {xq, nullptr, nullptr, nullptr, wpack, wmeta, nullptr, nullptr, static_cast<int>(n), partials};
+  pq::launch_gemm_group_partials(grp, 0, M, K, s);
   return pq::launch_status("pq_w4a8_gemm_partials launch");
 }

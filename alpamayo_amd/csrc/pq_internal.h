@@ -14,7 +14,11 @@ constexpr int kMaxGroup = 4;
 
 // One member of a GEMM group: its A operand (int8 rows xq + token scales xs,
 // or rotated rows xr + per-group maxima gmax), its packed weights, its bias
-// and its output y [m][n].
+// and its output y [m][n].  The partials instances of the kernels (the
+// parity entry points) write, instead of y, the member's int32 partials
+// [m][k/128][n] and, when the kernel quantizes A itself, the int8 image of A
+// it multiplies (a_out [m][k]) and the token scales of its epilogue
+// (as_out [m]).
 struct GemmMember {
   const int8_t* xq;
   const float* xs;
@@ -25,6 +29,9 @@ struct GemmMember {
   const void* bias;
   void* y;
   int n;
+  int32_t* partials;
+  int8_t* a_out;
+  float* as_out;
 };
 struct GemmGroup {
   GemmMember mem[kMaxGroup];
@@ -113,6 +120,10 @@ PQ_HIDDEN bool gemm_rotated_supported(int64_t m, int64_t k);
 // the kernel (gemm_rotated_supported(m, k)).
 PQ_HIDDEN void launch_gemm_group(GemmGroup grp, int aq, int bias_dtype, int y_dtype, int m, int k,
                                  hipStream_t stream);
+// launch_gemm_group's kernels, with the same configuration and tiling, in
+// their partials form: each member's int32 partials (and, for aq != 0, its
+// A image and token scales) go to the member's partials / a_out / as_out.
+PQ_HIDDEN void launch_gemm_group_partials(GemmGroup grp, int aq, int m, int k, hipStream_t stream);
 
 }  // namespace pq
 

@@ -1,6 +1,6 @@
 // The whole W4A8 linear (rotation + channel scale + per-token int8 quant +
-// int4 x int8 GEMM) behind one entry point, pq_w4a8_linear.  Two kernels
-// either way, chosen by the number of tokens m:
+// int4 x int8 GEMM) behind one entry point, pq_w4a8_linear.  Two or three
+// launches, chosen by the number of tokens m and the row length k:
 //
 //   split (decode: m * k <= 8192, one or two tokens of 4096 channels, or
 //     up to 2 tokens when k >= 8192): the rotation runs with
@@ -64,7 +64,7 @@ constexpr int kSplitRowsPerWave = 1;
 // (the decode layer at M = 17: 80.1 us with down on the row kernel).
 constexpr int kSplit3MaxRows = 32;
 bool use_split3(int64_t m, int64_t k) {
-  return !use_split(m, k) && m >= 1 && m <= kSplit3MaxRows && k >= 8192 && k <= 16384;
+  return !use_split(m, k) && m >= 1 && m <= kSplit3MaxRows && k >= 8192 && k <= 16384 && k % 128 == 0;
 }
 
 enum class Path { kSplit, kSplit3, kRows };
@@ -96,9 +96,21 @@ size_t group_workspace_size(int64_t m, int64_t k, int count) {
   return count * (a + s);
 }
 
+// Outputs of the parity entry point (pq_w4a8_linear_group_intermediates):
+// the int8 A operand and token scales each member's GEMM uses, and its int32
+// per-group partials.
+struct Probe {
+  int8_t* codes;      // [count][m][k]
+  float* xscale;      // [count][m]
+  int32_t* partials;  // member i: [m][k/128][n_i] at m * (k/128) * (n_0 + ... + n_{i-1})
+};
+
+// probe: run the linear's launches with the GEMM in its partials form and
+// return the intermediates instead of y (members' bias and y unused).
 int linear_group(const char* who, const void* x, int x_dtype, const pq_linear_member* members, int count,
                  int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot, unsigned flags, void* workspace,
-                 size_t workspace_bytes, hipStream_t s, const pq::NormArgs* norm = nullptr) {
+                 size_t workspace_bytes, hipStream_t s, const pq::NormArgs* norm = nullptr,
+                 const Probe* probe = nullptr) {
   PQ_REQUIRE(count >= 1 && count <= pq::kMaxGroup, PQ_ERR_ARG, "%s: count=%d not in 1..%d", who, count,
              pq::kMaxGroup);
   PQ_REQUIRE(members != nullptr, PQ_ERR_ARG, "%s: null member table", who);
@@ -118,7 +130,7 @@ int linear_group(const char* who, const void* x, int x_dtype, const pq_linear_me
     PQ_REQUIRE(mb.n > 0 && mb.n % 16 == 0 && mb.n <= (1 << 20), PQ_ERR_ARG,
                "%s: member %d: n=%lld must be a positive multiple of 16", who, i, (long long)mb.n);
     PQ_REQUIRE(mb.n * k / 2 < (int64_t(1) << 31), PQ_ERR_ARG, "%s: member %d: n*k/2 must stay below 2^31", who, i);
-    any_bias = any_bias || mb.bias != nullptr;
+    any_bias = any_bias || (mb.bias != nullptr && probe == nullptr);
   }
   PQ_REQUIRE(!any_bias || bias_dtype == PQ_F32 || bias_dtype == PQ_F16 || bias_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED,
              "%s: bias dtype code %d", who, bias_dtype);
@@ -127,12 +139,16 @@ int linear_group(const char* who, const void* x, int x_dtype, const pq_linear_me
   PQ_REQUIRE(x && pq::aligned_to(x, 16), PQ_ERR_ARG, "%s: x must be non-null and 16-byte aligned", who);
   for (int i = 0; i < count; ++i) {
     const pq_linear_member& mb = members[i];
-    PQ_REQUIRE(mb.rot_idx && mb.rot_cs && mb.wpack && mb.wmeta && mb.y, PQ_ERR_ARG, "%s: member %d: null pointer",
-               who, i);
+    PQ_REQUIRE(mb.rot_idx && mb.rot_cs && mb.wpack && mb.wmeta && (mb.y || probe), PQ_ERR_ARG,
+               "%s: member %d: null pointer", who, i);
     PQ_REQUIRE(pq::aligned_to(mb.rot_idx, 16) && pq::aligned_to(mb.rot_cs, 16) && pq::aligned_to(mb.wpack, 16) &&
-                   pq::aligned_to(mb.wmeta, 4) && pq::aligned_to(mb.y, pq::dtype_size(y_dtype)),
+                   pq::aligned_to(mb.wmeta, 4) && (probe || pq::aligned_to(mb.y, pq::dtype_size(y_dtype))),
                PQ_ERR_ARG, "%s: member %d: misaligned pointer", who, i);
   }
+  if (probe != nullptr)
+    PQ_REQUIRE(probe->codes && probe->xscale && probe->partials && pq::aligned_to(probe->codes, 16) &&
+                   pq::aligned_to(probe->xscale, 4) && pq::aligned_to(probe->partials, 4),
+               PQ_ERR_ARG, "%s: codes (16-byte aligned), xscale and partials must be non-null", who);
   const size_t need = group_workspace_size(m, k, count);
   PQ_REQUIRE(workspace != nullptr && workspace_bytes >= need && pq::aligned_to(workspace, 256), PQ_ERR_WORKSPACE,
              "%s: a 256-byte aligned workspace of %zu bytes is needed for m=%lld k=%lld count=%d, got %zu", who,
@@ -181,8 +197,58 @@ int linear_group(const char* who, const void* x, int x_dtype, const pq_linear_me
   }
   if (st != PQ_OK) return st;
   const int aq = path == Path::kSplit ? (mat16 ? 1 : 2) : 0;
-  pq::launch_gemm_group(gg, aq, bias_dtype, y_dtype, M, K, s);
-  return pq::launch_status("linear GEMM launch");
+  if (probe == nullptr) {
+    pq::launch_gemm_group(gg, aq, bias_dtype, y_dtype, M, K, s);
+    return pq::launch_status("linear GEMM launch");
+  }
+  // Parity form.  On the split pair path the GEMM writes the A image it
+  // quantized in its prologue; otherwise A is the int8 codes and scales the
+  // earlier launches left in the workspace, copied out as they are.
+  int64_t col0 = 0;
+  for (int i = 0; i < count; ++i) {
+    gg.mem[i].partials = probe->partials + m * (k / 128) * col0;
+    gg.mem[i].a_out = probe->codes + i * m * k;
+    gg.mem[i].as_out = probe->xscale + i * m;
+    gg.mem[i].y = nullptr;
+    gg.mem[i].bias = nullptr;
+    col0 += members[i].n;
+    if (path != Path::kSplit) {
+      hipError_t e = hipMemcpyAsync(gg.mem[i].a_out, gg.mem[i].xq, static_cast<size_t>(m * k), hipMemcpyDeviceToDevice, s);
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(gg.mem[i].as_out, gg.mem[i].xs, static_cast<size_t>(m) * sizeof(float),
+                           hipMemcpyDeviceToDevice, s);
+      PQ_REQUIRE(e == hipSuccess, PQ_ERR_HIP, "%s: copy of member %d's A operand: %s", who, i, hipGetErrorString(e));
+    }
+  }
+  pq::launch_gemm_group_partials(gg, aq, M, K, s);
+  return pq::launch_status("linear GEMM partials launch");
+}
+
+// The prologue arguments of the fused group entry points, checked.
+int prologue_args(const char* who, const void* x2, const void* norm_weight, float eps, int mode, void* h_out,
+                  void* sum_out, int x_dtype, int64_t m, pq::NormArgs* out) {
+  PQ_REQUIRE(mode == PQ_PRO_RMSNORM || mode == PQ_PRO_ADD || mode == PQ_PRO_SWIGLU, PQ_ERR_ARG, "%s: mode %d", who,
+             mode);
+  PQ_REQUIRE(x_dtype == PQ_F32 || x_dtype == PQ_F16 || x_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED, "%s: x dtype code %d",
+             who, x_dtype);
+  if (mode == PQ_PRO_RMSNORM)
+    PQ_REQUIRE(eps >= 0.0f && eps < 1.0f, PQ_ERR_ARG, "%s: eps=%g must be in [0, 1)", who, static_cast<double>(eps));
+  if (m > 0) {
+    const size_t es = static_cast<size_t>(pq::dtype_size(x_dtype));
+    if (mode == PQ_PRO_RMSNORM)
+      PQ_REQUIRE(norm_weight != nullptr && pq::aligned_to(norm_weight, es), PQ_ERR_ARG,
+                 "%s: norm_weight must be non-null and aligned to its dtype", who);
+    else
+      PQ_REQUIRE(x2 != nullptr, PQ_ERR_ARG, "%s: mode %d needs x2 (the residual / up rows)", who, mode);
+    PQ_REQUIRE(x2 == nullptr || pq::aligned_to(x2, 16), PQ_ERR_ARG, "%s: x2 (the residual or up rows) must be 16-byte aligned", who);
+    PQ_REQUIRE((h_out == nullptr || pq::aligned_to(h_out, es)) && (sum_out == nullptr || pq::aligned_to(sum_out, es)),
+               PQ_ERR_ARG, "%s: h_out and sum_out must be aligned to x's dtype", who);
+    PQ_REQUIRE(sum_out == nullptr || (mode != PQ_PRO_SWIGLU && x2 != nullptr), PQ_ERR_ARG,
+               "%s: sum_out needs a residual (and no SwiGLU)", who);
+    PQ_REQUIRE(h_out == nullptr || mode != PQ_PRO_ADD, PQ_ERR_ARG, "%s: h_out has no meaning for the add", who);
+  }
+  *out = {x2, mode == PQ_PRO_RMSNORM ? norm_weight : nullptr, h_out, sum_out, eps, mode};
+  return PQ_OK;
 }
 
 }  // namespace
@@ -271,29 +337,27 @@ extern "C" int pq_w4a8_linear_group_fused(const void* x, const void* x2, const v
                                           int count, int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot,
                                           unsigned flags, void* workspace, size_t workspace_bytes, void* stream) {
   const char* who = "pq_w4a8_linear_group_fused";
-  PQ_REQUIRE(mode == PQ_PRO_RMSNORM || mode == PQ_PRO_ADD || mode == PQ_PRO_SWIGLU, PQ_ERR_ARG, "%s: mode %d", who,
-             mode);
-  PQ_REQUIRE(x_dtype == PQ_F32 || x_dtype == PQ_F16 || x_dtype == PQ_BF16, PQ_ERR_UNSUPPORTED, "%s: x dtype code %d",
-             who, x_dtype);
-  if (mode == PQ_PRO_RMSNORM)
-    PQ_REQUIRE(eps >= 0.0f && eps < 1.0f, PQ_ERR_ARG, "%s: eps=%g must be in [0, 1)", who, static_cast<double>(eps));
-  if (m > 0) {
-    const size_t es = static_cast<size_t>(pq::dtype_size(x_dtype));
-    if (mode == PQ_PRO_RMSNORM)
-      PQ_REQUIRE(norm_weight != nullptr && pq::aligned_to(norm_weight, es), PQ_ERR_ARG,
-                 "%s: norm_weight must be non-null and aligned to its dtype", who);
-    else
-      PQ_REQUIRE(x2 != nullptr, PQ_ERR_ARG, "%s: mode %d needs x2 (the residual / up rows)", who, mode);
-    PQ_REQUIRE(x2 == nullptr || pq::aligned_to(x2, 16), PQ_ERR_ARG, "%s: x2 (the residual or up rows) must be 16-byte aligned", who);
-    PQ_REQUIRE((h_out == nullptr || pq::aligned_to(h_out, es)) && (sum_out == nullptr || pq::aligned_to(sum_out, es)),
-               PQ_ERR_ARG, "%s: h_out and sum_out must be aligned to x's dtype", who);
-    PQ_REQUIRE(sum_out == nullptr || (mode != PQ_PRO_SWIGLU && x2 != nullptr), PQ_ERR_ARG,
-               "%s: sum_out needs a residual (and no SwiGLU)", who);
-    PQ_REQUIRE(h_out == nullptr || mode != PQ_PRO_ADD, PQ_ERR_ARG, "%s: h_out has no meaning for the add", who);
-  }
-  const pq::NormArgs pro = {x2, mode == PQ_PRO_RMSNORM ? norm_weight : nullptr, h_out, sum_out, eps, mode};
+  pq::NormArgs pro{};
+  const int st = prologue_args(who, x2, norm_weight, eps, mode, h_out, sum_out, x_dtype, m, &pro);
+  if (st != PQ_OK) return st;
   return linear_group(who, x, x_dtype, members, count, bias_dtype, y_dtype, m, k, krot, flags, workspace,
                       workspace_bytes, static_cast<hipStream_t>(stream), &pro);
+}
+
+extern "C" int pq_w4a8_linear_group_intermediates(const void* x, const void* x2, const void* norm_weight, float eps,
+                                                  int mode, void* h_out, void* sum_out, int x_dtype,
+                                                  const pq_linear_member* members, int count, int64_t m, int64_t k,
+                                                  int krot, unsigned flags, void* workspace, size_t workspace_bytes,
+                                                  int8_t* codes, float* xscale, int32_t* partials, void* stream) {
+  const char* who = "pq_w4a8_linear_group_intermediates";
+  pq::NormArgs pro{};
+  if (mode != 0) {
+    const int st = prologue_args(who, x2, norm_weight, eps, mode, h_out, sum_out, x_dtype, m, &pro);
+    if (st != PQ_OK) return st;
+  }
+  const Probe probe = {codes, xscale, partials};
+  return linear_group(who, x, x_dtype, members, count, PQ_BF16, PQ_BF16, m, k, krot, flags, workspace,
+                      workspace_bytes, static_cast<hipStream_t>(stream), mode != 0 ? &pro : nullptr, &probe);
 }
 
 extern "C" int pq_w4a8_linear_group_rmsnorm(const void* x, const void* residual, const void* norm_weight, float eps,

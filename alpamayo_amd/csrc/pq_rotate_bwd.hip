@@ -311,7 +311,9 @@ extern "C" int pq_rotate_backward(const void* x, const void* grad_y, void* grad_
              "%s: Unsupported KROT = %d; compiled variants: 1/2/4/8/16", who, krot);
   PQ_REQUIRE(h % group_size == 0, PQ_ERR_ARG, "%s: h must be divisible by GROUP_SIZE (h=%lld, G=%d)", who,
              (long long)h, group_size);
-  PQ_REQUIRE(h <= (1 << 24), PQ_ERR_ARG, "%s: h=%lld too large", who, (long long)h);
+  // (h + 127) / 128 channel blocks go on grid.y, whose limit is 65535
+  PQ_REQUIRE(h <= 65535LL * 128, PQ_ERR_ARG, "%s: h=%lld too large (at most %lld)", who, (long long)h,
+             65535LL * 128);
   PQ_REQUIRE(dtype == PQ_F32 || dtype == PQ_F16 || dtype == PQ_BF16, PQ_ERR_UNSUPPORTED,
              "%s: dtype code %d (Float, Half or BFloat16)", who, dtype);
   PQ_REQUIRE((rows + kBwdRows - 1) / kBwdRows <= 0x7fffffffLL, PQ_ERR_ARG, "%s: too many rows", who);

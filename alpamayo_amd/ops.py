@@ -37,7 +37,6 @@ explicit workspace argument instead.
 
 from __future__ import annotations
 
-import ctypes
 import weakref
 from collections import OrderedDict
 
@@ -219,7 +218,9 @@ def register_packed_rotation(idx_ij, theta, scales, rot_idx, rot_cs, scales_f32)
 
 def _packed_for(idx_ij, theta, scales, group_size):
     """The registered (rot_idx, rot_cs, scales_f32) of these tensors, or None: nothing registered, a stale
-    entry, group 64, or angles that require grad (trained: they change every step)."""
+    entry, group 64, angles that require grad (trained: they change every step), or tensors made under
+    torch.inference_mode(), which carry no version counter, so an in-place change to them could not be seen
+    (the op then derives its parameters on the device: same results)."""
     if group_size != 128 or theta.requires_grad:
         return None
     srcs = (idx_ij, theta, scales)
@@ -227,7 +228,10 @@ def _packed_for(idx_ij, theta, scales, group_size):
     if ent is None:
         return None
     refs, state, packed = ent
-    if state != _tensor_state(srcs) or not all(r() is t for r, t in zip(refs, srcs)):
+    now = _tensor_state(srcs)
+    if any(st is not None and st[1] is None for st in now):
+        return None
+    if state != now or not all(r() is t for r, t in zip(refs, srcs)):
         return None
     if packed[0].device != idx_ij.device:
         return None
@@ -768,6 +772,50 @@ def linear_group_workspace_bytes(m: int, k: int, count: int) -> int:
     return int(_lib.load().pq_w4a8_linear_group_workspace_size(m, k, count))
 
 
+def w4a8_linear_group_intermediates(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, input_fp16=True,
+                                    materialize_fp16=True, x2=None, norm_weight=None, eps=0.0, mode=0,
+                                    return_h=False, return_sum=False):
+    """Parity probe of the grouped W4A8 linear (pq_w4a8_linear_group_intermediates; not a torch op and not a
+    fast path).  Runs the launches paroquant::w4a8_linear_group (mode 0) or
+    paroquant::w4a8_linear_group_fused (mode PQ_PRO_*, with x2 / norm_weight / eps as there) make for these
+    sizes, with the GEMM in its partials form, and returns per member what that GEMM multiplied and summed:
+    (codes int8 [count, m, k], xscale float32 [count, m], [partials int32 [m, k/128, n_i] per member],
+    h or None, s or None)."""
+    dev = x.device
+    _require(x.dtype in _DT, f"x must be float32/float16/bfloat16, got {x.dtype}")
+    xc = x.contiguous()
+    k = xc.size(-1)
+    nb = [None] * len(wpack)
+    members, _, keep, _, m, _ = _group_members(xc, rot_idx, rot_cs, scales, krot, wpack, wmeta, nb, torch.bfloat16)
+    count = len(wpack)
+    G = k // 128
+    codes = torch.empty((count, m, k), dtype=torch.int8, device=dev)
+    xscale = torch.empty((count, m), dtype=torch.float32, device=dev)
+    ns = [int(members[i].n) for i in range(count)]
+    flat = torch.empty(m * G * sum(ns), dtype=torch.int32, device=dev)
+    parts, off = [], 0
+    for n in ns:
+        parts.append(flat[off:off + m * G * n].view(m, G, n))
+        off += m * G * n
+    other = x2.contiguous() if x2 is not None else None
+    w = norm_weight.contiguous() if norm_weight is not None else None
+    h = torch.empty_like(xc) if return_h else None
+    sm = torch.empty_like(xc) if return_sum else None
+    scratch = _group_scratch(m, k, count, dev)
+    flags = (_lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0) | (_lib.PQ_RQ_MATERIALIZE_FP16 if materialize_fp16 else 0)
+    lib = _lib.load()
+    with _DeviceGuard(dev):
+        st = lib.pq_w4a8_linear_group_intermediates(
+            xc.data_ptr(), other.data_ptr() if other is not None else None, w.data_ptr() if w is not None else None,
+            float(eps), int(mode), h.data_ptr() if h is not None else None,
+            sm.data_ptr() if sm is not None else None, _DT[x.dtype], members, count, m, k, krot, flags,
+            scratch.data_ptr() if scratch is not None else None, scratch.numel() if scratch is not None else 0,
+            codes.data_ptr(), xscale.data_ptr(), flat.data_ptr(), _stream(dev))
+    _lib.check(st, "pq_w4a8_linear_group_intermediates")
+    del keep
+    return codes, xscale, parts, h, sm
+
+
 @torch.library.register_fake("paroquant::w4a8_linear")
 def _linear_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, input_fp16, materialize_fp16, out_dtype):
     return x.new_empty((*x.shape[:-1], wpack.size(0) * 16), dtype=out_dtype)
@@ -909,33 +957,3 @@ def _w16_linear_group_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias,
 @torch.library.register_fake("paroquant::w4a16_linear")
 def _w16_linear_fake(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, input_fp16, out_dtype):
     return x.new_empty((*x.shape[:-1], wpack.size(0) * 16), dtype=out_dtype)
-
-
-# ---------------------------------------------------------------------------
-# weight prefetch (decode): pq_prefetch
-# ---------------------------------------------------------------------------
-
-_PREFETCH_MAX = 16
-
-
-def prefetch(tensors, blocks: int = 0) -> None:
-    """Reads the tensors' device memory once (one load per 128-byte line) on the current stream so that a later
-    kernel finds it in L2 / the Infinity Cache.  It writes nothing and needs no synchronization for
-    correctness.  A measurement option (bench.py --decode-prefetch): at one decode token the reads cost more
-    than the GEMM saves, so the linear path does not call it.  blocks: workgroups per tensor (0 = the
-    library's default)."""
-    ts = [t for t in tensors if t is not None and t.numel() > 0]
-    if not ts:
-        return
-    dev = ts[0].device
-    lib = _lib.load()
-    for i in range(0, len(ts), _PREFETCH_MAX):
-        chunk = ts[i:i + _PREFETCH_MAX]
-        for t in chunk:
-            _same_device("prefetch tensor", t, dev)
-            _require(t.is_contiguous(), "prefetch: tensors must be contiguous")
-        ptrs = (ctypes.c_void_p * len(chunk))(*[t.data_ptr() for t in chunk])
-        sizes = (ctypes.c_size_t * len(chunk))(*[(t.numel() * t.element_size()) // 4 * 4 for t in chunk])
-        with _DeviceGuard(dev):
-            st = lib.pq_prefetch(ptrs, sizes, len(chunk), int(blocks), _stream(dev))
-        _lib.check(st, "prefetch")

@@ -111,7 +111,9 @@ class Rotation(nn.Module):
     @property
     def prepared(self) -> bool:
         """True while the packed operands were derived from the current theta / pairs / channel_scales:
-        False again after load_state_dict, an in-place update or a move of any of them."""
+        False again after load_state_dict, an in-place update or a move of any of them.  Buffers created under
+        torch.inference_mode() carry no version counter, so only a replacement or a move of them is seen:
+        after changing such a buffer in place, call prepare()."""
         return self.rot_cs.numel() > 0 and self._prep_src == self._param_source()
 
 

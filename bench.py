@@ -123,11 +123,6 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first copy 256 MiB device to device 3 times: the known-size kernel that calibrates "
                          "the FETCH_SIZE / WRITE_SIZE counter passes")
-    ap.add_argument("--decode-prefetch", choices=("none", "serial", "side"), default="none",
-                    help="measurement mode for the grouped decode layers: before each linear, read its weights "
-                         "into the caches with pq_prefetch on the same stream (serial), or read the next "
-                         "linear's weights on a second stream of the same priority joined at the end of the "
-                         "graph (side); none = the product path")
     ap.add_argument("--decode-m", type=str, default="1,4,16",
                     help="comma-separated decode token counts to time (M = 1 gives value)")
     args = ap.parse_args()
@@ -177,54 +172,27 @@ def main() -> int:
         g = workloads.generator(seed, device=dev)
         return [tuple(workloads.activations(M, K, g, device=dev) for K in (4096, 4096, 4096, 12288)) for _ in pool]
 
-    def layer_weights(li):
-        """The weight tensors each grouped call of layer li streams: q/k/v, o, gate/up, down."""
-        L = pool[li]
-        w = [[t for m in mods for t in (m.rotate_linear.qlinear.qweight, m.rotate_linear.qlinear.scales)]
-             for mods in (L[0:3], L[3:4], L[4:6], L[6:7])]
-        return w
-
-    side = torch.cuda.Stream() if args.decode_prefetch == "side" else None
-
-    def run_layer(li, X, grouped, prefetch="none"):
+    def run_layer(li, X, grouped):
         L = pool[li]
         xa, xo, xm, xd = X
         if grouped:
             qkv, gu = groups[li]
-            calls = [lambda: qkv(xa), lambda: [L[3](xo)], lambda: gu(xm), lambda: [L[6](xd)]]
-            if prefetch == "none":
-                return [y for c in calls for y in c()]
-            w = layer_weights(li)
-            w_next = layer_weights((li + 1) % len(pool))
-            out = []
-            main = torch.cuda.current_stream()
-            for i, c in enumerate(calls):
-                if prefetch == "serial":
-                    alpamayo_amd.ops.prefetch(w[i], 256)
-                else:
-                    side.wait_stream(main)
-                    with torch.cuda.stream(side):
-                        alpamayo_amd.ops.prefetch(w[i + 1] if i + 1 < len(w) else w_next[0], 256)
-                out += c()
-            if prefetch == "side":
-                main.wait_stream(side)
-            return out
+            return [*qkv(xa), L[3](xo), *gu(xm), L[6](xd)]
         return [L[0](xa), L[1](xa), L[2](xa), L[3](xo), L[4](xm), L[5](xm), L[6](xd)]
 
     def capture_layers(M, seed, grouped, n_layers=None):
         """One HIP graph holding the pool's layers (the first n_layers of them) in sequence, as a
         model's decode step is captured whole: a replay is that many steps."""
         xs = make_inputs(M, seed)[:n_layers]
-        pf = args.decode_prefetch if grouped else "none"
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             for li, X in enumerate(xs):
-                run_layer(li, X, grouped, pf)
+                run_layer(li, X, grouped)
         torch.cuda.current_stream().wait_stream(s)
         gr = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gr):
-            outs = [run_layer(li, X, grouped, pf) for li, X in enumerate(xs)]
+            outs = [run_layer(li, X, grouped) for li, X in enumerate(xs)]
         return gr, outs, xs
 
     def time_exact_steps(M, seed, grouped, steps, warmup):
@@ -699,7 +667,6 @@ def main() -> int:
                              "frac_hbm": round(v[1] / HBM_PEAK_GBS, 4),
                              "separate_linears_us_per_layer": round(decode_sep[M][0] * 1e3, 2),
                              "separate_linears_GBps": round(decode_sep[M][1], 1)} for M, v in decode.items()},
-        **({"decode_prefetch": args.decode_prefetch} if args.decode_prefetch != "none" else {}),
         "prefill_M3072": prefill,
         "verify_block_M16": verify,
         "ragged_batch": ragged,

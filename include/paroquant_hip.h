@@ -307,18 +307,6 @@ int pq_w4a8_linear_group_rmsnorm(const void* x, const void* residual, const void
                                  int count, int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot,
                                  unsigned flags, void* workspace, size_t workspace_bytes, void* stream);
 
-/* Reads count (0..16) byte ranges of device memory once, one 4-byte load per
- * 128-byte line, so that a kernel launched later finds those lines in the
- * GPU's caches (L2 and the Infinity Cache in front of HBM).  A measurement
- * option, not part of the linear path: at one decode token a GEMM whose
- * weights were read ahead runs 0.4-1.4 us faster, but reading them costs
- * about 6 us per linear on the same stream, and on a second stream of the
- * same priority the two branches of a captured graph compete for HBM.  Each
- * range pointer 4-byte aligned, each size a multiple of 4 (0 = skipped);
- * blocks = workgroups per range (0 = 64).  Writes nothing.  No counterpart in
- * the reference. */
-int pq_prefetch(const void* const* ptrs, const size_t* bytes, int count, int blocks, void* stream);
-
 /* ---- W4A16 (fp16 activations, no activation quant) ---- */
 
 /* Repack WQLinear weights for pq_w4a16_gemm: awq_qweight int32 [k, n/8] (the
@@ -393,6 +381,30 @@ int pq_w4a8_linear_group_fused(const void* x, const void* x2, const void* norm_w
                                void* h_out, void* sum_out, int x_dtype, const pq_linear_member* members, int count,
                                int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot, unsigned flags,
                                void* workspace, size_t workspace_bytes, void* stream);
+
+/* Parity form of pq_w4a8_linear_group (mode 0) and pq_w4a8_linear_group_fused
+ * (mode PQ_PRO_*, prologue arguments as there): the same launches, chosen by
+ * the same rules, up to the GEMM, whose kernel runs in its partials form
+ * (same configuration, tiling and MFMA code; its epilogue replaced by stores
+ * of the int32 accumulators).  Instead of y it returns, per member i:
+ *   codes    int8  [count][m][k]   the int8 activation codes the GEMM multiplied
+ *                                  (16-byte aligned);
+ *   xscale   float [count][m]      the token scales its epilogue applies;
+ *   partials int32 per-group partials sum_{k in g} (q[k, n] - z[g, n]) * codes[m, k],
+ *            member i's [m][k/128][n_i] block at m*(k/128)*(n_0+...+n_{i-1}).
+ * On the split pair path (one GEMM quantizing A in its prologue) codes and
+ * xscale are the LDS image of A and the scales that kernel derived (written
+ * by each member's first workgroup); on the other paths they are the codes
+ * and scales the rotate+quant launches left in the workspace.  Members' bias
+ * and y are not used.  A debugging / test entry point, not a fast path: it
+ * exists so that the intermediates of every production path can be checked
+ * against the reference semantics (per-token int8 quant and the Marlin
+ * GEMM's int32 accumulators, paroquant_marlin_w4a8.py:319-333). */
+int pq_w4a8_linear_group_intermediates(const void* x, const void* x2, const void* norm_weight, float eps, int mode,
+                                       void* h_out, void* sum_out, int x_dtype, const pq_linear_member* members,
+                                       int count, int64_t m, int64_t k, int krot, unsigned flags, void* workspace,
+                                       size_t workspace_bytes, int8_t* codes, float* xscale, int32_t* partials,
+                                       void* stream);
 
 #ifdef __cplusplus
 }

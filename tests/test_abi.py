@@ -350,23 +350,8 @@ def test_split_path_python_rule_matches_library():
         for m in list(range(0, 40)) + [63, 64, 96, 1000, 3072]:
             assert ops.split_path(m, k) == bool(lib.pq_w4a8_linear_split_path(m, k)), (m, k)
     assert ops.split_path(1, 16384 + 128) == bool(lib.pq_w4a8_linear_split_path(1, 16384 + 128))
+    # depths that are not a multiple of 128 take neither split path, in either form
+    for k in (8200, 12290, 4100, 100):
+        for m in (1, 2, 3, 17, 32):
+            assert not ops.split_path(m, k) and not lib.pq_w4a8_linear_split_path(m, k), (m, k)
 
-
-def test_prefetch_argument_checks():
-    lib = _lib.load()
-    P = ctypes.c_void_p * 17
-    S = ctypes.c_size_t * 17
-    ptrs = P(*([16] * 17))
-    sizes = S(*([64] * 17))
-    assert lib.pq_prefetch(ptrs, sizes, 17, 0, None) == 1
-    assert "count" in _err(lib)
-    assert lib.pq_prefetch(ptrs, sizes, -1, 0, None) == 1
-    assert lib.pq_prefetch(ptrs, sizes, 1, 65536, None) == 1
-    assert "blocks" in _err(lib)
-    assert lib.pq_prefetch(None, None, 2, 0, None) == 1
-    assert "null" in _err(lib)
-    assert lib.pq_prefetch(P(18), S(64), 1, 0, None) == 1          # misaligned range
-    assert lib.pq_prefetch(P(16), S(62), 1, 0, None) == 1          # not whole 4-byte words
-    assert lib.pq_prefetch(P(0), S(64), 1, 0, None) == 1           # null range
-    assert lib.pq_prefetch(P(16), S(0), 1, 0, None) == 0           # empty ranges are skipped: nothing to launch
-    assert lib.pq_prefetch(None, None, 0, 0, None) == 0

@@ -21,14 +21,17 @@ from tests.test_gpu_group import _members, _oracle
 pytestmark = pytest.mark.gpu
 
 CASES = [
-    # (M, K, member Ns): split rotation (M*K <= 12288, or M <= 4 for K >= 8192), the row
-    # rotate+quant path, ragged row counts
+    # (M, K, member Ns): the split pair (M*K <= 8192, or M <= 2 for K >= 8192), the three-launch
+    # long-row path (K >= 8192 up to 32 tokens), the row rotate+quant path, ragged row counts
     (1, 4096, (4096, 1024, 1024)),
     (1, 12288, (4096,)),
     (3, 12288, (4096,)),
     (7, 12288, (1024, 48)),
     (3, 4096, (1024, 1024)),
     (16, 12288, (4096,)),
+    (17, 12288, (4096,)),
+    (24, 12288, (1024, 48)),
+    (32, 16384, (4096,)),
     (300, 4096, (4096, 1024)),
     (1029, 2048, (1040, 16)),
 ]
