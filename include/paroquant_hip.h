@@ -207,14 +207,16 @@ int pq_w4a8_prepack(const int32_t* awq_qweight, const uint16_t* awq_scales,
                     const int32_t* awq_qzeros, uint8_t* wpack, uint32_t* wmeta, int64_t k,
                     int64_t n, int group_size, void* stream);
 
-/* Bytes of scratch pq_w4a8_linear needs between its kernels: for decode
- * sizes (m*k <= 12288, or m <= 4 when k >= 8192; pq_w4a8_linear_split_path)
- * the rotated rows and per-group maxima, m*k*4 rounded
- * up to 256 plus 4*m*(k/128) bytes; for k >= 8192 beyond that up to m = 16,
- * both of those plus the int8 activations and their scales (m*k rounded up
- * to 256, plus 4*m); otherwise the int8 activations and their scales only,
- * m*k rounded up to 256 plus 4*m bytes.  The scratch is written
- * before it is read; its content does not matter. */
+/* Bytes of scratch pq_w4a8_linear needs between its kernels.  Size it with
+ * this function rather than a formula of your own; the rule it follows is:
+ *   split pair (m*k <= 8192, or k >= 8192 and m <= 2): the rotated rows and
+ *     per-group maxima, m*k*4 rounded up to 256 plus 4*m*(k/128) bytes;
+ *   three-launch long rows (k a multiple of 128 in [8192, 16384], beyond the
+ *     split pair, up to m = 32): both of those plus the int8 activations and
+ *     their scales (m*k rounded up to 256, plus 4*m);
+ *   otherwise (the row rotate+quant kernel): the int8 activations and their
+ *     scales only, m*k rounded up to 256 plus 4*m bytes.
+ * The scratch is written before it is read; its content does not matter. */
 size_t pq_w4a8_linear_workspace_size(int64_t m, int64_t n, int64_t k, int krot);
 
 /* y = W4A8 GEMM of the per-token int8 quantization of the rotation of x:
@@ -265,11 +267,13 @@ typedef struct pq_linear_member {
 
 /* 1 when pq_w4a8_linear (and the group entry points) run m tokens of k
  * features through the split rotation (waves per 128-channel group, spread
- * over the chip): with a GEMM that quantizes A in its prologue, or for long
- * rows (k >= 8192, up to 16 tokens) with a token-scale + int8 kernel and the
- * GEMM on int8 A.  0 when they run the row rotate+quant kernel plus the GEMM.  Callers use it to decide whether an
- * elementwise step is cheaper fused into the rotation launch (it is on the
- * split path) or as a separate kernel.  No counterpart in the reference. */
+ * over the chip): with a GEMM that quantizes A in its prologue (m*k <= 8192,
+ * or k >= 8192 and m <= 2), or for long rows (k a multiple of 128 in
+ * [8192, 16384], up to 32 tokens) with a token-scale + int8 kernel and the
+ * GEMM on int8 A.  0 when they run the row rotate+quant kernel plus the
+ * GEMM.  Callers use it to decide whether an elementwise step is cheaper
+ * fused into the rotation launch (it is on the split path) or as a separate
+ * kernel.  No counterpart in the reference. */
 int pq_w4a8_linear_split_path(int64_t m, int64_t k);
 
 /* Bytes of workspace pq_w4a8_linear_group needs for count members sharing an
