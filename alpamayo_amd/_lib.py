@@ -74,6 +74,9 @@ SIGNATURES = {
     "pq_w4a8_linear_split_path": (_INT, [_I64, _I64]),
     "pq_w4a8_linear_group_fused": (_INT, [_P, _P, _P, ctypes.c_float, _INT, _P, _P, _INT, ctypes.POINTER(LinearMember),
                                           _INT, _INT, _INT, _I64, _I64, _INT, _UINT, _P, _SZ, _P]),
+    "pq_w4a8_linear_group_stage": (_INT, [_INT, _P, _P, _P, ctypes.c_float, _INT, _P, _P, _INT,
+                                          ctypes.POINTER(LinearMember), _INT, _INT, _INT, _I64, _I64, _INT, _UINT,
+                                          _P, _SZ, _P]),
     "pq_w4a8_linear_group_intermediates": (_INT, [_P, _P, _P, ctypes.c_float, _INT, _P, _P, _INT,
                                                   ctypes.POINTER(LinearMember), _INT, _I64, _I64, _INT, _UINT, _P,
                                                   _SZ, _P, _P, _P, _P]),

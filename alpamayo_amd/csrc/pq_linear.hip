@@ -107,10 +107,12 @@ struct Probe {
 
 // probe: run the linear's launches with the GEMM in its partials form and
 // return the intermediates instead of y (members' bias and y unused).
+// stage: 0 = every launch; 1 = the rotation (+ quant) launches only, into
+// the workspace; 2 = the GEMM launch only, from what stage 1 left there.
 int linear_group(const char* who, const void* x, int x_dtype, const pq_linear_member* members, int count,
                  int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot, unsigned flags, void* workspace,
                  size_t workspace_bytes, hipStream_t s, const pq::NormArgs* norm = nullptr,
-                 const Probe* probe = nullptr) {
+                 const Probe* probe = nullptr, int stage = 0) {
   PQ_REQUIRE(count >= 1 && count <= pq::kMaxGroup, PQ_ERR_ARG, "%s: count=%d not in 1..%d", who, count,
              pq::kMaxGroup);
   PQ_REQUIRE(members != nullptr, PQ_ERR_ARG, "%s: null member table", who);
@@ -136,7 +138,8 @@ int linear_group(const char* who, const void* x, int x_dtype, const pq_linear_me
              "%s: bias dtype code %d", who, bias_dtype);
   if (m == 0) return PQ_OK;
   PQ_REQUIRE(m * k < (int64_t(1) << 31), PQ_ERR_ARG, "%s: m*k=%lld must stay below 2^31", who, (long long)(m * k));
-  PQ_REQUIRE(x && pq::aligned_to(x, 16), PQ_ERR_ARG, "%s: x must be non-null and 16-byte aligned", who);
+  PQ_REQUIRE(stage == 2 || (x && pq::aligned_to(x, 16)), PQ_ERR_ARG, "%s: x must be non-null and 16-byte aligned",
+             who);
   for (int i = 0; i < count; ++i) {
     const pq_linear_member& mb = members[i];
     PQ_REQUIRE(mb.rot_idx && mb.rot_cs && mb.wpack && mb.wmeta && (mb.y || probe), PQ_ERR_ARG,
@@ -183,7 +186,9 @@ int linear_group(const char* who, const void* x, int x_dtype, const pq_linear_me
     }
   }
   int st = PQ_OK;
-  if (path == Path::kRows) {
+  if (stage == 2) {
+    // the GEMM alone, from the workspace stage 1 filled
+  } else if (path == Path::kRows) {
     pq::launch_rotate_quant_group(x, x_dtype, rg, m, K, krot, flags, s, norm);
     st = pq::launch_status("linear rotate+quant launch");
   } else {
@@ -195,7 +200,7 @@ int linear_group(const char* who, const void* x, int x_dtype, const pq_linear_me
       st = pq::launch_status("linear quant launch");
     }
   }
-  if (st != PQ_OK) return st;
+  if (st != PQ_OK || stage == 1) return st;
   const int aq = path == Path::kSplit ? (mat16 ? 1 : 2) : 0;
   if (probe == nullptr) {
     pq::launch_gemm_group(gg, aq, bias_dtype, y_dtype, M, K, s);
@@ -342,6 +347,23 @@ extern "C" int pq_w4a8_linear_group_fused(const void* x, const void* x2, const v
   if (st != PQ_OK) return st;
   return linear_group(who, x, x_dtype, members, count, bias_dtype, y_dtype, m, k, krot, flags, workspace,
                       workspace_bytes, static_cast<hipStream_t>(stream), &pro);
+}
+
+extern "C" int pq_w4a8_linear_group_stage(int stage, const void* x, const void* x2, const void* norm_weight, float eps,
+                                          int mode, void* h_out, void* sum_out, int x_dtype,
+                                          const pq_linear_member* members, int count, int bias_dtype, int y_dtype,
+                                          int64_t m, int64_t k, int krot, unsigned flags, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  const char* who = "pq_w4a8_linear_group_stage";
+  PQ_REQUIRE(stage == 1 || stage == 2, PQ_ERR_ARG, "%s: stage %d (1 = rotation launches, 2 = GEMM)", who, stage);
+  pq::NormArgs pro{};
+  if (stage == 1 && mode != 0) {
+    const int st = prologue_args(who, x2, norm_weight, eps, mode, h_out, sum_out, x_dtype, m, &pro);
+    if (st != PQ_OK) return st;
+  }
+  return linear_group(who, x, x_dtype, members, count, bias_dtype, y_dtype, m, k, krot, flags, workspace,
+                      workspace_bytes, static_cast<hipStream_t>(stream), stage == 1 && mode != 0 ? &pro : nullptr,
+                      nullptr, stage);
 }
 
 extern "C" int pq_w4a8_linear_group_intermediates(const void* x, const void* x2, const void* norm_weight, float eps,

@@ -772,6 +772,46 @@ def linear_group_workspace_bytes(m: int, k: int, count: int) -> int:
     return int(_lib.load().pq_w4a8_linear_group_workspace_size(m, k, count))
 
 
+class W4A8GroupStages:
+    """paroquant::w4a8_linear_group (or _fused with a prologue) split into its two stages
+    (pq_w4a8_linear_group_stage): ``rotate()`` makes the rotation (+ quant) launches into a workspace this
+    object owns, ``gemm()`` the GEMM launch from it, writing ``outs``.  Both enqueue on the current stream and
+    may be captured in graphs, separately.  Built once for fixed inputs and outputs (their addresses are
+    baked into the calls)."""
+
+    def __init__(self, x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, input_fp16=True,
+                 materialize_fp16=True, out_dtype=torch.bfloat16, x2=None, norm_weight=None, eps=0.0, mode=0):
+        self.dev = x.device
+        self.x = x.contiguous()
+        self.x2 = x2.contiguous() if x2 is not None else None
+        self.w = norm_weight.contiguous() if norm_weight is not None else None
+        self.members, self.outs, self._keep, self.bias_dt, self.m, self.k = _group_members(
+            self.x, rot_idx, rot_cs, scales, krot, wpack, wmeta, bias, out_dtype)
+        self.count = len(self.outs)
+        self.krot, self.eps, self.mode, self.out_dt = krot, float(eps), int(mode), _DT[out_dtype]
+        self.flags = ((_lib.PQ_RQ_INPUT_FP16 if input_fp16 else 0)
+                      | (_lib.PQ_RQ_MATERIALIZE_FP16 if materialize_fp16 else 0))
+        self.scratch = _group_scratch(self.m, self.k, self.count, self.dev)
+
+    def _call(self, stage):
+        lib = _lib.load()
+        sc = self.scratch
+        with _DeviceGuard(self.dev):
+            st = lib.pq_w4a8_linear_group_stage(
+                stage, self.x.data_ptr(), self.x2.data_ptr() if self.x2 is not None else None,
+                self.w.data_ptr() if self.w is not None else None, self.eps, self.mode, None, None, _DT[self.x.dtype],
+                self.members, self.count, self.bias_dt, self.out_dt, self.m, self.k, self.krot, self.flags,
+                sc.data_ptr() if sc is not None else None, sc.numel() if sc is not None else 0, _stream(self.dev))
+        _lib.check(st, f"pq_w4a8_linear_group_stage({stage})")
+
+    def rotate(self):
+        self._call(1)
+
+    def gemm(self):
+        self._call(2)
+        return self.outs
+
+
 def w4a8_linear_group_intermediates(x, rot_idx, rot_cs, scales, krot, wpack, wmeta, input_fp16=True,
                                     materialize_fp16=True, x2=None, norm_weight=None, eps=0.0, mode=0,
                                     return_h=False, return_sum=False):

@@ -45,16 +45,24 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0
 COPY_CAL_BYTES = 256 << 20
-# HBM bytes per decode-GEMM launch, measured with rocprofv3 FETCH_SIZE and
-# WRITE_SIZE passes and calibrated on a copy of known size; the summary
-# (with the commands that made it) holds it on a "traffic_bytes_per_launch:" line.
-TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "decode_gemm_m1_hbm_traffic.md")
+# HBM bytes per launch of a kernel, measured with rocprofv3 FETCH_SIZE and
+# WRITE_SIZE passes and calibrated on a copy of known size; each summary (with
+# the commands that made it) holds the figure on a "traffic_bytes_per_launch:" line.
+TRAFFIC_SUMMARIES = {
+    "decode_gemm_M1_layer": os.path.join(ROOT, "profiles", "decode_m1_layer_gemm_hbm_traffic.md"),
+    "decode_split_rotation_M1_layer": os.path.join(ROOT, "profiles", "decode_m1_layer_gemm_hbm_traffic.md"),
+    "decode_gemm_int8_a_M1": os.path.join(ROOT, "profiles", "decode_gemm_m1_hbm_traffic.md"),
+    "prefill_gemm_M3072": os.path.join(ROOT, "profiles", "prefill_m3072_gemm_hbm_traffic.md"),
+}
 
 
-def measured_traffic():
+def measured_traffic(name):
+    """The summary's traffic_bytes_per_launch figure for kernel `name` (a line "traffic_bytes_per_launch:"
+    or "traffic_bytes_per_launch[name]:"), or None."""
     try:
-        for line in open(TRAFFIC_SUMMARY):
-            if line.startswith("traffic_bytes_per_launch:"):
+        for line in open(TRAFFIC_SUMMARIES[name]):
+            if line.startswith(f"traffic_bytes_per_launch[{name}]:") or (
+                    line.startswith("traffic_bytes_per_launch:") and name == "decode_gemm_int8_a_M1"):
                 return int(line.split(":", 1)[1])
     except OSError:
         pass
@@ -72,6 +80,19 @@ def gemm_kernel_bytes(M: int, N: int, K: int) -> int:
     """Algorithmic bytes of the GEMM kernel alone: int4 codes, fp16 scales, int4 zeros,
     int8 activations + fp32 token scales in, bf16 out."""
     return N * K // 2 + 2 * N * K // 128 + N * K // 256 + M * K + 4 * M + 2 * M * N
+
+
+def rotated_gemm_bytes(M: int, N: int, K: int) -> int:
+    """Algorithmic bytes of the decode GEMM that quantizes its A operand in its prologue: int4 codes, fp16
+    scales, int4 zeros, the rotated fp16 rows and their fp32 group maxima in, bf16 out."""
+    return N * K // 2 + 2 * N * K // 128 + N * K // 256 + 2 * M * K + 4 * M * K // 128 + 2 * M * N
+
+
+def split_rotation_bytes(M: int, K: int, members: int) -> int:
+    """Algorithmic bytes of one split-rotation launch for `members` linears over one bf16 input: x read once;
+    per member its rotation parameters (fp16 angles, int16 pairs, fp16 channel scales) in, its rotated fp16
+    rows and fp32 group maxima out."""
+    return 2 * M * K + members * (3 * KROT * K + 2 * K + 2 * M * K + 4 * M * K // 128)
 
 
 def w16_linear_bytes(M: int, N: int, K: int) -> int:
@@ -114,6 +135,10 @@ def main() -> int:
     ap.add_argument("--no-ragged", action="store_true", help="skip the ragged packed batch")
     ap.add_argument("--no-w4a16", action="store_true", help="skip the W4A16 (WQLinear) figures")
     ap.add_argument("--no-mxfp4", action="store_true", help="skip the fused rotation + MXFP4 figures")
+    ap.add_argument("--no-separate", action="store_true",
+                    help="skip the decode layers with all seven linears called separately (so that a kernel "
+                         "trace's rotation and quantizing-GEMM launches all come from the grouped layer and its "
+                         "two-stage graphs)")
     ap.add_argument("--no-decode-per-shape", action="store_true",
                     help="skip the per-shape decode GEMM timing (so that a kernel trace's int8-A decode GEMM "
                          "launches all come from the roofline graph)")
@@ -123,6 +148,10 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first copy 256 MiB device to device 3 times: the known-size kernel that calibrates "
                          "the FETCH_SIZE / WRITE_SIZE counter passes")
+    ap.add_argument("--library-gemms", action="store_true",
+                    help="measurement mode: also time the vendor library's plain GEMMs at the M = 3072 shapes "
+                         "(torch._int_mm int8 -> int32, torch._scaled_mm fp8 -> bf16, bf16 matmul; hipBLASLt) "
+                         "beside this build's W4A8 GEMM")
     ap.add_argument("--decode-m", type=str, default="1,4,16",
                     help="comma-separated decode token counts to time (M = 1 gives value)")
     args = ap.parse_args()
@@ -250,13 +279,61 @@ def main() -> int:
     for M in decode_ms:
         b = sum(linear_bytes(M, N, K) for N, K in shapes)
         for grouped, table in ((True, decode), (False, decode_sep)):
+            if not grouped and args.no_separate:
+                continue
             ms = time_exact_steps(M, 5000 + M, grouped, args.steps, args.warmup)
             table[M] = (ms, b / (ms * 1e-3) / 1e9)
             log(f"decode M={M} {'grouped ' if grouped else 'separate'}: {ms * 1e3:.1f} us/layer, "
                 f"{table[M][1]:.0f} GB/s")
     ms_per_step, value = decode[1]
 
-    # ---- roofline of the dominant kernel: the decode GEMM at M = 1 --------
+    # ---- the headline layer's own kernels, each timed alone ----------------
+    # The grouped M = 1 layer in its two stages (pq_w4a8_linear_group_stage): all rotation launches
+    # (rotate_split_kernel) of the pool captured as one graph, all GEMM launches (gemm_skinny quantizing its
+    # A operand in the prologue, from the rotated rows the first stage left in the workspace) as another,
+    # each launch with exactly the configuration the layer runs.  Per launch: the GEMM moves its members'
+    # packed weights, scales and zeros, their rotated fp16 rows and group maxima, and writes bf16 y; the
+    # rotation reads x once and each member's parameters and writes its rotated fp16 rows and group maxima.
+    Mh = 1
+    stage_calls = []
+    for li, (xa, xo, xm, xd) in enumerate(make_inputs(Mh, 7002)):
+        L = pool[li]
+        for mods, x in ((L[0:3], xa), (L[3:4], xo), (L[4:6], xm), (L[6:7], xd)):
+            rls = [m.rotate_linear for m in mods]
+            st = alpamayo_amd.ops.W4A8GroupStages(
+                x, [r.rotation.rot_idx for r in rls], [r.rotation.rot_cs for r in rls],
+                [r.rotation.scales_f32 for r in rls], rls[0].rotation.krot, [r.qlinear.qweight for r in rls],
+                [r.qlinear.scales for r in rls], [r.qlinear.bias for r in rls], True, True, torch.bfloat16)
+            stage_calls.append((st, [(r.qlinear.out_features, r.qlinear.in_features) for r in rls]))
+
+    def capture_calls(fn):
+        s2 = torch.cuda.Stream()
+        s2.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s2):
+            fn()
+        torch.cuda.current_stream().wait_stream(s2)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        return g
+
+    g_rot = capture_calls(lambda: [st.rotate() for st, _ in stage_calls])
+    g_gemm = capture_calls(lambda: [st.gemm() for st, _ in stage_calls])
+    n_calls = len(stage_calls)
+    hrot_ms = time_graphs([g_rot], max(10, args.steps // 10), 3)
+    hgemm_ms = time_graphs([g_gemm], max(10, args.steps // 10), 3)
+    del g_rot, g_gemm
+    hgemm_bytes = sum(rotated_gemm_bytes(Mh, N, K) for _, shp in stage_calls for N, K in shp)
+    hrot_bytes = sum(split_rotation_bytes(Mh, shp[0][1], len(shp)) for _, shp in stage_calls)
+    hgemm_us = hgemm_ms * 1e3 / n_calls
+    hrot_us = hrot_ms * 1e3 / n_calls
+    hgemm_gbs = hgemm_bytes / (hgemm_ms * 1e-3) / 1e9
+    hrot_gbs = hrot_bytes / (hrot_ms * 1e-3) / 1e9
+    log(f"headline layer M=1, GEMM launches alone: {hgemm_us:.2f} us/launch avg, {hgemm_gbs:.0f} GB/s; "
+        f"rotation launches alone: {hrot_us:.2f} us/launch avg, {hrot_gbs:.0f} GB/s")
+    del stage_calls
+
+    # ---- the decode GEMM on int8 activations at M = 1 ---------------------
     xq_all = []
     for L, (xa, xo, xm, xd) in zip(pool, make_inputs(1, 7001)):
         row = []
@@ -367,7 +444,8 @@ def main() -> int:
             del g1
         log("prefill rotate+quant per K: " + ", ".join(f"K={k} {v['us']} us ({v['GBps']} GB/s)"
                                                        for k, v in rq_shape.items()))
-        prefill = {"ms_per_layer": round(ms, 4), "tops": round(tops, 1),
+        prefill_ops = ops
+        prefill = {"ms_per_layer": round(ms, 4), "tops": round(tops, 1), "gemm_only_ms": round(gms, 5),
                    "pct_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2),
                    "separate_linears_ms_per_layer": round(res[False], 4), "separate_linears_tops": round(tops_sep, 1),
                    "gemm_only_tops": round(gtops, 1), "gemm_only_pct_int8_peak": round(100 * gtops / INT8_PEAK_TOPS, 2),
@@ -375,6 +453,41 @@ def main() -> int:
         log(f"prefill M=3072: {ms:.3f} ms/layer grouped, {tops:.0f} TOPS ({prefill['pct_int8_peak']}%); "
             f"separate {res[False]:.3f} ms/layer, {tops_sep:.0f} TOPS; GEMMs alone {gtops:.0f} TOPS")
         del gg, xq, X
+
+    # ---- the vendor library's plain GEMMs at the prefill shapes (measurement mode) ----
+    # What a dense GEMM without int4 unpacking or group scales sustains on this GPU: int8 x int8 -> int32
+    # (torch._int_mm), fp8 e4m3 x fp8 -> bf16 (torch._scaled_mm, unit scales) and bf16 (torch.matmul), B
+    # column-major (the weight [N, K] transposed); four launches per captured graph.
+    libg = None
+    if args.library_gemms:
+        libg = {}
+        M = 3072
+        for N, K in sorted(set(shapes)):
+            a8 = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev)
+            w8 = torch.randint(-8, 8, (N, K), dtype=torch.int8, device=dev)
+            af = torch.randn(M, K, device=dev).to(torch.float8_e4m3fn)
+            wf = torch.randn(N, K, device=dev).to(torch.float8_e4m3fn)
+            ab = torch.randn(M, K, device=dev, dtype=torch.bfloat16)
+            wb = torch.randn(N, K, device=dev, dtype=torch.bfloat16)
+            one = torch.ones((), device=dev)
+            row = {}
+            for name, fn, peak in (("int8_int_mm", lambda: torch._int_mm(a8, w8.t()), INT8_PEAK_TOPS),
+                                   ("fp8_scaled_mm", lambda: torch._scaled_mm(af, wf.t(), scale_a=one, scale_b=one,
+                                                                              out_dtype=torch.bfloat16),
+                                    INT8_PEAK_TOPS),
+                                   ("bf16_matmul", lambda: torch.matmul(ab, wb.t()), FP16_PEAK_TFLOPS)):
+                fn()
+                g1 = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g1):
+                    for _ in range(4):
+                        fn()
+                us = time_graphs([g1], args.prefill_steps, 3) / 4 * 1e3
+                row[name] = {"us": round(us, 1), "pct_peak": round(100 * 2 * M * N * K / (us * 1e-6) / 1e12 / peak, 2)}
+                del g1
+            libg[f"{N}x{K}"] = row
+            log(f"library GEMMs M={M} N={N} K={K}: " + ", ".join(f"{k} {v['us']} us ({v['pct_peak']}%)"
+                                                                for k, v in row.items()))
+            del a8, w8, af, wf, ab, wb
 
     # ---- speculative verify block: 36 chained layers at M = 16 -------------
     # Per layer a -> (q, k, v) = L(a); o = L_o(q); h = RMSNorm_bf16(a + o) (eps 1e-6, weight U(0.8, 1.2));
@@ -624,6 +737,35 @@ def main() -> int:
             log(f"rotate+MXFP4 M={M} K={K}: {res['mxfp4'] * 1e3:.1f} us ({mx[f'M{M}']['GBps']:.0f} GB/s); "
                 f"rotate alone {res['rotate'] * 1e3:.1f} us ({mx[f'M{M}']['rotate_alone_GBps']:.0f} GB/s)")
 
+    # ---- rooflines ------------------------------------------------------------
+    # achieved = algorithmic bytes (or int8 ops) of the launches / their time, each graph timed with HIP events
+    # on its replay stream; traffic = the measured HBM bytes per launch of the same kernel (rocprofv3 counter
+    # passes, profiles/), or None.
+    def roof(bound, kernel, achieved_v, unit, peak, avg_us, launches, name, **extra):
+        return {"bound": bound, "kernel": kernel, "achieved": round(achieved_v, 1), "peak": peak, "unit": unit,
+                "frac": round(achieved_v / peak, 4), "traffic": measured_traffic(name),
+                "avg_launch_us": round(avg_us, 3), "launches_timed_per_replay": launches, **extra}
+
+    rooflines = {
+        "decode_gemm_M1_layer": roof(
+            "hbm", "gemm_skinny, A quantized in its prologue (AQ=1): the 32 GEMM launches of the 8-layer pool's "
+            "grouped M=1 layers (q/k/v group, o, gate/up group, down), as the headline layer runs them",
+            hgemm_gbs, "GB/s", HBM_PEAK_GBS, hgemm_us, n_calls, "decode_gemm_M1_layer",
+            bytes_per_launch=round(hgemm_bytes / n_calls)),
+        "decode_split_rotation_M1_layer": roof(
+            "hbm", "rotate_split_kernel: the 32 rotation launches of the same layers", hrot_gbs, "GB/s",
+            HBM_PEAK_GBS, hrot_us, n_calls, "decode_split_rotation_M1_layer",
+            bytes_per_launch=round(hrot_bytes / n_calls)),
+        "decode_gemm_int8_a_M1": roof(
+            "hbm", "gemm_skinny on int8 A (AQ=0), M=1: the 56 linears of the pool, one launch each",
+            achieved, "GB/s", HBM_PEAK_GBS, per_launch_us, len(gemm_launches), "decode_gemm_int8_a_M1"),
+    }
+    if prefill is not None:
+        rooflines["prefill_gemm_M3072"] = roof(
+            "mfma", "gemm_prefill (tile-pair form on 192x256 / 128x256 tiles): the 7 GEMM launches of one "
+            "M=3072 layer, one launch per linear", prefill["gemm_only_tops"], "TOP/s", INT8_PEAK_TOPS,
+            prefill["gemm_only_ms"] * 1e3 / 7, 7, "prefill_gemm_M3072", ops_per_launch=round(prefill_ops / 7))
+
     # ---- CPU baseline: the oracle on the host ------------------------------
     cpu = None
     if not args.no_cpu:
@@ -652,22 +794,16 @@ def main() -> int:
             "graph_replay": True,
             "layers_per_graph": args.pool_layers,
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "gemm_skinny (decode W4A8 GEMM), M=1, bytes-weighted over the 7 layer shapes",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(),
-            "avg_launch_us": round(per_launch_us, 3),
-        },
+        "roofline": rooflines["decode_gemm_M1_layer"],
+        "roofline_kernels": rooflines,
         "decode_gemm_per_shape_M1": gemm_per_shape,
         "decode": {f"M{M}": {"us_per_layer": round(v[0] * 1e3, 2), "GBps": round(v[1], 1),
                              "frac_hbm": round(v[1] / HBM_PEAK_GBS, 4),
-                             "separate_linears_us_per_layer": round(decode_sep[M][0] * 1e3, 2),
-                             "separate_linears_GBps": round(decode_sep[M][1], 1)} for M, v in decode.items()},
+                             **({"separate_linears_us_per_layer": round(decode_sep[M][0] * 1e3, 2),
+                                 "separate_linears_GBps": round(decode_sep[M][1], 1)} if M in decode_sep else {})}
+                   for M, v in decode.items()},
         "prefill_M3072": prefill,
+        **({"library_gemms_M3072": libg} if libg is not None else {}),
         "verify_block_M16": verify,
         "ragged_batch": ragged,
         "w4a16": w16,
@@ -678,55 +814,81 @@ def main() -> int:
     return 0
 
 
+def cpu_cores():
+    """Host cores this process may use: its affinity set, bounded by a cgroup CPU quota when one is set
+    (threads beyond the quota only time-slice).  Returns (cores, affinity count, quota or None)."""
+    aff = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        q, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if q != "max":
+            quota = max(1, -(-int(q) // int(period)))
+    except (OSError, ValueError):
+        pass
+    return (min(aff, quota) if quota else aff), aff, quota
+
+
 def cpu_baseline(seconds: float):
-    """Time the oracle's reference-path linear (AWQ unpack + dequant + fp32 matmul) on the host
-    over one decoder layer's seven linears at M = 1 (a bounded sample)."""
+    """Time the oracle's reference-path linear (AWQ unpack + dequant_awq + fp32 matmul, after the numpy rotation
+    and per-token quant) on the host, on every core the process may use:
+      - decode: one decoder layer's seven linears at M = 1, repeated for about `seconds` (median per layer);
+      - prefill: a bounded sample of the M = 3072 layer, its q_proj-shaped linear (4096 -> 4096) at the full
+        3072 rows, one pass, in int8 TOP/s (the same ops the GPU figure counts: 2*M*N*K)."""
     import numpy as np
 
     from alpamayo_amd import workloads
     from oracle import linear as olin
     from oracle import rotation as orot
 
-    try:
-        from threadpoolctl import threadpool_info, threadpool_limits
-    except ImportError:  # pragma: no cover
-        threadpool_limits = None
-    cores = min(16, len(os.sched_getaffinity(0)))
-    ctx = threadpool_limits(limits=cores) if threadpool_limits else None
-    try:
+    from threadpoolctl import threadpool_info, threadpool_limits
+
+    cores, aff, quota = cpu_cores()
+
+    def run(sp, c, s, x):
+        return olin.reference_path_dequant(x, sp.pairs.numpy(), c, s, sp.channel_scales.float().reshape(-1).numpy(),
+                                           sp.w.awq_qweight.numpy(), sp.w.awq_scales.numpy(), sp.w.awq_qzeros.numpy())
+
+    with threadpool_limits(limits=cores):
+        used = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
         specs = []
         g = workloads.generator(1001)
         for n, (N, K) in workloads.QWEN3_8B_LINEARS.items():
             sp = workloads.linear_spec(n, N, K, g)
             c, s = orot.cos_sin_table(sp.theta.numpy())
-            x = workloads.activations(1, K, g).float().numpy()
-            specs.append((sp, c, s, x))
+            specs.append((sp, c, s, workloads.activations(1, K, g).float().numpy()))
         layer_bytes = sum(linear_bytes(1, sp.N, sp.K) for sp, _, _, _ in specs)
-        layers, t0 = 0, time.perf_counter()
-        times = []
+        layers, t0, times = 0, time.perf_counter(), []
         while True:
             t1 = time.perf_counter()
             for sp, c, s, x in specs:
-                olin.reference_path_dequant(x, sp.pairs.numpy(), c, s, sp.channel_scales.float().reshape(-1).numpy(),
-                                            sp.w.awq_qweight.numpy(), sp.w.awq_scales.numpy(), sp.w.awq_qzeros.numpy())
+                run(sp, c, s, x)
             times.append(time.perf_counter() - t1)
             layers += 1
             if time.perf_counter() - t0 > seconds or layers >= 50:
                 break
-        if threadpool_limits:
-            used = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
-        else:
-            used = cores
         per_layer = float(np.median(times))
-    finally:
-        if ctx is not None:
-            ctx.__exit__(None, None, None)
+        # prefill sample: the q_proj shape at M = 3072
+        Mp = 3072
+        sp, c, s, _ = specs[0]
+        xp = workloads.activations(Mp, sp.K, workloads.generator(1010)).float().numpy()
+        t1 = time.perf_counter()
+        run(sp, c, s, xp)
+        pf_s = time.perf_counter() - t1
     gbps = layer_bytes / per_layer / 1e9
-    log(f"cpu oracle: {per_layer * 1e3:.1f} ms/layer over {layers} layers, {gbps:.3f} GB/s, {used} threads")
+    pf_tops = 2 * Mp * sp.N * sp.K / pf_s / 1e12
+    log(f"cpu oracle: {per_layer * 1e3:.1f} ms/layer over {layers} layers, {gbps:.3f} GB/s; "
+        f"M=3072 q_proj sample {pf_s:.2f} s = {pf_tops:.4f} TOP/s; {used} threads "
+        f"(affinity {aff}, cgroup quota {quota})")
     return {"value": round(gbps, 4), "unit": "GB/s", "cores": int(used), "kind": "port",
-            "sample": f"{layers} passes of one decoder layer's 7 linears at M=1 (median {per_layer * 1e3:.0f} ms/layer): "
-                      "numpy oracle reference path (AWQ unpack, dequant_awq, fp32 matmul)",
-            "ms_per_step": round(per_layer * 1e3, 2)}
+            "sample": f"{layers} passes of one decoder layer's 7 linears at M=1 (median {per_layer * 1e3:.0f} "
+                      "ms/layer): numpy oracle reference path (rotation, per-token int8 quant, AWQ unpack, "
+                      "dequant_awq, fp32 matmul)",
+            "ms_per_step": round(per_layer * 1e3, 2), "affinity_cores": aff, "cgroup_cpu_quota": quota,
+            "prefill_M3072": {"value": round(pf_tops, 5), "unit": "TOP/s",
+                              "pct_int8_peak": round(100 * pf_tops / INT8_PEAK_TOPS, 5),
+                              "seconds": round(pf_s, 3),
+                              "sample": "one pass of the layer's q_proj-shaped linear (4096->4096) at all 3072 rows "
+                                        "through the same reference path (one of the M=3072 layer's 7 linears)"}}
 
 
 if __name__ == "__main__":

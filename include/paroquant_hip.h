@@ -386,6 +386,21 @@ int pq_w4a8_linear_group_fused(const void* x, const void* x2, const void* norm_w
                                int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot, unsigned flags,
                                void* workspace, size_t workspace_bytes, void* stream);
 
+/* pq_w4a8_linear_group (mode 0) or pq_w4a8_linear_group_fused (mode PQ_PRO_*)
+ * in its two stages: stage 1 makes the rotation (+ quant) launches, whose
+ * output stays in the workspace; stage 2 makes the GEMM launch from it.  The
+ * two calls take the same arguments (stage 2 reads neither x nor the
+ * prologue's, which may be NULL) and the same workspace, not touched in
+ * between; in that order on one stream they make exactly the launches, and
+ * give exactly the results, of the one-call form.  For callers that place
+ * the stages apart (other work between them, separate graph nodes) and for
+ * timing each kernel of the linear on its own.  No counterpart in the
+ * reference, whose linear is one call (paroquant_marlin_w4a8.py:59-65). */
+int pq_w4a8_linear_group_stage(int stage, const void* x, const void* x2, const void* norm_weight, float eps,
+                               int mode, void* h_out, void* sum_out, int x_dtype, const pq_linear_member* members,
+                               int count, int bias_dtype, int y_dtype, int64_t m, int64_t k, int krot,
+                               unsigned flags, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Parity form of pq_w4a8_linear_group (mode 0) and pq_w4a8_linear_group_fused
  * (mode PQ_PRO_*, prologue arguments as there): the same launches, chosen by
  * the same rules, up to the GEMM, whose kernel runs in its partials form
