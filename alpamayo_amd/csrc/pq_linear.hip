@@ -9,7 +9,7 @@
 //     row's absmax per group; the decode GEMM derives the token scales and
 //     quantizes A into LDS in its prologue, while its first weight blocks
 //     are already in flight.
-//   split3 (k >= 8192 beyond that, up to 32 tokens): the split rotation
+//   split3 (k >= 4096 beyond that, up to 32 tokens): the split rotation
 //     with the rows spread over waves, a token-scale + int8 kernel, then
 //     the decode GEMM on int8 A (three launches).
 //   rows (otherwise): pq_rotate_quant_i8 (rotation + absmax + int8 quant of
@@ -48,14 +48,17 @@ bool use_split(int64_t m, int64_t k) {
   return (m * k <= 8192 || (k >= 8192 && m <= 2)) && pq::gemm_rotated_supported(m, k);
 }
 
-// Long rows past the split pair, up to 32 tokens: the split rotation with
-// its rows spread over waves (kSplitRowsPerWave rows each), a small kernel
-// for the token scales and int8 codes, then the decode GEMM on int8 A.  The
-// row kernel runs each row on one CU, whose VALU needs about 12 us for the
-// 96 groups of a 12288-channel row (down, k = 12288, at m = 6: 17.8 us
-// against 22.2 us; m = 16: 20.0 / 24.0).  At k = 4096 the third launch costs
-// more than it saves (the decode layers at 3-16 tokens 1-2 % slower).
-// One row per wave: the 36-layer verify block at 16 tokens 2.40 -> 2.34 ms
+// Rows of 4096 channels or more past the split pair, up to 32 tokens: the
+// split rotation with its rows spread over waves (kSplitRowsPerWave rows
+// each), a small kernel for the token scales and int8 codes, then the decode
+// GEMM on int8 A.  The row kernel runs each row on one CU, whose VALU needs
+// about 12 us for the 96 groups of a 12288-channel row (down, k = 12288, at
+// m = 6: 17.8 us against 22.2 us; m = 16: 20.0 / 24.0).  At k = 4096 the
+// three launches win too once the token-scale kernel requests its rows
+// together with the group maxima (the grouped decode layer at m = 4:
+// 50.0 -> 49.2 us, m = 16: 59.4 -> 59.1 us; the 36-layer verify block
+// 2.298 -> 2.268 ms, where the RMSNorm in front of gate/up runs in the split
+// rotation).  One row per wave: the verify block at 16 tokens 2.40 -> 2.34 ms
 // against four rows per wave (2.36 ms with two, 2.50 ms with eight).
 constexpr int kSplitRowsPerWave = 1;
 // Up to 32 tokens: with one row per wave the split rotation takes any row
@@ -64,7 +67,7 @@ constexpr int kSplitRowsPerWave = 1;
 // (the decode layer at M = 17: 80.1 us with down on the row kernel).
 constexpr int kSplit3MaxRows = 32;
 bool use_split3(int64_t m, int64_t k) {
-  return !use_split(m, k) && m >= 1 && m <= kSplit3MaxRows && k >= 8192 && k <= 16384 && k % 128 == 0;
+  return !use_split(m, k) && m >= 1 && m <= kSplit3MaxRows && k >= 4096 && k <= 16384 && k % 128 == 0;
 }
 
 enum class Path { kSplit, kSplit3, kRows };

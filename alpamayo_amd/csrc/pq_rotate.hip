@@ -575,26 +575,33 @@ __global__ __launch_bounds__(256) void quant_split_kernel(const pq::QuantGroup g
   const int row = blockIdx.y;
   const int G = h >> 7;
   const int lane = threadIdx.x & 63;
+  const int c8 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  // the thread's 8 values are requested together with the group maxima (one
+  // memory round trip, not two); threads past h re-read the row's last 8
+  const int64_t o = static_cast<int64_t>(row) * h + min(c8, h - 8);
+  uint4 v16;
+  float4 va, vb;
+  if constexpr (MAT16) {
+    v16 = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(mb.xr) + o);
+  } else {
+    va = *reinterpret_cast<const float4*>(static_cast<const float*>(mb.xr) + o);
+    vb = *reinterpret_cast<const float4*>(static_cast<const float*>(mb.xr) + o + 4);
+  }
   const float* gm = mb.gmax + static_cast<int64_t>(row) * G;
   uint32_t u = 0;
   for (int i = lane; i < G; i += 64) u = max(u, __float_as_uint(gm[i]));
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) u = max(u, static_cast<uint32_t>(__shfl_xor(static_cast<int>(u), o)));
+  for (int s = 32; s > 0; s >>= 1) u = max(u, static_cast<uint32_t>(__shfl_xor(static_cast<int>(u), s)));
   const float am = __uint_as_float(u);
-  const int c8 = (blockIdx.x * 256 + threadIdx.x) * 8;
   if (c8 >= h) return;
-  const int64_t o = static_cast<int64_t>(row) * h + c8;
   const float inv = pqd::inv_scale(am);
   uint2 q;
   if constexpr (MAT16) {
-    const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(mb.xr) + o);
-    q.x = pqd::quant4_f16(v.x, v.y, inv);
-    q.y = pqd::quant4_f16(v.z, v.w, inv);
+    q.x = pqd::quant4_f16(v16.x, v16.y, inv);
+    q.y = pqd::quant4_f16(v16.z, v16.w, inv);
   } else {
-    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(mb.xr) + o);
-    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(mb.xr) + o + 4);
-    q.x = pqd::quant4(a.x, a.y, a.z, a.w, inv);
-    q.y = pqd::quant4(b.x, b.y, b.z, b.w, inv);
+    q.x = pqd::quant4(va.x, va.y, va.z, va.w, inv);
+    q.y = pqd::quant4(vb.x, vb.y, vb.z, vb.w, inv);
   }
   *reinterpret_cast<uint2*>(mb.xq + o) = q;
   if (c8 == 0) mb.xscale[row] = am / 127.0f;

@@ -211,8 +211,8 @@ int pq_w4a8_prepack(const int32_t* awq_qweight, const uint16_t* awq_scales,
  * this function rather than a formula of your own; the rule it follows is:
  *   split pair (m*k <= 8192, or k >= 8192 and m <= 2): the rotated rows and
  *     per-group maxima, m*k*4 rounded up to 256 plus 4*m*(k/128) bytes;
- *   three-launch long rows (k a multiple of 128 in [8192, 16384], beyond the
- *     split pair, up to m = 32): both of those plus the int8 activations and
+ *   three launches (k a multiple of 128 in [4096, 16384], beyond the split
+ *     pair, up to m = 32): both of those plus the int8 activations and
  *     their scales (m*k rounded up to 256, plus 4*m);
  *   otherwise (the row rotate+quant kernel): the int8 activations and their
  *     scales only, m*k rounded up to 256 plus 4*m bytes.
@@ -268,8 +268,9 @@ typedef struct pq_linear_member {
 /* 1 when pq_w4a8_linear (and the group entry points) run m tokens of k
  * features through the split rotation (waves per 128-channel group, spread
  * over the chip): with a GEMM that quantizes A in its prologue (m*k <= 8192,
- * or k >= 8192 and m <= 2), or for long rows (k a multiple of 128 in
- * [8192, 16384], up to 32 tokens) with a token-scale + int8 kernel and the
+ * or k >= 8192 and m <= 2), or for rows of 4096 channels or more (k a
+ * multiple of 128 in [4096, 16384], up to 32 tokens) with a token-scale +
+ * int8 kernel and the
  * GEMM on int8 A.  0 when they run the row rotate+quant kernel plus the
  * GEMM.  Callers use it to decide whether an elementwise step is cheaper
  * fused into the rotation launch (it is on the split path) or as a separate

@@ -124,8 +124,8 @@ def test_workspace_size_rules():
     assert lib.pq_w4a8_linear_workspace_size(1, 4096, 12288, 16) == split(1, 12288)
     assert lib.pq_w4a8_linear_workspace_size(2, 4096, 4096, 8) == split(2, 4096)
     assert lib.pq_w4a8_linear_workspace_size(2, 4096, 12288, 8) == split(2, 12288)
-    # long rows (k >= 8192) past that, up to 32 tokens: rotated rows and int8 codes, then group
-    # maxima and token scales
+    # rows of k >= 4096 past that, up to 32 tokens: rotated rows and int8 codes, then group maxima
+    # and token scales
     def split3(m, k):
         return (m * k * 4 + 255) // 256 * 256 + (m * k + 255) // 256 * 256 + m * (k // 128) * 4 + m * 4
     assert lib.pq_w4a8_linear_workspace_size(3, 4096, 12288, 8) == split3(3, 12288)
@@ -133,12 +133,14 @@ def test_workspace_size_rules():
     assert lib.pq_w4a8_linear_workspace_size(16, 4096, 12288, 8) == split3(16, 12288)
     assert lib.pq_w4a8_linear_workspace_size(32, 4096, 12288, 8) == split3(32, 12288)
     assert lib.pq_w4a8_linear_group_workspace_size(16, 8192, 2) == 2 * split3(16, 8192)
-    # otherwise the row path holds xq and xscale
-    assert lib.pq_w4a8_linear_workspace_size(4, 4096, 4096, 8) == 4 * 4096 + 16
-    assert lib.pq_w4a8_linear_workspace_size(3, 4096, 4096, 8) == 3 * 4096 + 12
+    assert lib.pq_w4a8_linear_workspace_size(4, 4096, 4096, 8) == split3(4, 4096)
+    assert lib.pq_w4a8_linear_workspace_size(3, 4096, 4096, 8) == split3(3, 4096)
     assert lib.pq_w4a8_linear_workspace_size(17, 4096, 12288, 8) == split3(17, 12288)
+    assert lib.pq_w4a8_linear_workspace_size(32, 4096, 4096, 8) == split3(32, 4096)
+    # otherwise the row path holds xq and xscale
     assert lib.pq_w4a8_linear_workspace_size(33, 4096, 12288, 8) == 33 * 12288 + 132
-    assert lib.pq_w4a8_linear_workspace_size(17, 4096, 4096, 8) == 17 * 4096 + 68
+    assert lib.pq_w4a8_linear_workspace_size(33, 4096, 4096, 8) == 33 * 4096 + 132
+    assert lib.pq_w4a8_linear_workspace_size(5, 4096, 2048, 8) == 5 * 2048 + 20
     assert lib.pq_w4a8_linear_workspace_size(3, 64, 100, 8) == 0       # invalid shape -> 0
 
 
@@ -261,9 +263,10 @@ def test_w4a16_group_workspace_rule():
 def test_split_path_rule():
     lib = _lib.load()
     assert lib.pq_w4a8_linear_split_path(1, 4096) == 1
-    assert lib.pq_w4a8_linear_split_path(3, 4096) == 0   # three tokens: the row kernel
+    assert lib.pq_w4a8_linear_split_path(3, 4096) == 1   # three tokens: the three launches
     assert lib.pq_w4a8_linear_split_path(1, 12288) == 1
-    assert lib.pq_w4a8_linear_split_path(4, 4096) == 0
+    assert lib.pq_w4a8_linear_split_path(4, 4096) == 1
+    assert lib.pq_w4a8_linear_split_path(5, 2048) == 0   # short rows: the row kernel
     # long rows: the split pair up to 2 tokens, then the three-launch split path (never the row kernel)
     assert lib.pq_w4a8_linear_split_path(2, 12288) == 1
     assert lib.pq_w4a8_linear_split_path(4, 12288) == 1
@@ -274,9 +277,11 @@ def test_split_path_rule():
     assert lib.pq_w4a8_linear_split_path(17, 12288) == 1
     assert lib.pq_w4a8_linear_split_path(32, 16384) == 1
     assert lib.pq_w4a8_linear_split_path(33, 12288) == 0
-    assert lib.pq_w4a8_linear_split_path(16, 4096) == 0
+    assert lib.pq_w4a8_linear_split_path(16, 4096) == 1
+    assert lib.pq_w4a8_linear_split_path(33, 4096) == 0
     assert lib.pq_w4a8_linear_split_path(2, 4096) == 1
-    assert lib.pq_w4a8_linear_split_path(4, 6144) == 0
+    assert lib.pq_w4a8_linear_split_path(4, 6144) == 1
+    assert lib.pq_w4a8_linear_split_path(3, 3968) == 0
     assert lib.pq_w4a8_linear_split_path(0, 4096) == 0
 
 
