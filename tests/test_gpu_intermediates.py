@@ -85,7 +85,8 @@ def test_plain_group_intermediates(M, layout):
 
 
 @pytest.mark.parametrize("M,K,ns", [(1, 4096, (4096, 1024)), (2, 4096, (1024,)), (2, 12288, (4096,)),
-                                    (5, 12288, (1024,)), (20, 8192, (1024, 64)), (9, 4096, (1024,))])
+                                    (5, 12288, (1024,)), (20, 8192, (1024, 64)), (9, 4096, (1024,)),
+                                    (6, 2048, (1024,))])
 def test_unrounded_rows_intermediates(M, K, ns):
     """flags (False, False): no fp16 rounding of the input or of the rotated rows (the fp32 operand of the
     quantizing prologue, AQ = 2, and of quant_split_kernel)."""

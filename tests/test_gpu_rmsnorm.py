@@ -30,7 +30,8 @@ def _bits_close(got_np, ref_np, min_equal=0.999):
 
 CASES = [
     # (M, K, member Ns): the split pair (M*K <= 8192, or M <= 2 for K >= 8192), the three-launch
-    # long-row path (K >= 8192 up to 32 tokens), the row rotate+quant path, ragged row counts
+    # path (K >= 4096 up to 32 tokens), the row rotate+quant path (short rows at a few tokens, and
+    # from 33 tokens), ragged row counts
     (1, 4096, (4096, 1024, 1024)),
     (3, 4096, (1024, 1024)),
     (1, 12288, (4096,)),
@@ -43,6 +44,7 @@ CASES = [
     (32, 16384, (4096,)),
     (300, 4096, (4096, 1024, 1024)),
     (1029, 2048, (1040, 16)),
+    (6, 2048, (1024, 64)),
 ]
 
 
