@@ -17,11 +17,16 @@ __device__ __forceinline__ uint32_t quant1(float v, float inv) {
   return static_cast<uint32_t>(static_cast<int>(r)) & 0xffu;
 }
 
-// The code as an int32 (only its low byte is used), from a product that is
-// already formed.
+// The code in the low byte of the result (the other bytes are not part of
+// it), from a product p = v * inv that is already formed.  Every caller
+// scales by 127 / absmax of the very values it quantizes, so p lies in
+// [-127, 127] up to two roundings; adding 1.5 * 2^23 lands in [2^23, 2^24),
+// where float32 spacing is 1, so the sum is rne(p) + 1.5 * 2^23 and its low
+// byte is rne(p) in two's complement -- the code of rne, clamp and convert,
+// in two instructions.  The max keeps the clamp's answer for a NaN product
+// (code -128).
 __device__ __forceinline__ uint32_t quant_scaled(float p) {
-  const float r = fminf(fmaxf(__builtin_rintf(p), -128.0f), 127.0f);
-  return static_cast<uint32_t>(static_cast<int>(r));
+  return __float_as_uint(fmaxf(p, -128.0f) + 12582912.0f);
 }
 
 // Low bytes of four codes, a in byte 0: three byte permutes.
@@ -49,6 +54,55 @@ __device__ __forceinline__ uint32_t quant4_f16(uint32_t w01, uint32_t w23, float
 }
 
 __device__ __forceinline__ float inv_scale(float absmax) { return absmax > 0.0f ? 127.0f / absmax : 0.0f; }
+
+// -0.0f that the compiler cannot see through (it would fold an fma with a
+// constant -0 addend back into a multiply).
+__device__ __forceinline__ float opaque_neg_zero() {
+  float nz;
+  asm volatile("s_mov_b32 %0, 0x80000000" : "=s"(nz));
+  return nz;
+}
+
+// v rounded to fp16, times s: one v_cvt_f16_f32 and one v_fma_mix_f32.
+// fma(h, s, -0) equals the product h * s bit for bit (adding -0 changes no
+// rounded product, a -0 product included); nz is opaque_neg_zero().
+__device__ __forceinline__ float f16_scaled(float v, float s, float nz) {
+  return __builtin_fmaf(static_cast<float>(static_cast<_Float16>(v)), s, nz);
+}
+
+// Two floats -> a dword of two fp16 (a in the low half), rounded to nearest
+// even: one v_cvt_pk_f16_f32.
+__device__ __forceinline__ uint32_t pk_f16(float a, float b) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const f2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
+}
+
+// A dword of two fp16 taken from an array of fp16 pairs: number i0 in the low
+// half, number i1 in the high half (fp16 number i of d is half i & 1 of
+// d[i >> 1]).  One byte permute when i0, i1 are known at compile time.
+template <int N>
+__device__ __forceinline__ uint32_t f16_pair(const uint32_t (&d)[N], int i0, int i1) {
+  const uint32_t sel = ((i0 & 1) ? 0x0302u : 0x0100u) | ((i1 & 1) ? 0x07060000u : 0x05040000u);
+  return __builtin_amdgcn_perm(d[i1 >> 1], d[i0 >> 1], sel);
+}
+
+// N floats -> N fp16 stored side by side at p (aligned to 2 N bytes).
+template <int N>
+__device__ __forceinline__ void store_f16xn(uint16_t* p, const float (&v)[N]) {
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8, "1, 2, 4 or 8 values");
+  if constexpr (N == 1) {
+    *p = pq_f32_to_f16(v[0]);
+  } else {
+    uint32_t w[N / 2];
+#pragma unroll
+    for (int q = 0; q < N / 2; ++q) w[q] = pk_f16(v[2 * q], v[2 * q + 1]);
+    if constexpr (N == 2) *reinterpret_cast<uint32_t*>(p) = w[0];
+    else if constexpr (N == 4) *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+    else *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
 
 // ---------------------------------------------------------------------------
 // int4 weight unpacking (layout in pq_gemm.hip): a dword of 8 codes -> two

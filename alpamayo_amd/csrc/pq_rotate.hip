@@ -243,9 +243,19 @@ constexpr int kRQWaves = 8;
 // dtype (the rotation::rotate result); kRqMxfp4 their OCP MXFP4 codes and
 // E8M0 scales (mb.out / mb.xrot, the rotation::rotate_and_quant_mxfp4
 // result).  The last two take no prologue, no fp16 rounding and no flags.
+//
+// IN fixes how the input reaches the rotation: kInAsIs as it is, kInF16
+// rounded to fp16 (PQ_RQ_INPUT_FP16; the rounding and the channel scale
+// then cost one v_cvt_f16_f32 and one v_fma_mix_f32), kInFlag as the flag
+// says at run time.
+//
+// With MAT16 the row buffer is channel-major: channel c's RB fp16 values lie
+// side by side at rowbuf[c * RB], so a lane stores a slot's RB rows with
+// RB / 2 packed converts and one LDS write.
 constexpr int kRqInt8 = 0, kRqRows = 1, kRqMxfp4 = 2;
+constexpr int kInAsIs = 0, kInF16 = 1, kInFlag = 2;
 
-template <int DT, int KP, bool MAT16, int RB, bool NORM, int OUT = kRqInt8>
+template <int DT, int KP, bool MAT16, int RB, bool NORM, int OUT = kRqInt8, int IN = kInFlag>
 __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void* __restrict__ x,
                                                                        const pq::RotGroup grp, int64_t row_begin,
                                                                        int h, int krot, unsigned flags,
@@ -266,6 +276,7 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
   const int lane = t & 63;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);   // wave-uniform: scalar branches
   const bool in16 = (flags & PQ_RQ_INPUT_FP16) != 0;
+  const float nz = pqd::opaque_neg_zero();
   const int G = h >> 7;
   RowT* rowbuf = reinterpret_cast<RowT*>(lds_raw);
   const int64_t row0 = row_begin + static_cast<int64_t>(blockIdx.x) * RB;
@@ -284,11 +295,27 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
   pqd::RotLane<KP> rl[2];
   uint32_t xa[2][RB], xb[2][RB];
   float sa[2] = {1.0f, 1.0f}, sb[2] = {1.0f, 1.0f};
+  // bfloat16 rows of the int8 path (16-byte aligned, h a multiple of 128)
+  // are read as dwords: lanes 2i and 2i+1 load the same pair of channels and
+  // each moves its own half into the high half of a float with one byte
+  // permute (a 16-bit load costs a zero-extension here on top of the shift).
+  constexpr bool kPairLoads = DT == PQ_BF16 && OUT == kRqInt8;
+  const uint32_t psel = (lane & 1) ? 0x03020c0cu : 0x01000c0cu;
+  auto raw_f32 = [&](uint32_t raw) -> float {
+    if constexpr (kPairLoads) return __uint_as_float(__builtin_amdgcn_perm(0u, raw, psel));
+    else return pq_raw_to_f32<DT>(raw);
+  };
+  const int lane_ch = kPairLoads ? (lane & ~1) : lane;
+  // channel lane (+ c0) of the row that starts at element e0 (a multiple of 128)
+  auto load_row = [&](const void* base, int64_t e0) -> uint32_t {
+    if constexpr (kPairLoads) return *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(base) + e0 + lane_ch);
+    else return pq_load_raw<DT>(base, e0 + lane_ch);
+  };
   auto load_inputs = [&](int g, uint32_t (&va)[RB], uint32_t (&vb)[RB], float& s0, float& s1) {
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-      va[r] = pq_load_raw<DT>(x, (row0 + r) * h + g * 128 + lane);
-      vb[r] = pq_load_raw<DT>(x, (row0 + r) * h + g * 128 + 64 + lane);
+      va[r] = load_row(x, (row0 + r) * h + g * 128);
+      vb[r] = load_row(x, (row0 + r) * h + g * 128 + 64);
     }
     s0 = sp[(g * 128 + lane) & smask];
     s1 = sp[(g * 128 + 64 + lane) & smask];
@@ -308,8 +335,8 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
     if constexpr (NORM) {
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
-        va[r] = pq_load_raw<DT>(nres, (row0 + r) * h + g * 128 + lane);
-        vb[r] = pq_load_raw<DT>(nres, (row0 + r) * h + g * 128 + 64 + lane);
+        va[r] = load_row(nres, (row0 + r) * h + g * 128);
+        vb[r] = load_row(nres, (row0 + r) * h + g * 128 + 64);
       }
       w0 = pq_load_raw<DT>(nwp, g * 128 + lane);
       w1 = pq_load_raw<DT>(nwp, g * 128 + 64 + lane);
@@ -348,16 +375,16 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
       float a[RB], b[RB];
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
-        float lo = pq_raw_to_f32<DT>(xa[ph][r]), hi = pq_raw_to_f32<DT>(xb[ph][r]);
+        float lo = raw_f32(xa[ph][r]), hi = raw_f32(xb[ph][r]);
         if constexpr (NORM) {
           const int64_t ro = (row0 + r) * h + g * 128 + lane;
           if (pro_glu) {
-            lo = pqd::swiglu<DT>(lo, pq_raw_to_f32<DT>(ra[ph][r]));
-            hi = pqd::swiglu<DT>(hi, pq_raw_to_f32<DT>(rb[ph][r]));
+            lo = pqd::swiglu<DT>(lo, raw_f32(ra[ph][r]));
+            hi = pqd::swiglu<DT>(hi, raw_f32(rb[ph][r]));
           } else {
             if (nm.res != nullptr) {
-              lo = pqd::round_to_dt<DT>(lo + pq_raw_to_f32<DT>(ra[ph][r]));
-              hi = pqd::round_to_dt<DT>(hi + pq_raw_to_f32<DT>(rb[ph][r]));
+              lo = pqd::round_to_dt<DT>(lo + raw_f32(ra[ph][r]));
+              hi = pqd::round_to_dt<DT>(hi + raw_f32(rb[ph][r]));
             }
             if (write_norm && nm.s_out != nullptr) {
               pq_store_from_f32<DT>(nm.s_out, ro, lo);
@@ -373,20 +400,29 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
             pq_store_from_f32<DT>(nm.h_out, ro + 64, hi);
           }
         }
-        lo = (in16 ? pq_round_f16(lo) : lo) * s0;
-        hi = (in16 ? pq_round_f16(hi) : hi) * s1;
+        if constexpr (IN == kInF16) {
+          lo = pqd::f16_scaled(lo, s0, nz);
+          hi = pqd::f16_scaled(hi, s1, nz);
+        } else if constexpr (IN == kInFlag) {
+          lo = (in16 ? pq_round_f16(lo) : lo) * s0;
+          hi = (in16 ? pq_round_f16(hi) : hi) * s1;
+        } else {
+          lo = lo * s0;
+          hi = hi * s1;
+        }
         a[r] = sw ? hi : lo;
         b[r] = sw ? lo : hi;
       }
       pqd::rot_layers<KP, RB>(cur, krot, a, b);
       const int fa = g * 128 + pqd::rot_final_a(cur), fb = g * 128 + pqd::rot_final_b(cur);
+      if constexpr (MAT16) {
+        pqd::store_f16xn<RB>(rowbuf + fa * RB, a);
+        pqd::store_f16xn<RB>(rowbuf + fb * RB, b);
+      }
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
         const float vi = a[r], vj = b[r];
-        if constexpr (MAT16) {
-          rowbuf[r * h + fa] = pq_f32_to_f16(vi);
-          rowbuf[r * h + fb] = pq_f32_to_f16(vj);
-        } else {
+        if constexpr (!MAT16) {
           rowbuf[r * h + fa] = vi;
           rowbuf[r * h + fb] = vj;
         }
@@ -473,55 +509,82 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
     if (lane == 0) red[w][r] = v;
   }
   __syncthreads();
-  // Each row's absmax and 127 / absmax, once per row.
-  __shared__ float s_am[RB], s_inv[RB];
+  // Each row's 127 / absmax, and its token scale, once per row.
+  __shared__ float s_inv[RB];
   if (t < RB) {
     float am = 0.0f;
 #pragma unroll
     for (int ww = 0; ww < kRQWaves; ++ww) am = fmaxf(am, red[ww][t]);
     if constexpr (MAT16) am = pq_round_f16(am);   // = the absmax of the fp16 rows
-    s_am[t] = am;
     s_inv[t] = pqd::inv_scale(am);
+    if (xq != nullptr) xscale[row0 + t] = am / 127.0f;   // null: only the fp16 rows are wanted (W4A16)
   }
   __syncthreads();
 
-  // Quantize the row buffer: 8 elements per thread per step.
-  const int per_row = h >> 3;
-  for (int e = t; e < RB * per_row; e += kRQWaves * 64) {
-    const int r = e / per_row;
-    const int c8 = (e - r * per_row) * 8;
-    const float am = s_am[r];
-    const float inv = s_inv[r];
-    float f[8];
-    uint4 u16{};
-    if constexpr (MAT16) {
-      u16 = *reinterpret_cast<const uint4*>(rowbuf + r * h + c8);
-      if (xrot != nullptr) *reinterpret_cast<uint4*>(xrot + (row0 + r) * h + c8) = u16;
-    } else {
+  if constexpr (MAT16) {
+    // Quantize the channel-major fp16 buffer: a thread takes 8 channels of all
+    // RB rows (RB 16-byte reads), then writes each row's 8 codes (8 bytes,
+    // coalesced across the threads) and, when asked, its 8 fp16 values.
+    for (int e = t; e < (h >> 3); e += kRQWaves * 64) {
+      const int c8 = e * 8;
+      uint32_t d[4 * RB];   // (channel c8 + k, row r) is fp16 number k * RB + r of d
+      const uint4* src = reinterpret_cast<const uint4*>(rowbuf + c8 * RB);
+#pragma unroll
+      for (int q = 0; q < RB; ++q) {
+        const uint4 u = src[q];
+        d[4 * q] = u.x;
+        d[4 * q + 1] = u.y;
+        d[4 * q + 2] = u.z;
+        d[4 * q + 3] = u.w;
+      }
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const int64_t ro = (row0 + r) * h + c8;
+        if (xrot != nullptr) {
+          uint32_t w[4];
+#pragma unroll
+          for (int m = 0; m < 4; ++m) w[m] = pqd::f16_pair(d, 2 * m * RB + r, (2 * m + 1) * RB + r);
+          *reinterpret_cast<uint4*>(xrot + ro) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        if (xq != nullptr) {
+          const float inv = s_inv[r];
+          uint32_t c[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const int i = k * RB + r;
+            c[k] = pqd::quant_scaled(pqd::mul_f16(d[i >> 1], (i & 1) != 0, inv));
+          }
+          *reinterpret_cast<uint2*>(xq + ro) =
+              make_uint2(pqd::pack4(c[0], c[1], c[2], c[3]), pqd::pack4(c[4], c[5], c[6], c[7]));
+        }
+      }
+    }
+  } else {
+    // Quantize the row buffer: 8 elements per thread per step.
+    const int per_row = h >> 3;
+    for (int e = t; e < RB * per_row; e += kRQWaves * 64) {
+      const int r = e / per_row;
+      const int c8 = (e - r * per_row) * 8;
+      const float inv = s_inv[r];
+      float f[8];
       const float4 a = *reinterpret_cast<const float4*>(rowbuf + r * h + c8);
       const float4 b = *reinterpret_cast<const float4*>(rowbuf + r * h + c8 + 4);
       f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
       f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
       if (xrot != nullptr) {
         uint4 o;
-        o.x = pq_f32_to_f16(f[0]) | (static_cast<uint32_t>(pq_f32_to_f16(f[1])) << 16);
-        o.y = pq_f32_to_f16(f[2]) | (static_cast<uint32_t>(pq_f32_to_f16(f[3])) << 16);
-        o.z = pq_f32_to_f16(f[4]) | (static_cast<uint32_t>(pq_f32_to_f16(f[5])) << 16);
-        o.w = pq_f32_to_f16(f[6]) | (static_cast<uint32_t>(pq_f32_to_f16(f[7])) << 16);
+        o.x = pqd::pk_f16(f[0], f[1]);
+        o.y = pqd::pk_f16(f[2], f[3]);
+        o.z = pqd::pk_f16(f[4], f[5]);
+        o.w = pqd::pk_f16(f[6], f[7]);
         *reinterpret_cast<uint4*>(xrot + (row0 + r) * h + c8) = o;
       }
-    }
-    if (xq != nullptr) {   // null: only the fp16 rows are wanted (the W4A16 linear)
-      uint2 o;
-      if constexpr (MAT16) {
-        o.x = pqd::quant4_f16(u16.x, u16.y, inv);
-        o.y = pqd::quant4_f16(u16.z, u16.w, inv);
-      } else {
+      if (xq != nullptr) {
+        uint2 o;
         o.x = quant4(f[0], f[1], f[2], f[3], inv);
         o.y = quant4(f[4], f[5], f[6], f[7], inv);
+        *reinterpret_cast<uint2*>(xq + (row0 + r) * h + c8) = o;
       }
-      *reinterpret_cast<uint2*>(xq + (row0 + r) * h + c8) = o;
-      if (c8 == 0) xscale[row0 + r] = am / 127.0f;
     }
   }
 }
@@ -709,29 +772,46 @@ inline int rq_rows_per_block(int64_t rows, int h, bool mat16) {
   return rb;
 }
 
-template <int DT, int KP, bool MAT16, int RB, bool NORM, int OUT = kRqInt8>
+template <int DT, int KP, bool MAT16, int RB, bool NORM, int OUT, int IN>
 void launch_rq_rb(const void* x, const pq::RotGroup& grp, int64_t row_begin, int64_t nblocks, int h, int krot,
                   unsigned flags, const pq::NormArgs& nm, hipStream_t stream) {
   if (nblocks <= 0) return;
   const size_t lds = static_cast<size_t>(RB) * h * (MAT16 ? 2 : 4);
   const dim3 grid(static_cast<unsigned>(nblocks), static_cast<unsigned>(grp.count));
-  rotate_quant_kernel<DT, KP, MAT16, RB, NORM, OUT><<<grid, kRQWaves * 64, lds, stream>>>(x, grp, row_begin, h,
-                                                                                          krot, flags, nm);
+  rotate_quant_kernel<DT, KP, MAT16, RB, NORM, OUT, IN><<<grid, kRQWaves * 64, lds, stream>>>(x, grp, row_begin,
+                                                                                              h, krot, flags, nm);
 }
 
-template <int DT, int KP, bool MAT16, bool NORM, int OUT = kRqInt8>
-void launch_rq(const void* x, const pq::RotGroup& grp, int64_t rows, int h, int krot, unsigned flags,
-               const pq::NormArgs& nm, hipStream_t stream) {
+template <int DT, int KP, bool MAT16, bool NORM, int OUT, int IN>
+void launch_rq_in(const void* x, const pq::RotGroup& grp, int64_t rows, int h, int krot, unsigned flags,
+                  const pq::NormArgs& nm, hipStream_t stream) {
   const int rb = rq_rows_per_block(rows, h, MAT16);
   const int64_t full = rows / rb;
   switch (rb) {
-    case 8: launch_rq_rb<DT, KP, MAT16, 8, NORM, OUT>(x, grp, 0, full, h, krot, flags, nm, stream); break;
-    case 4: launch_rq_rb<DT, KP, MAT16, 4, NORM, OUT>(x, grp, 0, full, h, krot, flags, nm, stream); break;
-    case 2: launch_rq_rb<DT, KP, MAT16, 2, NORM, OUT>(x, grp, 0, full, h, krot, flags, nm, stream); break;
+    case 8: launch_rq_rb<DT, KP, MAT16, 8, NORM, OUT, IN>(x, grp, 0, full, h, krot, flags, nm, stream); break;
+    case 4: launch_rq_rb<DT, KP, MAT16, 4, NORM, OUT, IN>(x, grp, 0, full, h, krot, flags, nm, stream); break;
+    case 2: launch_rq_rb<DT, KP, MAT16, 2, NORM, OUT, IN>(x, grp, 0, full, h, krot, flags, nm, stream); break;
     default: break;
   }
   const int64_t done = rb > 1 ? full * rb : 0;   // the remaining rows, one block each
-  launch_rq_rb<DT, KP, MAT16, 1, NORM, OUT>(x, grp, done, rows - done, h, krot, flags, nm, stream);
+  launch_rq_rb<DT, KP, MAT16, 1, NORM, OUT, IN>(x, grp, done, rows - done, h, krot, flags, nm, stream);
+}
+
+// The input treatment as a compile-time choice: an fp16 input is already
+// fp16 (its prologue rounds to x's dtype as well), a bfloat16 one gets an
+// instance per flag value, float32 reads the flag at run time.  The plain and
+// MXFP4 outputs take no flags.
+template <int DT, int KP, bool MAT16, bool NORM, int OUT = kRqInt8>
+void launch_rq(const void* x, const pq::RotGroup& grp, int64_t rows, int h, int krot, unsigned flags,
+               const pq::NormArgs& nm, hipStream_t stream) {
+  if constexpr (OUT != kRqInt8 || DT == PQ_F16) {
+    launch_rq_in<DT, KP, MAT16, NORM, OUT, kInAsIs>(x, grp, rows, h, krot, flags, nm, stream);
+  } else if constexpr (DT == PQ_BF16) {
+    if (flags & PQ_RQ_INPUT_FP16) launch_rq_in<DT, KP, MAT16, NORM, OUT, kInF16>(x, grp, rows, h, krot, flags, nm, stream);
+    else launch_rq_in<DT, KP, MAT16, NORM, OUT, kInAsIs>(x, grp, rows, h, krot, flags, nm, stream);
+  } else {
+    launch_rq_in<DT, KP, MAT16, NORM, OUT, kInFlag>(x, grp, rows, h, krot, flags, nm, stream);
+  }
 }
 
 // The register-chain rotation of whole rows with a plain (OUT = kRqRows) or
