@@ -91,9 +91,18 @@ __device__ __forceinline__ uint32_t f16_pair(const uint32_t (&d)[N], int i0, int
 // N floats -> N fp16 stored side by side at p (aligned to 2 N bytes).
 template <int N>
 __device__ __forceinline__ void store_f16xn(uint16_t* p, const float (&v)[N]) {
-  static_assert(N == 1 || N == 2 || N == 4 || N == 8, "1, 2, 4 or 8 values");
+  static_assert(N >= 1 && N <= 8 && N != 5 && N != 7, "1, 2, 3, 4, 6 or 8 values");
   if constexpr (N == 1) {
     *p = pq_f32_to_f16(v[0]);
+  } else if constexpr (N == 3) {   // 2-byte aligned
+    p[0] = pq_f32_to_f16(v[0]);
+    p[1] = pq_f32_to_f16(v[1]);
+    p[2] = pq_f32_to_f16(v[2]);
+  } else if constexpr (N == 6) {   // 4-byte aligned
+    uint32_t* q = reinterpret_cast<uint32_t*>(p);
+    q[0] = pk_f16(v[0], v[1]);
+    q[1] = pk_f16(v[2], v[3]);
+    q[2] = pk_f16(v[4], v[5]);
   } else {
     uint32_t w[N / 2];
 #pragma unroll

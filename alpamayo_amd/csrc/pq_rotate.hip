@@ -13,6 +13,7 @@
 // All updates are written with explicit fmaf and the file is compiled with
 // -ffp-contract=off, so the float32 sequence is fixed:
 //   xi' = fma(xi, c, xj*s),  xj' = fma(xj, c, -(xi*s)).
+#include <algorithm>
 #include <type_traits>
 
 #include "pq_device.h"
@@ -765,7 +766,9 @@ constexpr int64_t kMaxGrid = 1 << 20;
 // Rows per block: more rows per block read the parameters fewer times, fewer
 // keep enough blocks in flight; the row buffer stays within 96 KB.  Two rows
 // up to 2048 rows (K = 4096, M = 1264: 15.4 -> 13.8 us against four), four
-// from there (M = 3072: 21.8 us against 24.4 us with two, 28.7 us with eight).
+// from there (M = 3072: 21.8 us against 24.4 us with two, 28.7 us with eight),
+// eight from 4096.  The fp16-row kernel from 2048 rows chooses by how its
+// blocks fill the chip (rq_rows_fp16).
 inline int rq_rows_per_block(int64_t rows, int h, bool mat16) {
   int rb = rows >= 4096 ? 8 : rows >= 2048 ? 4 : rows >= 256 ? 2 : 1;
   while (rb > 1 && static_cast<int64_t>(rb) * h * (mat16 ? 2 : 4) > 96 * 1024) rb >>= 1;
@@ -782,15 +785,93 @@ void launch_rq_rb(const void* x, const pq::RotGroup& grp, int64_t row_begin, int
                                                                                               h, krot, flags, nm);
 }
 
+// The device's CU count and LDS bytes per CU (queried once; 0 if unknown).
+struct CuInfo {
+  int cus = 0;
+  int lds = 0;
+};
+inline CuInfo cu_info() {
+  static const CuInfo info = [] {
+    CuInfo c;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&c.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipDeviceGetAttribute(&c.lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess)
+      c = CuInfo{};
+    return c;
+  }();
+  return info;
+}
+
+// Blocks of one fp16-row instance that registers and waves allow per CU
+// (the runtime's occupancy calculator without the row buffer), queried once.
+template <int DT, int KP, int RB, bool NORM, int IN>
+int rq_blocks_per_cu_regs() {
+  static const int n = [] {
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, rotate_quant_kernel<DT, KP, true, RB, NORM, kRqInt8, IN>,
+                                                     kRQWaves * 64, 0) != hipSuccess)
+      b = 0;
+    return b;
+  }();
+  return n;
+}
+
+// Rows per block of the fp16-row kernel from 2048 rows: every block of a
+// launch is equal work, so the launch takes as many rounds as its blocks
+// fill on the chip (CUs x blocks per CU), and a part-filled last round costs
+// nearly a full one.  Among 8, 6, 4, 3 and 2 rows, with at least two blocks
+// (16 waves) per CU and a row buffer within 96 KB, take the one whose blocks
+// fill their rounds best; a smaller one only when it fills them better by
+// more than 2 %, since more rows per block read the layer parameters fewer
+// times.  At 3072 rows: 6 rows for K = 4096 (512 blocks, one round: 21.4 ->
+// 21.2 us; the prefill layer 0.871 / 0.880 -> 0.857 / 0.860 ms), 3 for
+// K = 12288 (2 rounds of 2 blocks per CU: 58.0 / 58.8 -> 51.5 / 51.6 us
+// against 4 rows, whose 96 KB row buffer leaves one block per CU).
+template <int DT, int KP, bool NORM, int IN>
+int rq_rows_fp16(int64_t rows, int h, int members) {
+  const CuInfo ci = cu_info();
+  if (rows < 2048 || ci.cus <= 0 || ci.lds <= 0) return rq_rows_per_block(rows, h, true);
+  const int cand[5] = {8, 6, 4, 3, 2};
+  const int regs[5] = {rq_blocks_per_cu_regs<DT, KP, 8, NORM, IN>(), rq_blocks_per_cu_regs<DT, KP, 6, NORM, IN>(),
+                       rq_blocks_per_cu_regs<DT, KP, 4, NORM, IN>(), rq_blocks_per_cu_regs<DT, KP, 3, NORM, IN>(),
+                       rq_blocks_per_cu_regs<DT, KP, 2, NORM, IN>()};
+  int best = 0;
+  double best_fill = -1.0;
+  for (int i = 0; i < 5; ++i) {
+    const int64_t lds = static_cast<int64_t>(cand[i]) * h * 2;
+    if (lds > 96 * 1024) continue;
+    const int64_t per_cu = std::min<int64_t>(regs[i], ci.lds / (lds + 1024));   // + the static LDS
+    if (per_cu < 2) continue;
+    const int64_t blocks = rows / cand[i] * members;
+    const int64_t cap = per_cu * ci.cus;
+    const int64_t rounds = (blocks + cap - 1) / cap;
+    const double fill = static_cast<double>(blocks) / static_cast<double>(rounds * cap);
+    if (fill > best_fill + 0.02) {
+      best = cand[i];
+      best_fill = fill;
+    }
+  }
+  return best > 0 ? best : rq_rows_per_block(rows, h, true);
+}
+
 template <int DT, int KP, bool MAT16, bool NORM, int OUT, int IN>
 void launch_rq_in(const void* x, const pq::RotGroup& grp, int64_t rows, int h, int krot, unsigned flags,
                   const pq::NormArgs& nm, hipStream_t stream) {
-  const int rb = rq_rows_per_block(rows, h, MAT16);
+  int rb = 0;
+  if constexpr (MAT16) rb = rq_rows_fp16<DT, KP, NORM, IN>(rows, h, grp.count);
+  else rb = rq_rows_per_block(rows, h, false);
   const int64_t full = rows / rb;
   switch (rb) {
     case 8: launch_rq_rb<DT, KP, MAT16, 8, NORM, OUT, IN>(x, grp, 0, full, h, krot, flags, nm, stream); break;
     case 4: launch_rq_rb<DT, KP, MAT16, 4, NORM, OUT, IN>(x, grp, 0, full, h, krot, flags, nm, stream); break;
     case 2: launch_rq_rb<DT, KP, MAT16, 2, NORM, OUT, IN>(x, grp, 0, full, h, krot, flags, nm, stream); break;
+    case 6:
+      if constexpr (MAT16) launch_rq_rb<DT, KP, MAT16, 6, NORM, OUT, IN>(x, grp, 0, full, h, krot, flags, nm, stream);
+      break;
+    case 3:
+      if constexpr (MAT16) launch_rq_rb<DT, KP, MAT16, 3, NORM, OUT, IN>(x, grp, 0, full, h, krot, flags, nm, stream);
+      break;
     default: break;
   }
   const int64_t done = rb > 1 ? full * rb : 0;   // the remaining rows, one block each

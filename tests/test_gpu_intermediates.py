@@ -166,6 +166,7 @@ def test_swiglu_prologue_intermediates(M, K):
     (1264, 12288, (4096,)),
     (3072, 4096, (4096, 1024, 1024)),    # q on 192 x 256 tiles, k/v on 128 x 256 tiles (tile-pair form)
     (3072, 12288, (4096,)),              # down at full depth, 192 x 256 tiles
+    (2053, 512, (1040, 16)),             # row blocks sized to fill rounds, with a remainder row
 ])
 def test_prefill_intermediates_row_subset(M, K, ns):
     """Prefill: the row rotate+quant kernel and the prefill GEMM in the form production runs (tile pairs on the

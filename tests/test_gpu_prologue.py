@@ -36,6 +36,7 @@ CASES = [
     (300, 4096, (4096, 1024)),
     (1029, 2048, (1040, 16)),
     (6, 2048, (1024, 64)),
+    (2053, 512, (1040, 16)),   # from 2048 rows: blocks sized to fill rounds (three rows here) and a remainder
 ]
 
 

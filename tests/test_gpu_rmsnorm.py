@@ -3,7 +3,10 @@
 sum s against the RMSNorm oracle (Qwen3VLTextRMSNorm.forward,
 modeling_qwen3_vl.py:354-359), and the members' outputs against the plain
 group run on the h the kernel wrote (bit-identical: same rotation input) and
-against the oracle chain."""
+against the oracle chain fed that h.  (h may differ from the oracle's by one
+bf16 ulp in up to 0.1 % of its elements -- the float32 rsqrt -- and such a
+difference can move an int8 code by one, so the chain is checked stage by
+stage.)"""
 
 import zlib
 
@@ -45,6 +48,7 @@ CASES = [
     (300, 4096, (4096, 1024, 1024)),
     (1029, 2048, (1040, 16)),
     (6, 2048, (1024, 64)),
+    (2053, 512, (1040, 16)),   # from 2048 rows: blocks sized to fill rounds (three rows here) and a remainder
 ]
 
 
@@ -74,7 +78,7 @@ def test_rmsnorm_group(M, K, ns, with_res):
     for mb, y, yp, N in zip(mbs, outs[:len(ns)], plain, ns):
         assert y.shape == (M, N)
         assert torch.equal(y, yp), "the fused norm must feed the rotation exactly the h it writes"
-        assert_bf16_close(to_np(y), _oracle(mb, h_ref, flags))
+        assert_bf16_close(to_np(y), _oracle(mb, to_np(h_gpu), flags))
 
 
 def test_module_option_and_graph_replay():

@@ -44,7 +44,10 @@ def _run(x, rot, scales_f32, input_fp16=True, materialize=True):
 @pytest.mark.parametrize("M,K", [(1, 4096), (4, 4096), (16, 4096), (16, 12288), (3, 128), (70, 1024), (300, 4096),
                                  (7, 16384),
                                  # two, four and eight rows per workgroup, each with remainder rows
-                                 (1301, 512), (2501, 512), (4099, 256)])
+                                 (1301, 512), (2501, 512), (4099, 256),
+                                 # from 2048 rows the fp16-row kernel sizes its blocks to fill whole rounds of
+                                 # the chip: six rows per workgroup here, with a remainder of 1 and 5 rows
+                                 (2053, 512), (3077, 512)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_fused_matches_oracle(M, K, dtype):
     print(f"rotate_quant M={M} K={K} dtype={dtype}", flush=True)
@@ -107,6 +110,23 @@ def test_full_prefill_shape_row_subset():
         assert_codes_close(q[rows], qref)
         np.testing.assert_allclose(s[rows], sref, rtol=1e-6)
         assert np.all(np.abs(q).max(axis=1) == 127)   # every row reaches +-127
+
+
+def test_long_rows_three_per_block_row_subset():
+    """2051 rows of K = 12288: blocks of three rows (a four-row buffer of 96 KB would leave one workgroup per CU)
+    and two single-row blocks for the remainder; rows at both ends, at block edges and in the remainder."""
+    M, K = 2051, 12288
+    for dtype in (torch.bfloat16, torch.float16):
+        print(f"rotate_quant long rows M={M} K={K} dtype={dtype}", flush=True)
+        rot = _prepared(K, 51)
+        x = workloads.activations(M, K, workloads.generator(52)).to(dtype)
+        q, s, r = _run(x, rot, rot.cs.float().reshape(-1))
+        rows = np.array([0, 1, 2, 3, 4, 5, 1023, 1024, 1025, 2045, 2046, 2047, 2048, 2049, 2050])
+        v, qref, sref = olin.rotate_quant(to_np(x)[rows], rot.pairs.numpy(), rot.c, rot.s,
+                                          rot.cs.float().reshape(-1).numpy())
+        assert np.mean(r[rows] == v.astype(np.float16).astype(np.float32)) >= 0.999
+        assert_codes_close(q[rows], qref)
+        np.testing.assert_allclose(s[rows], sref, rtol=1e-6, atol=0)
 
 
 def test_bad_params_rejected():
