@@ -498,7 +498,7 @@ __device__ __forceinline__ void rotate_group_rows(const void* __restrict__ x, co
     }
     // the group's absmax of the stored rows: rounding to fp16 is monotonic,
     // so it is the float32 absmax rounded once
-    float mx = pq_wave_max(fmaxf(fabsf(va), fabsf(vb)));
+    float mx = pq_wave_max_nonneg(fmaxf(fabsf(va), fabsf(vb)));
     if constexpr (MAT16) mx = pq_round_f16(mx);
     if (m < M && lane == 0) gmax[static_cast<int64_t>(m) * G + g] = mx;
   }

@@ -183,7 +183,7 @@ __global__ __launch_bounds__(kRotWaves * 64) void rotate_kernel(const void* __re
 template <int NT>
 __device__ __forceinline__ float block_max(float v, float* red) {
   constexpr int NW = NT / 64;
-  v = pq_wave_max(v);
+  v = pq_wave_max_nonneg(v);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   float m = red[0];
@@ -506,7 +506,7 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
 
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
-    const float v = pq_wave_max(rmax[r]);
+    const float v = pq_wave_max_nonneg(rmax[r]);
     if (lane == 0) red[w][r] = v;
   }
   __syncthreads();
