@@ -104,24 +104,24 @@ __device__ __forceinline__ void pq_store_dyn(void* p, int dt, int64_t i, float v
   else static_cast<uint16_t*>(p)[i] = pq_f32_to_bf16(v);
 }
 
-// Wave64 max of non-negative, non-NaN floats (an absmax: their bit patterns
-// order like unsigned integers), the same in every lane.  Six v_max_u32 with
-// DPP operands -- lane pairs and quads, mirrored half rows and rows of 16,
-// then lane 15 of rows 0 / 2 into rows 1 / 3 and lane 31 into rows 2 / 3 --
-// leave the maximum in lane 63.  Lanes a step does not write take 0, which
-// changes no maximum here.
+// Wave64 maximum of unsigned integers, or of non-negative, non-NaN floats (an
+// absmax: their bit patterns order like unsigned integers), the same in every
+// lane.  Six v_max_u32 with DPP operands -- lane pairs and quads, mirrored
+// half rows and rows of 16, then lane 15 of rows 0 / 2 into rows 1 / 3 and
+// lane 31 into rows 2 / 3 -- leave the maximum in lane 63.  Lanes a step does
+// not write take 0, which changes no maximum here.
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ uint32_t pq_dpp_umax(uint32_t u) {
   const uint32_t o = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(u), CTRL, ROW_MASK, 0xf, false));
   return u > o ? u : o;
 }
-__device__ __forceinline__ float pq_wave_max_nonneg(float v) {
-  uint32_t u = __float_as_uint(v);
+__device__ __forceinline__ uint32_t pq_wave_umax(uint32_t u) {
   u = pq_dpp_umax<0xb1, 0xf>(u);    // quad_perm [1, 0, 3, 2]
   u = pq_dpp_umax<0x4e, 0xf>(u);    // quad_perm [2, 3, 0, 1]
   u = pq_dpp_umax<0x141, 0xf>(u);   // row_half_mirror
   u = pq_dpp_umax<0x140, 0xf>(u);   // row_mirror
   u = pq_dpp_umax<0x142, 0xa>(u);   // row_bcast:15
   u = pq_dpp_umax<0x143, 0xc>(u);   // row_bcast:31
-  return __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u), 63)));
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u), 63));
 }
+__device__ __forceinline__ float pq_wave_max_nonneg(float v) { return __uint_as_float(pq_wave_umax(__float_as_uint(v))); }

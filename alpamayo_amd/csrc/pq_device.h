@@ -193,11 +193,20 @@ struct RotLane {
   float cs[2 * KP];
 };
 
-template <int KP>
+// g is wave-uniform.  SADDR: the group's base address is scalar and the
+// lane's part a 32-bit offset, so the loads take the saddr + voffset form with
+// no per-lane 64-bit address arithmetic (the compiler keeps the two offsets
+// in four VGPRs); otherwise the per-lane address is formed at each call (the
+// row kernel, whose six-row instance must stay within 128 VGPRs to keep two
+// workgroups per CU).
+template <int KP, bool SADDR = true>
 __device__ __forceinline__ void load_rot_lane(const uint32_t* __restrict__ rot_idx, const float* __restrict__ rot_cs,
                                               int g, int lane, RotLane<KP>& p) {
   const int64_t o = static_cast<int64_t>(g) * 64 + lane;
-  const uint4* wi = reinterpret_cast<const uint4*>(rot_idx + o * (KP / 2));
+  const uint32_t* gi = rot_idx + static_cast<int64_t>(g) * 64 * (KP / 2);
+  const float* gc = rot_cs + static_cast<int64_t>(g) * 64 * (2 * KP);
+  const uint4* wi = SADDR ? reinterpret_cast<const uint4*>(gi + lane * (KP / 2))
+                          : reinterpret_cast<const uint4*>(rot_idx + o * (KP / 2));
 #pragma unroll
   for (int q = 0; q < KP / 8; ++q) {
     const uint4 v = wi[q];
@@ -206,7 +215,8 @@ __device__ __forceinline__ void load_rot_lane(const uint32_t* __restrict__ rot_i
     p.w[4 * q + 2] = v.z;
     p.w[4 * q + 3] = v.w;
   }
-  const float4* c = reinterpret_cast<const float4*>(rot_cs + o * (2 * KP));
+  const float4* c = SADDR ? reinterpret_cast<const float4*>(gc + lane * (2 * KP))
+                          : reinterpret_cast<const float4*>(rot_cs + o * (2 * KP));
 #pragma unroll
   for (int q = 0; q < KP / 2; ++q) {
     const float4 v = c[q];
@@ -306,7 +316,10 @@ __device__ __forceinline__ void load8_as_f32(const void* base, int64_t elem, flo
 }
 
 // Wave64 sum through xor butterflies: every lane ends with the same value
-// (the same additions in the same association, only commuted).
+// (the same additions in the same association, only commuted).  (A DPP
+// version gathers the sum in another association; against the float64
+// RMSNorm oracle it moved one normalized element of the tests by 2 bf16 ulps,
+// so the sum keeps this order.)
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);

@@ -302,6 +302,7 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
   // permute (a 16-bit load costs a zero-extension here on top of the shift).
   constexpr bool kPairLoads = DT == PQ_BF16 && OUT == kRqInt8;
   const uint32_t psel = (lane & 1) ? 0x03020c0cu : 0x01000c0cu;
+  static_assert(!kPairLoads || IN != kInFlag, "bfloat16 input fixes its treatment at compile time");
   auto raw_f32 = [&](uint32_t raw) -> float {
     if constexpr (kPairLoads) return __uint_as_float(__builtin_amdgcn_perm(0u, raw, psel));
     else return pq_raw_to_f32<DT>(raw);
@@ -346,7 +347,7 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
   // the first group's loads go out before the RMSNorm factor is reduced, so
   // they are in flight while waves 0..RB-1 sum their rows
   if (w < G) {
-    pqd::load_rot_lane<KP>(rot_idx, rot_cs, w, lane, rl[0]);
+    pqd::load_rot_lane<KP, false>(rot_idx, rot_cs, w, lane, rl[0]);
     load_inputs(w, xa[0], xb[0], sa[0], sb[0]);
     load_norm(w, ra[0], rb[0], wa[0], wb[0]);
   }
@@ -366,7 +367,7 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
       if (g >= G) break;   // wave-uniform
       const int nx = ph ^ 1;
       const int gn = (g + kRQWaves < G) ? g + kRQWaves : g;   // clamped: the loads stay unconditional
-      pqd::load_rot_lane<KP>(rot_idx, rot_cs, gn, lane, rl[nx]);
+      pqd::load_rot_lane<KP, false>(rot_idx, rot_cs, gn, lane, rl[nx]);
       load_inputs(gn, xa[nx], xb[nx], sa[nx], sb[nx]);
       load_norm(gn, ra[nx], rb[nx], wa[nx], wb[nx]);
 
@@ -374,51 +375,73 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
       const bool sw = pqd::rot_init_swapped(cur);
       const float s0 = has_scales ? sa[ph] : 1.0f, s1 = has_scales ? sb[ph] : 1.0f;
       float a[RB], b[RB];
+      if constexpr (kPairLoads && !NORM) {
+        // The initial slot swap rides in the byte permute that unpacks the
+        // bfloat16 values: with the dword of channel lane + 64 as its upper
+        // source, adding 4 to the selector's two data bytes takes that
+        // channel instead (two selectors per group, no select per row).
+        const uint32_t to_b = sw ? 0x04040000u : 0u;
+        const uint32_t sel_a = psel + to_b, sel_b = psel + (0x04040000u - to_b);
+        const float sc_a = sw ? s1 : s0, sc_b = sw ? s0 : s1;
 #pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        float lo = raw_f32(xa[ph][r]), hi = raw_f32(xb[ph][r]);
-        if constexpr (NORM) {
-          const int64_t ro = (row0 + r) * h + g * 128 + lane;
-          if (pro_glu) {
-            lo = pqd::swiglu<DT>(lo, raw_f32(ra[ph][r]));
-            hi = pqd::swiglu<DT>(hi, raw_f32(rb[ph][r]));
+        for (int r = 0; r < RB; ++r) {
+          const float va = __uint_as_float(__builtin_amdgcn_perm(xb[ph][r], xa[ph][r], sel_a));
+          const float vb = __uint_as_float(__builtin_amdgcn_perm(xb[ph][r], xa[ph][r], sel_b));
+          if constexpr (IN == kInF16) {
+            a[r] = pqd::f16_scaled(va, sc_a, nz);
+            b[r] = pqd::f16_scaled(vb, sc_b, nz);
           } else {
-            if (nm.res != nullptr) {
-              lo = pqd::round_to_dt<DT>(lo + raw_f32(ra[ph][r]));
-              hi = pqd::round_to_dt<DT>(hi + raw_f32(rb[ph][r]));
-            }
-            if (write_norm && nm.s_out != nullptr) {
-              pq_store_from_f32<DT>(nm.s_out, ro, lo);
-              pq_store_from_f32<DT>(nm.s_out, ro + 64, hi);
-            }
-            if (pro_norm) {
-              lo = pqd::rms_apply<DT>(lo, s_rinv[r], pq_raw_to_f32<DT>(wa[ph]));
-              hi = pqd::rms_apply<DT>(hi, s_rinv[r], pq_raw_to_f32<DT>(wb[ph]));
-            }
-          }
-          if ((pro_norm || pro_glu) && write_norm && nm.h_out != nullptr) {
-            pq_store_from_f32<DT>(nm.h_out, ro, lo);
-            pq_store_from_f32<DT>(nm.h_out, ro + 64, hi);
+            a[r] = va * sc_a;
+            b[r] = vb * sc_b;
           }
         }
-        if constexpr (IN == kInF16) {
-          lo = pqd::f16_scaled(lo, s0, nz);
-          hi = pqd::f16_scaled(hi, s1, nz);
-        } else if constexpr (IN == kInFlag) {
-          lo = (in16 ? pq_round_f16(lo) : lo) * s0;
-          hi = (in16 ? pq_round_f16(hi) : hi) * s1;
-        } else {
-          lo = lo * s0;
-          hi = hi * s1;
+      } else {
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+          float lo = raw_f32(xa[ph][r]), hi = raw_f32(xb[ph][r]);
+          if constexpr (NORM) {
+            const int64_t ro = (row0 + r) * h + g * 128 + lane;
+            if (pro_glu) {
+              lo = pqd::swiglu<DT>(lo, raw_f32(ra[ph][r]));
+              hi = pqd::swiglu<DT>(hi, raw_f32(rb[ph][r]));
+            } else {
+              if (nm.res != nullptr) {
+                lo = pqd::round_to_dt<DT>(lo + raw_f32(ra[ph][r]));
+                hi = pqd::round_to_dt<DT>(hi + raw_f32(rb[ph][r]));
+              }
+              if (write_norm && nm.s_out != nullptr) {
+                pq_store_from_f32<DT>(nm.s_out, ro, lo);
+                pq_store_from_f32<DT>(nm.s_out, ro + 64, hi);
+              }
+              if (pro_norm) {
+                lo = pqd::rms_apply<DT>(lo, s_rinv[r], pq_raw_to_f32<DT>(wa[ph]));
+                hi = pqd::rms_apply<DT>(hi, s_rinv[r], pq_raw_to_f32<DT>(wb[ph]));
+              }
+            }
+            if ((pro_norm || pro_glu) && write_norm && nm.h_out != nullptr) {
+              pq_store_from_f32<DT>(nm.h_out, ro, lo);
+              pq_store_from_f32<DT>(nm.h_out, ro + 64, hi);
+            }
+          }
+          if constexpr (IN == kInF16) {
+            lo = pqd::f16_scaled(lo, s0, nz);
+            hi = pqd::f16_scaled(hi, s1, nz);
+          } else if constexpr (IN == kInFlag) {
+            lo = (in16 ? pq_round_f16(lo) : lo) * s0;
+            hi = (in16 ? pq_round_f16(hi) : hi) * s1;
+          } else {
+            lo = lo * s0;
+            hi = hi * s1;
+          }
+          a[r] = sw ? hi : lo;
+          b[r] = sw ? lo : hi;
         }
-        a[r] = sw ? hi : lo;
-        b[r] = sw ? lo : hi;
       }
       pqd::rot_layers<KP, RB>(cur, krot, a, b);
       const int fa = g * 128 + pqd::rot_final_a(cur), fb = g * 128 + pqd::rot_final_b(cur);
-      if constexpr (MAT16) {
-        pqd::store_f16xn<RB>(rowbuf + fa * RB, a);
-        pqd::store_f16xn<RB>(rowbuf + fb * RB, b);
+      if constexpr (MAT16) {   // (24-bit multiplies: full rate for 3 and 6 rows too)
+        pqd::store_f16xn<RB>(rowbuf + __umul24(fa, RB), a);
+        pqd::store_f16xn<RB>(rowbuf + __umul24(fb, RB), b);
       }
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
@@ -654,9 +677,7 @@ __global__ __launch_bounds__(256) void quant_split_kernel(const pq::QuantGroup g
   const float* gm = mb.gmax + static_cast<int64_t>(row) * G;
   uint32_t u = 0;
   for (int i = lane; i < G; i += 64) u = max(u, __float_as_uint(gm[i]));
-#pragma unroll
-  for (int s = 32; s > 0; s >>= 1) u = max(u, static_cast<uint32_t>(__shfl_xor(static_cast<int>(u), s)));
-  const float am = __uint_as_float(u);
+  const float am = __uint_as_float(pq_wave_umax(u));
   if (c8 >= h) return;
   const float inv = pqd::inv_scale(am);
   uint2 q;
