@@ -129,6 +129,31 @@ def test_long_rows_three_per_block_row_subset():
         np.testing.assert_allclose(s[rows], sref, rtol=1e-6, atol=0)
 
 
+def test_first_call_inside_graph_capture():
+    """From 2048 rows the row kernel's rows per workgroup come from the runtime's occupancy calculator, queried on
+    the first launch of each kernel instance.  Here that first launch is inside a HIP graph capture (float32 input,
+    12 layers, fp16 rows: an instance no other test runs at 2048 rows or more): the capture must succeed and every
+    replay must equal an eager call."""
+    K, M, krot = 256, 2050, 12
+    g = workloads.generator(77)
+    pairs, theta, cs = workloads.rotation_params(K, g, krot=krot)
+    rot_idx, rot_cs, c, s = packed_rotation(pairs, theta)
+    x = workloads.activations(M, K, g).float().cuda()
+    args = (rot_idx.cuda(), rot_cs.cuda(), cs.float().reshape(-1).cuda(), krot, True, True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):   # no eager call before: the capture holds the first launch
+        q, xs = torch.ops.paroquant.rotate_quant_i8(x, *args)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        q2, xs2 = torch.ops.paroquant.rotate_quant_i8(x, *args)
+        torch.cuda.synchronize()
+        assert torch.equal(q, q2) and torch.equal(xs, xs2)
+    _, qref, sref = olin.rotate_quant(to_np(x), pairs.numpy(), c, s, cs.float().reshape(-1).numpy())
+    assert_codes_close(to_np(q), qref)
+    np.testing.assert_allclose(to_np(xs), sref, rtol=1e-6)
+
+
 def test_bad_params_rejected():
     x = torch.zeros(2, 256, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(RuntimeError, match="rot_idx"):
