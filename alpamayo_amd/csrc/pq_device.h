@@ -297,22 +297,47 @@ __device__ __forceinline__ float round_to_dt(float v) {
   else return v;
 }
 
+// Eight consecutive elements of a row as raw bits: one 16-byte load (two for
+// float32).
 template <int DT>
-__device__ __forceinline__ void load8_as_f32(const void* base, int64_t elem, float f[8]) {
+struct Raw8 {
+  uint4 a;
+  uint4 b;   // float32 only
+};
+
+template <int DT>
+__device__ __forceinline__ Raw8<DT> load8_raw(const void* base, int64_t elem) {
+  Raw8<DT> r;
   if constexpr (DT == PQ_F32) {
-    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + elem);
-    const float4 a = p[0], b = p[1];
-    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
-    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const float*>(base) + elem);
+    r.a = p[0];
+    r.b = p[1];
   } else {
-    const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + elem);
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    r.a = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + elem);
+    r.b = make_uint4(0u, 0u, 0u, 0u);
+  }
+  return r;
+}
+
+template <int DT>
+__device__ __forceinline__ void unpack8(const Raw8<DT>& r, float f[8]) {
+  if constexpr (DT == PQ_F32) {
+    f[0] = __uint_as_float(r.a.x); f[1] = __uint_as_float(r.a.y); f[2] = __uint_as_float(r.a.z);
+    f[3] = __uint_as_float(r.a.w); f[4] = __uint_as_float(r.b.x); f[5] = __uint_as_float(r.b.y);
+    f[6] = __uint_as_float(r.b.z); f[7] = __uint_as_float(r.b.w);
+  } else {
+    const uint32_t w[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       f[2 * e] = pq_raw_to_f32<DT>(w[e] & 0xffffu);
       f[2 * e + 1] = pq_raw_to_f32<DT>(w[e] >> 16);
     }
   }
+}
+
+template <int DT>
+__device__ __forceinline__ void load8_as_f32(const void* base, int64_t elem, float f[8]) {
+  unpack8<DT>(load8_raw<DT>(base, elem), f);
 }
 
 // Wave64 sum through xor butterflies: every lane ends with the same value
@@ -326,41 +351,98 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// sum_k s[k]^2 of one row (h % 8 == 0), s = x (+ res) rounded to DT, by one
-// wave: lane l sums the 8-element chunks 8l, 8l + 512, ... in order (each
-// square rounded, then added), then the butterfly.  Every wave that calls it
-// on the same row gets the same bits.
-template <int DT, int kB = 4>
-__device__ __forceinline__ float row_sumsq(const void* __restrict__ x, const void* __restrict__ res, int64_t row_off,
-                                           int h, int lane) {
-  // The loads of kB chunks are issued together (indices clamped into the row,
-  // so they stay unconditional); the sum then runs over the chunks in the
-  // same order as one chunk at a time, so the result does not change.
-  // The residual loads are unconditional too (from x when there is none): a
-  // load under a branch made the compiler wait for every load at the join,
-  // one round trip per chunk.
+// The RMSNorm sum of squares of one row (h % 8 == 0), s = x (+ res) rounded
+// to DT, in one fixed association that every kernel uses: lane l's 8-element
+// chunks k (elements 8l + 512k .. 8l + 512k + 7) fall into kSumClasses = 8
+// classes k mod 8; P_w adds the squares of class w's chunks in ascending k,
+// each chunk's eight in order (one float32 chain); the lane's total is
+// ((P_0 + P_1) + ...) + P_7, and the xor butterfly adds the lanes.  One wave
+// can form all eight partials (row_sumsq), or eight waves one each, shared
+// through LDS (row_sumsq_part, row_sumsq_total): the same bits either way.
+// Loads use indices clamped into the row, so they stay unconditional (the
+// residual's from x when there is none): a load under a branch made the
+// compiler wait for every load at the join.
+constexpr int kSumClasses = 8;
+
+// acc + the eight squares of one chunk, in order.
+template <int DT>
+__device__ __forceinline__ float add_sq8(const Raw8<DT>& xv, const Raw8<DT>& rv, bool has_res, float acc) {
+  float f[8];
+  unpack8<DT>(xv, f);
+  if (has_res) {
+    float r[8];
+    unpack8<DT>(rv, r);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = round_to_dt<DT>(f[e] + r[e]);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc = acc + f[e] * f[e];
+  return acc;
+}
+
+// The partials of lane l for the NC classes w, w + cs, ..., w + (NC - 1) cs
+// of one row: acc[j] is class w + j cs.  Each step requests kQ chunks of
+// every class.
+template <int DT, int NC, int kQ>
+__device__ __forceinline__ void row_sumsq_part(const void* __restrict__ x, const void* __restrict__ res,
+                                               int64_t row_off, int h, int lane, int w, int cs, float (&acc)[NC]) {
   const void* rs = res != nullptr ? res : x;
-  float acc = 0.0f;
-  for (int c0 = lane * 8; c0 < h; c0 += 512 * kB) {
-    float f[kB][8], r[kB][8];
 #pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      const int c8 = min(c0 + 512 * b, h - 8);
-      load8_as_f32<DT>(x, row_off + c8, f[b]);
-      load8_as_f32<DT>(rs, row_off + c8, r[b]);
-    }
+  for (int j = 0; j < NC; ++j) acc[j] = 0.0f;
+  // class w is the first: once its chunk is past the row, so are the others'
+  for (int k0 = w; lane * 8 + 512 * k0 < h; k0 += kQ * kSumClasses) {
+    Raw8<DT> xv[NC][kQ], rv[NC][kQ];
 #pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      if (c0 + 512 * b >= h) break;
-      if (res != nullptr) {
+    for (int j = 0; j < NC; ++j)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) f[b][e] = round_to_dt<DT>(f[b][e] + r[b][e]);
+      for (int q = 0; q < kQ; ++q) {
+        const int c8 = min(lane * 8 + 512 * (k0 + j * cs + q * kSumClasses), h - 8);
+        xv[j][q] = load8_raw<DT>(x, row_off + c8);
+        rv[j][q] = load8_raw<DT>(rs, row_off + c8);
       }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc = acc + f[b][e] * f[b][e];
+    for (int j = 0; j < NC; ++j)
+#pragma unroll
+      for (int q = 0; q < kQ; ++q)
+        if (lane * 8 + 512 * (k0 + j * cs + q * kSumClasses) < h)
+          acc[j] = add_sq8<DT>(xv[j][q], rv[j][q], res != nullptr, acc[j]);
+  }
+}
+
+// The row's total from the lane's eight partials (P[w] = class w).
+__device__ __forceinline__ float row_sumsq_total(const float (&p)[kSumClasses]) {
+  float t = p[0];
+#pragma unroll
+  for (int w = 1; w < kSumClasses; ++w) t = t + p[w];
+  return wave_sum(t);
+}
+
+// All eight partials by one wave: the chunks of kB consecutive classes
+// requested together, each added to its own class's chain.
+template <int DT, int kB = kSumClasses>
+__device__ __forceinline__ float row_sumsq(const void* __restrict__ x, const void* __restrict__ res, int64_t row_off,
+                                           int h, int lane) {
+  static_assert(kSumClasses % kB == 0, "batches of whole class sets");
+  const void* rs = res != nullptr ? res : x;
+  float p[kSumClasses];
+#pragma unroll
+  for (int w = 0; w < kSumClasses; ++w) p[w] = 0.0f;
+  for (int k0 = 0; lane * 8 + 512 * k0 < h; k0 += kSumClasses) {
+#pragma unroll
+    for (int w0 = 0; w0 < kSumClasses; w0 += kB) {
+      Raw8<DT> xv[kB], rv[kB];
+#pragma unroll
+      for (int q = 0; q < kB; ++q) {
+        const int c8 = min(lane * 8 + 512 * (k0 + w0 + q), h - 8);
+        xv[q] = load8_raw<DT>(x, row_off + c8);
+        rv[q] = load8_raw<DT>(rs, row_off + c8);
+      }
+#pragma unroll
+      for (int q = 0; q < kB; ++q)
+        if (lane * 8 + 512 * (k0 + w0 + q) < h) p[w0 + q] = add_sq8<DT>(xv[q], rv[q], res != nullptr, p[w0 + q]);
     }
   }
-  return wave_sum(acc);
+  return row_sumsq_total(p);
 }
 
 // rsqrt(mean + eps) as two correctly rounded float32 operations.
@@ -391,7 +473,8 @@ __device__ __forceinline__ float swiglu(float g, float u) {
 //
 // With NORM the group's rows first go through the prologue of `mode`
 // (PQ_PRO_*): RMSNORM computes each row's RMSNorm factor over the whole row
-// (every wave of the launch gets the same bits) and normalizes, ADD adds the
+// (every wave of the launch gets the same bits; rinv >= 0 passes it in,
+// summed by the caller in the same association) and normalizes, ADD adds the
 // residual, SWIGLU forms silu(x) * up; the wave rotates the result and, when
 // h_out / s_out are set, writes it (h) or the residual sum s for the group's
 // channels.
@@ -404,7 +487,7 @@ __device__ __forceinline__ void rotate_group_rows(const void* __restrict__ x, co
                                                   const void* __restrict__ nw = nullptr,
                                                   void* __restrict__ h_out = nullptr,
                                                   void* __restrict__ s_out = nullptr, float eps = 0.0f,
-                                                  int mode = PQ_PRO_RMSNORM) {
+                                                  int mode = PQ_PRO_RMSNORM, float rinv = -1.0f) {
   const int G = h >> 7;
   const bool in16 = (flags & PQ_RQ_INPUT_FP16) != 0;
   const bool has_scales = scales != nullptr;
@@ -467,7 +550,9 @@ __device__ __forceinline__ void rotate_group_rows(const void* __restrict__ x, co
       for (int m = 0; m < MR; ++m) {
         const int mm = m < M ? m : M - 1;
         const int64_t ro = static_cast<int64_t>(mm) * h;
-        const float r = norm ? rms_inv(row_sumsq<DT, MR <= 4 ? 8 : 4>(x, nres, ro, h, lane), h, eps) : 1.0f;
+        const float r = !norm         ? 1.0f
+                        : rinv >= 0.0f ? rinv
+                                       : rms_inv(row_sumsq<DT, MR <= 4 ? 8 : 4>(x, nres, ro, h, lane), h, eps);
         if (nres != nullptr) {
           xlo[m] = round_to_dt<DT>(xlo[m] + nlo[m]);
           xhi[m] = round_to_dt<DT>(xhi[m] + nhi[m]);

@@ -353,7 +353,7 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
   }
   if (pro_norm) {
     if (w < RB) {
-      const float r = pqd::rms_inv(pqd::row_sumsq<DT, 8>(x, nm.res, (row0 + w) * h, h, lane), h, nm.eps);
+      const float r = pqd::rms_inv(pqd::row_sumsq<DT>(x, nm.res, (row0 + w) * h, h, lane), h, nm.eps);
       if (lane == 0) s_rinv[w] = r;
     }
     pqd::lds_barrier();   // s_rinv is written (LDS only: the loads above stay in flight)
@@ -626,13 +626,26 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
 // ---------------------------------------------------------------------------
 constexpr int kSplitWaves = 1;
 
-template <int DT, int KP, bool MAT16, int MR, bool NORM>
-__global__ __launch_bounds__(kSplitWaves * 64) void rotate_split_kernel(const void* __restrict__ x,
-                                                                         const pq::RotGroup grp, int M, int h,
-                                                                         int krot, unsigned flags,
-                                                                         const pq::NormArgs nm) {
-  const int g = blockIdx.x * kSplitWaves + (threadIdx.x >> 6);
-  if (g >= (h >> 7)) return;   // whole waves only; this kernel has no barrier
+// With the RMSNorm prologue and one row per wave, WPB = kSplitNormWaves
+// waves per workgroup take WPB consecutive groups of the row and share its
+// sum of squares: wave w sums the chunk classes w, w + WPB, ... of the row,
+// the eight partials meet in LDS and every wave adds them in the fixed order,
+// which gives the bits a single wave gets summing the whole row, with 1/WPB
+// of the loads per wave.  Four waves: against one wave per workgroup summing
+// the whole row, the 36-layer verify block (M = 16) 2.160 -> 2.120 ms and the
+// fused decode chain (M = 1) 1.550 -> 1.533 ms; eight waves 2.130 / 1.552 ms
+// (fewer CUs at M = 1), two 2.128 / 1.533 ms.
+constexpr int kSplitNormWaves = 4;
+
+template <int DT, int KP, bool MAT16, int MR, bool NORM, int WPB = kSplitWaves>
+__global__ __launch_bounds__(WPB * 64) void rotate_split_kernel(const void* __restrict__ x, const pq::RotGroup grp,
+                                                                int M, int h, int krot, unsigned flags,
+                                                                const pq::NormArgs nm) {
+  constexpr bool kCoop = WPB > 1;
+  static_assert(WPB == 1 || (pqd::kSumClasses % WPB == 0 && MR == 1 && NORM),
+                "shared row sums: one row per wave, RMSNorm prologue");
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int g = blockIdx.x * WPB + wv;
   const pq::RotMember& mb = grp.mem[blockIdx.y];
   // the normalized rows and the residual sum are the same for every member: member 0 writes them
   const bool first = blockIdx.y == 0;
@@ -643,11 +656,29 @@ __global__ __launch_bounds__(kSplitWaves * 64) void rotate_split_kernel(const vo
   auto at = [](const void* p, int64_t bytes) -> void* {
     return p == nullptr ? nullptr : const_cast<char*>(static_cast<const char*>(p)) + bytes;
   };
+  float rinv = -1.0f;
+  if constexpr (kCoop) {
+    if (nm.mode == PQ_PRO_RMSNORM) {   // uniform over the launch
+      constexpr int NC = pqd::kSumClasses / WPB;
+      __shared__ float s_part[pqd::kSumClasses][64];
+      float pw[NC];
+      pqd::row_sumsq_part<DT, NC, NC >= 4 ? 1 : 4 / NC>(at(x, e0 * xsz), at(nm.res, e0 * xsz), 0, h, lane, wv, WPB,
+                                                         pw);
+#pragma unroll
+      for (int j = 0; j < NC; ++j) s_part[wv + j * WPB][lane] = pw[j];
+      pqd::lds_barrier();
+      float p[pqd::kSumClasses];
+#pragma unroll
+      for (int c = 0; c < pqd::kSumClasses; ++c) p[c] = s_part[c][lane];
+      rinv = pqd::rms_inv(pqd::row_sumsq_total(p), h, nm.eps);
+    }
+  }
+  if (g >= (h >> 7)) return;   // whole waves, after the workgroup's only barrier
   pqd::rotate_group_rows<DT, KP, MAT16, MR, NORM>(
       at(x, e0 * xsz), mb.rot_idx, mb.rot_cs, mb.scales, at(mb.out, e0 * (MAT16 ? 2 : 4)),
-      mb.out_scale + static_cast<int64_t>(row0) * (h >> 7), min(MR, M - row0), h, krot, flags, g, threadIdx.x & 63,
+      mb.out_scale + static_cast<int64_t>(row0) * (h >> 7), min(MR, M - row0), h, krot, flags, g, lane,
       at(nm.res, e0 * xsz), nm.w, first ? at(nm.h_out, e0 * xsz) : nullptr, first ? at(nm.s_out, e0 * xsz) : nullptr,
-      nm.eps, nm.mode);
+      nm.eps, nm.mode, rinv);
 }
 
 // Per-token int8 quantization of the split rotation's rows, for token counts
@@ -696,6 +727,15 @@ template <int DT, int KP, bool MAT16, bool NORM>
 void launch_split_kp(const void* x, const pq::RotGroup& grp, int M, int h, int krot, unsigned flags,
                      const pq::NormArgs& nm, int rows_per_wave, hipStream_t stream) {
   const int rows = rows_per_wave > 0 && rows_per_wave < M ? rows_per_wave : M;
+  if constexpr (NORM) {
+    if (rows == 1 && nm.mode == PQ_PRO_RMSNORM) {
+      constexpr int W = kSplitNormWaves;
+      const dim3 grid(static_cast<unsigned>((h / 128 + W - 1) / W), static_cast<unsigned>(grp.count),
+                      static_cast<unsigned>(M));
+      rotate_split_kernel<DT, KP, MAT16, 1, true, W><<<grid, W * 64, 0, stream>>>(x, grp, M, h, krot, flags, nm);
+      return;
+    }
+  }
   const dim3 grid(static_cast<unsigned>((h / 128 + kSplitWaves - 1) / kSplitWaves), static_cast<unsigned>(grp.count),
                   static_cast<unsigned>((M + rows - 1) / rows));
 #define PQ_SPLIT(MR_)                                                                                      \

@@ -81,6 +81,37 @@ def test_rmsnorm_group(M, K, ns, with_res):
         assert_bf16_close(to_np(y), _oracle(mb, to_np(h_gpu), flags))
 
 
+@pytest.mark.parametrize("K", [4096, 4224])
+def test_same_bits_on_every_path(K):
+    """The normalized rows do not depend on the path: the row kernel (one wave
+    sums each row), the split pair at M = 2 (one wave, all of a row's chunk
+    classes) and the split rotations with one row per wave at M = 1 and
+    M = 16 (the waves of a workgroup each sum some classes and share them)
+    give the same bits for the same rows.  K = 4224 leaves 33 groups (a
+    workgroup with idle waves) and rows whose lanes hold unequal chunk counts."""
+    print(f"rmsnorm same bits K={K}", flush=True)
+    seed = zlib.crc32(f"rms-paths-{K}".encode())
+    krot, flags = 8, (True, True)
+    mbs = _members((1024,), K, krot, seed, with_bias=False)
+    g = workloads.generator(seed + 1)
+    x = workloads.activations(300, K, g).cuda()
+    res = workloads.activations(300, K, g).cuda()
+    w = (0.8 + 0.4 * torch.rand(K, generator=g)).to(torch.bfloat16).cuda()
+    args = ([m["rot_idx"] for m in mbs], [m["rot_cs"] for m in mbs], [m["scales"] for m in mbs], krot,
+            [m["wp"] for m in mbs], [m["wm"] for m in mbs], [m["bias"] for m in mbs], flags[0], flags[1],
+            torch.bfloat16)
+
+    def normed(m):
+        outs = torch.ops.paroquant.w4a8_linear_group_rmsnorm(x[:m], res[:m], w, 1e-6, *args, True, False)
+        return outs[1]
+
+    full = normed(300)
+    for m in (16, 2, 1):
+        assert torch.equal(normed(m), full[:m]), f"M={m}"
+    h_ref, _ = orms.rmsnorm(to_np(x), to_np(w), 1e-6, to_np(res), "bf16")
+    _bits_close(to_np(full), h_ref)
+
+
 def test_module_option_and_graph_replay():
     """SharedInputRotateLinears(norm_weight=...) inside a captured graph, replayed with eager work between."""
     K = 4096
