@@ -125,3 +125,22 @@ __device__ __forceinline__ uint32_t pq_wave_umax(uint32_t u) {
   return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u), 63));
 }
 __device__ __forceinline__ float pq_wave_max_nonneg(float v) { return __uint_as_float(pq_wave_umax(__float_as_uint(v))); }
+// The same for N values, each step applied to all N before the next: the
+// independent DPP operations fill each other's wait states.
+template <int N>
+__device__ __forceinline__ void pq_wave_umax_n(uint32_t (&u)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) u[i] = pq_dpp_umax<0xb1, 0xf>(u[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) u[i] = pq_dpp_umax<0x4e, 0xf>(u[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) u[i] = pq_dpp_umax<0x141, 0xf>(u[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) u[i] = pq_dpp_umax<0x140, 0xf>(u[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) u[i] = pq_dpp_umax<0x142, 0xa>(u[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) u[i] = pq_dpp_umax<0x143, 0xc>(u[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) u[i] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u[i]), 63));
+}

@@ -527,10 +527,13 @@ __global__ __launch_bounds__(kRQWaves * 64) void rotate_quant_kernel(const void*
     return;
   }
 
+  uint32_t ubits[RB];   // the rows' maxima are >= 0: their bits order like unsigned integers
 #pragma unroll
-  for (int r = 0; r < RB; ++r) {
-    const float v = pq_wave_max_nonneg(rmax[r]);
-    if (lane == 0) red[w][r] = v;
+  for (int r = 0; r < RB; ++r) ubits[r] = __float_as_uint(rmax[r]);
+  pq_wave_umax_n<RB>(ubits);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < RB; ++r) red[w][r] = __uint_as_float(ubits[r]);
   }
   __syncthreads();
   // Each row's 127 / absmax, and its token scale, once per row.
