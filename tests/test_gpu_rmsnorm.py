@@ -6,7 +6,8 @@ group run on the h the kernel wrote (bit-identical: same rotation input) and
 against the oracle chain fed that h.  (h may differ from the oracle's by one
 bf16 ulp in up to 0.1 % of its elements -- the float32 rsqrt -- and such a
 difference can move an int8 code by one, so the chain is checked stage by
-stage.)"""
+stage.)  Each row of h is also checked to be exactly the oracle's formula for
+an r within a few float32 ulps of the oracle's."""
 
 import zlib
 
@@ -72,6 +73,7 @@ def test_rmsnorm_group(M, K, ns, with_res):
     h_gpu = outs[len(ns)]
     h_ref, s_ref = orms.rmsnorm(to_np(x), to_np(w), 1e-6, to_np(res) if with_res else None, "bf16")
     _bits_close(to_np(h_gpu), h_ref)
+    assert _rows_match_some_r(to_np(h_gpu), to_np(x), to_np(res) if with_res else None, to_np(w), 1e-6, "bf16")
     if with_res:
         np.testing.assert_array_equal(olin.bf16_bits(to_np(outs[-1])), olin.bf16_bits(s_ref))
     plain = torch.ops.paroquant.w4a8_linear_group(h_gpu, *args)
@@ -110,6 +112,66 @@ def test_same_bits_on_every_path(K):
         assert torch.equal(normed(m), full[:m]), f"M={m}"
     h_ref, _ = orms.rmsnorm(to_np(x), to_np(w), 1e-6, to_np(res), "bf16")
     _bits_close(to_np(full), h_ref)
+
+
+def _rows_match_some_r(h_gpu, x, res, w, eps, tag, span=128):
+    """Whether each row of h_gpu is exactly the oracle's h = round(w * round(s * r'))
+    for one r' within `span` float32 ulps of the oracle's r (the float32 sum
+    of squares in the kernel's association and the oracle's float64 sum give
+    r's that differ in their last bits; any other difference fails)."""
+    s = orms.residual_sum(x, res, tag)
+    r = orms.rms_factor(s, eps)
+    w = np.asarray(w, dtype=np.float32)
+    ok = np.zeros(h_gpu.shape[0], dtype=bool)
+    for d in range(-span, span + 1):
+        rr = (r.view(np.int32) + np.int32(d)).view(np.float32)
+        h = orms.round_to(w * orms.round_to(s * rr, tag), tag)
+        ok |= np.all(h == h_gpu, axis=-1)
+        if ok.all():
+            return True
+    return bool(ok.all())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("M", [1, 2, 16, 300])
+def test_rmsnorm_other_dtypes(dtype, M):
+    """fp16 and float32 activations through the fused RMSNorm on each path
+    (M = 1 and 16: split rotations sharing the row sum across waves; M = 2:
+    one wave sums the row; M = 300: the row kernel): h against the oracle
+    (each row exactly the oracle's formula for an r within a few float32
+    ulps of the oracle's: the sums of squares differ in their last bits; an
+    fp16 h can then move by two ulps, h = round(w * round(s * r)) with w up
+    to 1.2), the residual sum exact, the members' outputs equal to the plain
+    group run on the h the kernel wrote, and every path's h equal to the row
+    kernel's."""
+    print(f"rmsnorm dtype={dtype} M={M}", flush=True)
+    K = 4096
+    seed = zlib.crc32(f"rms-dt-{dtype}-{M}".encode())
+    krot, flags = 8, (True, True)
+    mbs = _members((1024, 64), K, krot, seed, with_bias=True)
+    g = workloads.generator(seed + 1)
+    x = workloads.activations(300, K, g).to(dtype).cuda()
+    res = workloads.activations(300, K, g).to(dtype).cuda()
+    w = (0.8 + 0.4 * torch.rand(K, generator=g)).to(dtype).cuda()
+    args = ([m["rot_idx"] for m in mbs], [m["rot_cs"] for m in mbs], [m["scales"] for m in mbs], krot,
+            [m["wp"] for m in mbs], [m["wm"] for m in mbs], [m["bias"] for m in mbs], flags[0], flags[1],
+            torch.bfloat16)
+    outs = torch.ops.paroquant.w4a8_linear_group_rmsnorm(x[:M], res[:M], w, 1e-6, *args, True, True)
+    h_gpu, s_gpu = outs[2], outs[3]
+    assert h_gpu.dtype == dtype and s_gpu.dtype == dtype
+    tag = "f16" if dtype == torch.float16 else "f32"
+    h_ref, s_ref = orms.rmsnorm(to_np(x[:M]), to_np(w), 1e-6, to_np(res[:M]), tag)
+    np.testing.assert_array_equal(to_np(s_gpu), s_ref)
+    hg = to_np(h_gpu).astype(np.float32)
+    if dtype == torch.float16:   # (float32: a last-bit change of r reaches most elements)
+        assert np.mean(hg == h_ref) >= 0.995
+    assert _rows_match_some_r(hg, to_np(x[:M]), to_np(res[:M]), to_np(w), 1e-6, tag)
+    plain = torch.ops.paroquant.w4a8_linear_group(h_gpu, *args)
+    for y, yp in zip(outs[:2], plain):
+        assert torch.equal(y, yp), "the fused norm must feed the rotation exactly the h it writes"
+    if M < 300:
+        full = torch.ops.paroquant.w4a8_linear_group_rmsnorm(x, res, w, 1e-6, *args, True, False)[2]
+        assert torch.equal(h_gpu, full[:M])
 
 
 def test_module_option_and_graph_replay():
