@@ -129,3 +129,41 @@ def test_module_options_and_graph_replay(M):
         del junk
     with pytest.raises(ValueError):
         qkv(x, residual=r, return_normed=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("M,K", [(1, 4096), (16, 4096), (300, 4096), (1, 12288), (16, 12288)])
+def test_prologues_other_dtypes(dtype, M, K):
+    """The residual add and the SwiGLU prologue on fp16 and float32 activations,
+    on the split pair, the three-launch path and the row kernel: the sum equal
+    to torch's add in that dtype, the activation within one ulp of torch's
+    silu(gate) * up in fp16 (float32: rtol 1e-5, the exponentials may differ
+    in their last bits) and within two of the oracle's, and the members'
+    outputs equal to the plain group run on the rows the kernel wrote."""
+    print(f"prologues dtype={dtype} M={M} K={K}", flush=True)
+    seed = zlib.crc32(f"pro-dt-{dtype}-{M}-{K}".encode())
+    krot, flags = 8, (True, True)
+    mbs = _members((1024, 48), K, krot, seed, with_bias=True)
+    g = workloads.generator(seed + 1)
+    x, r = (workloads.activations(M, K, g).to(dtype).cuda() for _ in range(2))
+    args = _args(mbs, krot, flags)
+    outs = torch.ops.paroquant.w4a8_linear_group_fused(x, r, None, 0.0, _lib.PQ_PRO_ADD, *args, False, True)
+    s = outs[-1]
+    assert s.dtype == dtype and torch.equal(s, x + r)
+    for y, yp in zip(outs[:2], torch.ops.paroquant.w4a8_linear_group(x + r, *args)):
+        assert torch.equal(y, yp)
+    outs = torch.ops.paroquant.w4a8_linear_group_fused(x, r, None, 0.0, _lib.PQ_PRO_SWIGLU, *args, True, False)
+    act = outs[-1]
+    ref_t = torch.nn.functional.silu(x) * r
+    if dtype == torch.float16:
+        a = act.cpu().view(torch.int16).numpy().astype(np.int32)
+        b = ref_t.cpu().view(torch.int16).numpy().astype(np.int32)
+        assert np.abs(a - b).max(initial=0) <= 1 and np.mean(a == b) >= 0.999
+        ref_o = orms.swiglu(to_np(x), to_np(r), "f16").astype(np.float16)
+        o = torch.from_numpy(ref_o).view(torch.int16).numpy().astype(np.int32)
+        assert np.abs(a - o).max(initial=0) <= 2 and np.mean(a == o) >= 0.999
+    else:
+        np.testing.assert_allclose(to_np(act), to_np(ref_t), rtol=1e-5, atol=1e-30)
+        np.testing.assert_allclose(to_np(act), orms.swiglu(to_np(x), to_np(r), "f32"), rtol=1e-5, atol=1e-30)
+    for y, yp in zip(outs[:2], torch.ops.paroquant.w4a8_linear_group(act, *args)):
+        assert torch.equal(y, yp)
