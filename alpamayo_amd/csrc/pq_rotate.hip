@@ -710,7 +710,14 @@ __global__ __launch_bounds__(256) void quant_split_kernel(const pq::QuantGroup g
   }
   const float* gm = mb.gmax + static_cast<int64_t>(row) * G;
   uint32_t u = 0;
-  for (int i = lane; i < G; i += 64) u = max(u, __float_as_uint(gm[i]));
+  // Up to 128 groups (k <= 16384 on every caller): two maxima per lane,
+  // requested together, with clamped indices (a repeated maximum changes
+  // nothing); a loop over them waited for each before requesting the next.
+  if (G <= 128) {
+    u = max(__float_as_uint(gm[min(lane, G - 1)]), __float_as_uint(gm[min(lane + 64, G - 1)]));
+  } else {
+    for (int i = lane; i < G; i += 64) u = max(u, __float_as_uint(gm[i]));
+  }
   const float am = __uint_as_float(pq_wave_umax(u));
   if (c8 >= h) return;
   const float inv = pqd::inv_scale(am);
