@@ -174,6 +174,31 @@ def test_rmsnorm_other_dtypes(dtype, M):
         assert torch.equal(h_gpu, full[:M])
 
 
+@pytest.mark.parametrize("krot,flags", [(16, (True, True)), (1, (False, False)), (8, (True, False))])
+@pytest.mark.parametrize("M", [1, 16, 300])
+def test_rmsnorm_other_rotations(krot, flags, M):
+    """The fused RMSNorm with 16 and 1 Givens layers and with the other input /
+    row-buffer flags (no fp16 input cast, float32 rotated rows), on the split
+    rotation sharing the row sum (M = 1, 16) and the row kernel (M = 300)."""
+    print(f"rmsnorm krot={krot} flags={flags} M={M}", flush=True)
+    K = 4096
+    seed = zlib.crc32(f"rms-rot-{krot}-{flags}-{M}".encode())
+    mbs = _members((1024, 64), K, krot, seed, with_bias=True)
+    g = workloads.generator(seed + 1)
+    x, res = (workloads.activations(M, K, g) for _ in range(2))
+    w = (0.8 + 0.4 * torch.rand(K, generator=g)).to(torch.bfloat16)
+    args = ([m["rot_idx"] for m in mbs], [m["rot_cs"] for m in mbs], [m["scales"] for m in mbs], krot,
+            [m["wp"] for m in mbs], [m["wm"] for m in mbs], [m["bias"] for m in mbs], flags[0], flags[1],
+            torch.bfloat16)
+    outs = torch.ops.paroquant.w4a8_linear_group_rmsnorm(x.cuda(), res.cuda(), w.cuda(), 1e-6, *args, True, True)
+    h_gpu = outs[2]
+    assert _rows_match_some_r(to_np(h_gpu), to_np(x), to_np(res), to_np(w), 1e-6, "bf16")
+    plain = torch.ops.paroquant.w4a8_linear_group(h_gpu, *args)
+    for mb, y, yp in zip(mbs, outs[:2], plain):
+        assert torch.equal(y, yp), "the fused norm must feed the rotation exactly the h it writes"
+        assert_bf16_close(to_np(y), _oracle(mb, to_np(h_gpu), flags))
+
+
 def test_module_option_and_graph_replay():
     """SharedInputRotateLinears(norm_weight=...) inside a captured graph, replayed with eager work between."""
     K = 4096
