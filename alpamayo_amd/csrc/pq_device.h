@@ -357,8 +357,9 @@ __device__ __forceinline__ float wave_sum(float v) {
 // classes k mod 8; P_w adds the squares of class w's chunks in ascending k,
 // each chunk's eight in order (one float32 chain); the lane's total is
 // ((P_0 + P_1) + ...) + P_7, and the xor butterfly adds the lanes.  One wave
-// can form all eight partials (row_sumsq), or eight waves one each, shared
-// through LDS (row_sumsq_part, row_sumsq_total): the same bits either way.
+// can form all eight partials (row_sumsq), or the waves of a workgroup a few
+// each, exchanged through LDS (row_sumsq_part, row_sumsq_total): the same
+// bits either way.
 // Loads use indices clamped into the row, so they stay unconditional (the
 // residual's from x when there is none): a load under a branch made the
 // compiler wait for every load at the join.

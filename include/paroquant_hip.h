@@ -299,8 +299,9 @@ int pq_w4a8_linear_group(const void* x, int x_dtype, const pq_linear_member* mem
  * launches: the members read h instead of x, where
  *   s = x + residual (rounded to x's dtype; s = x when residual is NULL),
  *   h = round(w * round(s * rsqrt(mean(s^2) + eps))),
- * both roundings to x's dtype, mean and rsqrt in float32.  norm_weight: [k]
- * in x's dtype.  When set, h_out and sum_out ([m, k], x's dtype) receive h
+ * both roundings to x's dtype, mean and rsqrt in float32.  The float32 sum of
+ * squares runs in one fixed order on every path, so a row's h does not depend
+ * on m or on the other rows of the call.  norm_weight: [k] in x's dtype.  When set, h_out and sum_out ([m, k], x's dtype) receive h
  * and s (sum_out needs a residual).  residual must be 16-byte aligned.
  * Reference: Qwen3VLTextRMSNorm.forward (src/alpamayo_r1/models/qwen3_vl/
  * modeling_qwen3_vl.py:354-359) in front of the ParoQuant linears that read
