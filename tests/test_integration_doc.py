@@ -1,4 +1,4 @@
-"""INTEGRATION.md's drop-in snippet for load_paroquant_model (paroquant_marlin_w4a8.py:426-510), executed as
+"""The integration guide's drop-in snippet for load_paroquant_model (paroquant_marlin_w4a8.py:426-510), executed as
 the document writes it, on a toy model with AlpamayoR1's module paths (tests/ckpt_util.py): the checkpoint
 load on the CPU, the whole block (load, then convert_model_to_marlin_w4a8) on the GPU."""
 
@@ -13,19 +13,20 @@ from alpamayo_amd.quantization import BF16RotateLinearWrapper, MarlinW4A8Linear
 from tests.ckpt_util import ToyAlpamayo, paroquant_state_dict
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GUIDE = os.path.join(ROOT, "INTEGRATION.md")
 
 
 def _snippet():
-    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    text = open(GUIDE).read()
     blocks = re.findall(r"```python\n(.*?)```", text, flags=re.S)
     found = [b for b in blocks if "load_paroquant_checkpoint(" in b and "convert_model_to_marlin_w4a8(" in b]
-    assert len(found) == 1, "INTEGRATION.md holds one load -> convert block"
+    assert len(found) == 1, "the guide holds one load -> convert block"
     return found[0]
 
 
 def _run(code, device):
     ns = {"model": ToyAlpamayo(), "paro_checkpoint": paroquant_state_dict(), "device": device}
-    exec(compile(code, "INTEGRATION.md", "exec"), ns)   # noqa: S102 -- the document's own code
+    exec(compile(code, GUIDE, "exec"), ns)   # noqa: S102 -- the guide's own code
     return ns
 
 
