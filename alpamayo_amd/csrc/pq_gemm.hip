@@ -60,7 +60,13 @@ namespace {
 // rotation's output): the workgroup derives each row's token scale, writes
 // the int8 codes of all M rows into LDS (row stride K + 16 bytes, so the 16
 // rows of an A fragment hit distinct banks) and reads A from there.  The
-// first batch of weight loads is issued before that prologue.
+// first batch of weight loads is issued before that prologue.  3 = one fp16
+// rotated row (M = 1, K <= 16384) plus its group maxima, quantized in
+// registers: every wave takes the token scale from the maxima (a DPP
+// maximum, no barrier), quantizes a dword of 4 codes per lane for two of its
+// groups at a time (lanes 0-31 one group, 32-63 the other) and gathers its
+// A fragments from them with ds_bpermute: no LDS image, no barrier before
+// the first MFMA.
 constexpr int kSkinnyRows = 16;
 
 // The member of a group that owns workgroup tile `unit` (members own
@@ -136,7 +142,11 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
   // compiler's wait before their first use also waited for the weight
   // blocks issued after them, which put the whole prologue behind the
   // weights' round trip.
-  if constexpr (AQ != 0) {
+  static_assert(AQ != 3 || !RBLK, "one row");
+  uint32_t gm3 = 0;   // AQ == 3: the larger of the lane's two group maxima (G <= 128)
+  if constexpr (AQ == 3)
+    gm3 = max(__float_as_uint(gmax[min(lane, G - 1)]), __float_as_uint(gmax[min(lane + 64, G - 1)]));
+  if constexpr (AQ == 1 || AQ == 2) {
 #pragma unroll
     for (int q = 0; q < kPreMax; ++q) gm[q] = gmax[min(static_cast<int>(threadIdx.x) + q * nthr, M * G - 1)];
     preloaded = M * k8 <= kPre * nthr;
@@ -162,11 +172,23 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
   // One batch of U groups per wave; batch 0 (which holds the prologue) is
   // peeled off the loop, so the common single-batch case has no back edge
   // (the compiler otherwise waits for earlier loads before reusing registers).
+  constexpr int QR = (U + 1) / 2;   // AQ == 3: quantizer rounds per batch (two groups each)
+  float am3 = 0.0f, inv3 = 0.0f;
   auto run_batch = [&](const int it) {
     const int g0 = wave + it * W * U;
     v4i wb[U][NT];
     uint32_t wm[U][NT];
     v4i a0[U], a1[U];
+    // AQ == 3: lane l quantizes codes 4 (l & 31) .. + 3 of the batch's group
+    // 2 r + (l >> 5); requested ahead of the weights (clamped, unconditional)
+    uint2 ah[QR];
+    if constexpr (AQ == 3) {
+#pragma unroll
+      for (int r = 0; r < QR; ++r) {
+        const int g = min(g0 + W * min(2 * r + (lane >> 5), U - 1), G - 1);
+        ah[r] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(xr) + g * 128 + 4 * (lane & 31));
+      }
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       // with the AQ prologue, a group past G loads group G-1 (unused) rather
@@ -191,7 +213,27 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
         }
       }
     }
-    if constexpr (AQ != 0) {
+    uint32_t qd[QR];
+    if constexpr (AQ == 3) {
+      if (it == 0) {   // the token scale, the same in every wave (maxima >= 0: unsigned order)
+        am3 = __uint_as_float(pq_wave_umax(gm3));
+        inv3 = inv_scale(am3);
+      }
+#pragma unroll
+      for (int r = 0; r < QR; ++r) qd[r] = quant4_f16(ah[r].x, ah[r].y, inv3);
+      if constexpr (PARTIALS) {
+        // Parity form: the member's first workgroup writes the codes and the token scale it multiplies.
+        if (blockIdx.x == static_cast<unsigned>(grp.first[mi])) {
+#pragma unroll
+          for (int r = 0; r < QR; ++r) {
+            const int uu = 2 * r + (lane >> 5), g = g0 + W * uu;
+            if (uu < U && g < G) *reinterpret_cast<uint32_t*>(mb.a_out + g * 128 + 4 * (lane & 31)) = qd[r];
+          }
+          if (it == 0 && threadIdx.x == 0) mb.as_out[0] = am3 / 127.0f;
+        }
+      }
+    }
+    if constexpr (AQ == 1 || AQ == 2) {
       if (it == 0) {
         // Part 2: token scales, then the int8 image of A in LDS.
         if (threadIdx.x < kSkinnyRows) s_amax[threadIdx.x] = 0.0f;
@@ -263,10 +305,23 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int g = g0 + W * u;
-      if (g < G) {
-        if constexpr (AQ != 0) {   // A from the LDS image, next to its use
+      // AQ == 3 multiplies a group past G too (its clamped operands, scaled
+      // by 0): behind this branch the compiler moved the batch's weight loads
+      // down to their use, after the quantization
+      if (AQ == 3 || g < G) {
+        if constexpr (AQ == 1 || AQ == 2) {   // A from the LDS image, next to its use
           a0[u] = *reinterpret_cast<const v4i*>(al + g * 128);
           a1[u] = *reinterpret_cast<const v4i*>(al + g * 128 + 16);
+        } else if constexpr (AQ == 3) {
+          // codes j*32 .. j*32+31 of group u: dwords 8j .. 8j+7 of the lanes that quantized it
+          // (g is wave-uniform here, so every lane takes part)
+          const int src = ((u & 1) * 32 + 8 * j) * 4;
+          const int v = static_cast<int>(qd[u >> 1]);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            a0[u][q] = __builtin_amdgcn_ds_bpermute(src + 4 * q, v);
+            a1[u][q] = __builtin_amdgcn_ds_bpermute(src + 16 + 4 * q, v);
+          }
         }
         // Rows past M hold a copy of a real row: MFMA rows are independent
         // and those results are never stored, so they need no masking.
@@ -291,10 +346,10 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
               const int m = 4 * j + v;
-              if (m < M) partials[(static_cast<int64_t>(m) * G + g) * N + (tile0 + nt) * 16 + c] = p[v];
+              if (m < M && g < G) partials[(static_cast<int64_t>(m) * G + g) * N + (tile0 + nt) * 16 + c] = p[v];
             }
           } else {
-            const float sc = meta_scale(meta);
+            const float sc = AQ != 3 || g < G ? meta_scale(meta) : 0.0f;
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[nt][v] = fmaf(static_cast<float>(p[v]), sc, acc[nt][v]);
           }
@@ -321,7 +376,7 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
 #pragma unroll
     for (int w = 0; w < W; ++w) sum += red[w][nt][rv][rl];
     const int n = (tile0 + nt) * 16 + (rl & 15);
-    const float xsm = AQ != 0 ? s_amax[m] / 127.0f : xs[m];
+    const float xsm = AQ == 3 ? am3 / 127.0f : AQ != 0 ? s_amax[m] / 127.0f : xs[m];
     pq_store_dyn(y, y_dtype, static_cast<int64_t>(m) * N + n, epilogue(sum, xsm, bias, bias_dtype, n));
   }
 }
@@ -834,7 +889,7 @@ void launch_skinny_nwu(pq::GemmGroup grp, int bias_dtype, int y_dtype, int M, in
   grp.first[0] = 0;
   for (int i = 0; i < grp.count; ++i) grp.first[i + 1] = grp.first[i] + grp.mem[i].n / 16 / NT;
   const unsigned tiles = static_cast<unsigned>(grp.first[grp.count]);
-  const size_t lds = AQ != 0 ? static_cast<size_t>(M) * (K + 16) : 0;
+  const size_t lds = (AQ == 1 || AQ == 2) ? static_cast<size_t>(M) * (K + 16) : 0;
   if constexpr (AQ == 0) {
     if (M > kSkinnyRows) {   // int8 A, 17-32 rows: one grid row per block of 16
       const dim3 grid(tiles, static_cast<unsigned>((M + kSkinnyRows - 1) / kSkinnyRows));
@@ -910,7 +965,8 @@ void launch_gemm_group(GemmGroup grp, int aq, int bias_dtype, int y_dtype, int m
     launch_skinny<false, 0>(cfg, grp, bias_dtype, y_dtype, m, k, stream);
     return;
   }
-  if (aq == 1) launch_skinny<false, 1>(cfg, grp, bias_dtype, y_dtype, m, k, stream);
+  if (aq == 1 && m == 1) launch_skinny<false, 3>(cfg, grp, bias_dtype, y_dtype, m, k, stream);
+  else if (aq == 1) launch_skinny<false, 1>(cfg, grp, bias_dtype, y_dtype, m, k, stream);
   else launch_skinny<false, 2>(cfg, grp, bias_dtype, y_dtype, m, k, stream);
 }
 
@@ -922,6 +978,7 @@ void launch_gemm_group_partials(GemmGroup grp, int aq, int m, int k, hipStream_t
   }
   const SkinnyCfg cfg = choose_skinny_group(grp, m, k, aq != 0);
   if (aq == 0) launch_skinny<true, 0>(cfg, grp, 0, 0, m, k, stream);
+  else if (aq == 1 && m == 1) launch_skinny<true, 3>(cfg, grp, 0, 0, m, k, stream);
   else if (aq == 1) launch_skinny<true, 1>(cfg, grp, 0, 0, m, k, stream);
   else launch_skinny<true, 2>(cfg, grp, 0, 0, m, k, stream);
 }
