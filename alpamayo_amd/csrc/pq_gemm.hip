@@ -174,19 +174,37 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
   // (the compiler otherwise waits for earlier loads before reusing registers).
   constexpr int QR = (U + 1) / 2;   // AQ == 3: quantizer rounds per batch (two groups each)
   float am3 = 0.0f, inv3 = 0.0f;
-  auto run_batch = [&](const int it) {
+  // AQ == 3: lane l quantizes codes 4 (l & 31) .. + 3 of batch it's group
+  // 2 r + (l >> 5), from 8 bytes of the fp16 row (clamped, unconditional).
+  // The first kPreB batches' bytes are requested at once, ahead of the
+  // first weights; later batches request theirs ahead of their own weights.
+  constexpr int kPreB = AQ == 3 ? 4 : 1;
+  auto load_ah = [&](const int it, uint2 (&ah)[QR]) {
+#pragma unroll
+    for (int r = 0; r < QR; ++r) {
+      const int g = min(wave + it * W * U + W * min(2 * r + (lane >> 5), U - 1), G - 1);
+      ah[r] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(xr) + g * 128 + 4 * (lane & 31));
+    }
+  };
+  uint2 ahp[kPreB][QR];
+  if constexpr (AQ == 3) {
+#pragma unroll
+    for (int b = 0; b < kPreB; ++b) load_ah(b, ahp[b]);
+  }
+  // PB: the batch's index into ahp when it is a constant below kPreB, else -1
+  auto run_batch = [&](const int it, auto pb) {
+    constexpr int PB = decltype(pb)::value;
     const int g0 = wave + it * W * U;
     v4i wb[U][NT];
     uint32_t wm[U][NT];
     v4i a0[U], a1[U];
-    // AQ == 3: lane l quantizes codes 4 (l & 31) .. + 3 of the batch's group
-    // 2 r + (l >> 5); requested ahead of the weights (clamped, unconditional)
     uint2 ah[QR];
     if constexpr (AQ == 3) {
+      if constexpr (PB >= 0) {
 #pragma unroll
-      for (int r = 0; r < QR; ++r) {
-        const int g = min(g0 + W * min(2 * r + (lane >> 5), U - 1), G - 1);
-        ah[r] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(xr) + g * 128 + 4 * (lane & 31));
+        for (int r = 0; r < QR; ++r) ah[r] = ahp[PB][r];
+      } else {
+        load_ah(it, ah);
       }
     }
 #pragma unroll
@@ -357,8 +375,17 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
       }
     }
   };
-  run_batch(0);
-  for (int it = 1; it < batches; ++it) run_batch(it);
+  using First = std::integral_constant<int, 0>;
+  using Later = std::integral_constant<int, -1>;
+  run_batch(0, First{});
+  if constexpr (AQ == 3) {
+    if (batches > 1) run_batch(1, std::integral_constant<int, 1>{});
+    if (batches > 2) run_batch(2, std::integral_constant<int, 2>{});
+    if (batches > 3) run_batch(3, std::integral_constant<int, 3>{});
+    for (int it = kPreB; it < batches; ++it) run_batch(it, Later{});
+  } else {
+    for (int it = 1; it < batches; ++it) run_batch(it, Later{});
+  }
   if constexpr (PARTIALS) return;
 
 #pragma unroll
@@ -852,8 +879,11 @@ struct SkinnyCfg {
 //   tile per workgroup at every token count (two from 5 tokens up measured
 //   slower there: the M = 8 layer 58.3 against 55.8 us, the verify block
 //   2.45 against 2.41 ms).  Not when a member of a group has an odd tile
-//   count, nor with 16 waves behind the A-quantizing prologue (that
-//   combination spills).
+//   count, nor with 16 waves behind the LDS A-quantizing prologue (2-16
+//   rows: that combination spills).  At one row, whose A is quantized in
+//   registers, two tiles on 16 waves stay (the q/k/v group: 192 workgroups,
+//   one batch; GEMM launches 6.64 -> 6.60 us, the decode chain 1.493 ->
+//   1.484 ms).
 // - Behind that prologue, where every workgroup first quantizes the whole
 //   activation row into LDS, 16 waves per workgroup only up to 4 per SIMD
 //   over the grid (the q/k/v group, 384 workgroups, on 8 waves: the M = 1
@@ -869,7 +899,7 @@ SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k, bool two_tiles_ok = tru
   int nt = (two_tiles_ok && tiles % 2 == 0 && (tiles >= 768 || (tiles > 256 && tiles < 512))) ? 2 : 1;
   const int rblk = aq ? 1 : static_cast<int>((m + kSkinnyRows - 1) / kSkinnyRows);   // int8 A: row blocks of 16
   int w = waves_for(static_cast<int64_t>(tiles / nt) * rblk);
-  if (aq && nt == 2 && w == 16) {
+  if (aq && m > 1 && nt == 2 && w == 16) {
     nt = 1;
     w = waves_for(tiles);
   }
