@@ -83,8 +83,8 @@ def gemm_kernel_bytes(M: int, N: int, K: int) -> int:
 
 
 def rotated_gemm_bytes(M: int, N: int, K: int) -> int:
-    """Algorithmic bytes of the decode GEMM that quantizes its A operand in its prologue: int4 codes, fp16
-    scales, int4 zeros, the rotated fp16 rows and their fp32 group maxima in, bf16 out."""
+    """Algorithmic bytes of the decode GEMM that quantizes its A operand itself: int4 codes, fp16 scales,
+    int4 zeros, the rotated fp16 rows and their fp32 group maxima in, bf16 out."""
     return N * K // 2 + 2 * N * K // 128 + N * K // 256 + 2 * M * K + 4 * M * K // 128 + 2 * M * N
 
 
@@ -290,7 +290,7 @@ def main() -> int:
     # ---- the headline layer's own kernels, each timed alone ----------------
     # The grouped M = 1 layer in its two stages (pq_w4a8_linear_group_stage): all rotation launches
     # (rotate_split_kernel) of the pool captured as one graph, all GEMM launches (gemm_skinny quantizing its
-    # A operand in the prologue, from the rotated rows the first stage left in the workspace) as another,
+    # A operand itself, from the rotated row the first stage left in the workspace) as another,
     # each launch with exactly the configuration the layer runs.  Per launch: the GEMM moves its members'
     # packed weights, scales and zeros, their rotated fp16 rows and group maxima, and writes bf16 y; the
     # rotation reads x once and each member's parameters and writes its rotated fp16 rows and group maxima.
@@ -748,8 +748,9 @@ def main() -> int:
 
     rooflines = {
         "decode_gemm_M1_layer": roof(
-            "hbm", "gemm_skinny, A quantized in its prologue (AQ=1): the 32 GEMM launches of the 8-layer pool's "
-            "grouped M=1 layers (q/k/v group, o, gate/up group, down), as the headline layer runs them",
+            "hbm", "gemm_skinny, A quantized in registers by each wave (AQ=3): the 32 GEMM launches of the "
+            "8-layer pool's grouped M=1 layers (q/k/v group, o, gate/up group, down), as the headline layer runs "
+            "them",
             hgemm_gbs, "GB/s", HBM_PEAK_GBS, hgemm_us, n_calls, "decode_gemm_M1_layer",
             bytes_per_launch=round(hgemm_bytes / n_calls)),
         "decode_split_rotation_M1_layer": roof(
