@@ -891,7 +891,10 @@ struct SkinnyCfg {
 //   36-layer decode chain 1.587 -> 1.575 ms, the M = 2 layer 45.6 -> 45.2
 //   us; the other shapes measured no better).
 // - The shallowest batch of at least two groups that divides the K groups
-//   (an uneven last batch is masked by a scalar branch).
+//   (an uneven last batch is masked by a scalar branch); one group per batch
+//   on int8 A at 9-16 rows (the M = 12 layer 54.7 / 54.8 -> 53.8 / 53.7 us,
+//   M = 16 57.2 / 57.4 -> 56.9 / 56.6 us, the verify block 2.109 -> 2.097 ms;
+//   at M = 4 one group per batch measured slower, 47.6 -> 48.7 us).
 SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k, bool two_tiles_ok = true, bool aq = false) {
   const int G = static_cast<int>(k / 128);
   const int tiles = static_cast<int>(n / 16);
@@ -906,7 +909,7 @@ SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k, bool two_tiles_ok = tru
   if (aq && w == 16 && static_cast<int64_t>(tiles / nt) * 16 > 4096) w = 8;
   while (w > 4 && w > G) w >>= 1;
   int u = 2;
-  if (G <= w) u = 1;
+  if (G <= w || (!aq && m > 8 && m <= kSkinnyRows)) u = 1;
   else if (G % (w * 2) == 0) u = 2;
   else if (G % (w * 3) == 0) u = 3;
   else if (G % (w * 4) == 0) u = 4;
