@@ -146,9 +146,11 @@ def test_add_prologue_intermediates(M):
 
 
 @pytest.mark.parametrize("M,K", [(1, 12288), (2, 12288), (3, 12288), (16, 12288), (17, 12288), (24, 12288),
-                                 (32, 12288), (32, 16384), (2, 4096), (16, 4096)])
+                                 (32, 12288), (32, 16384), (2, 4096), (16, 4096), (1, 16384), (1, 8320)])
 def test_swiglu_prologue_intermediates(M, K):
-    """down_proj's input silu(gate) * up: the split pair, the long-row path up to 32 tokens, the row path."""
+    """down_proj's input silu(gate) * up: the split pair, the long-row path up to 32 tokens, the row path.
+    At one token the GEMM quantizes A in registers: K = 16384 takes all 128 group maxima, K = 8320 (65
+    groups) leaves the last batch part past K."""
     ns = (4096,)
     print(f"intermediates swiglu down M={M} K={K}", flush=True)
     seed = zlib.crc32(f"imdg{M}-{K}".encode())
