@@ -60,13 +60,13 @@ namespace {
 // rotation's output): the workgroup derives each row's token scale, writes
 // the int8 codes of all M rows into LDS (row stride K + 16 bytes, so the 16
 // rows of an A fragment hit distinct banks) and reads A from there.  The
-// first batch of weight loads is issued before that prologue.  3 = one fp16
-// rotated row (M = 1, K <= 16384) plus its group maxima, quantized in
-// registers: every wave takes the token scale from the maxima (a DPP
-// maximum, no barrier), quantizes a dword of 4 codes per lane for two of its
-// groups at a time (lanes 0-31 one group, 32-63 the other) and gathers its
-// A fragments from them with ds_bpermute: no LDS image, no barrier before
-// the first MFMA.
+// first batch of weight loads is issued before that prologue.  3 / 4 = one /
+// two fp16 rotated rows (K <= 16384) plus their group maxima, quantized in
+// registers: every wave takes the token scales from the maxima (DPP maxima,
+// no barrier), quantizes a dword of 4 codes per lane for two (group, row)
+// slots at a time (lanes 0-31 one, 32-63 the other) and gathers its A
+// fragments from them with ds_bpermute: no LDS image, no barrier before the
+// first MFMA.
 constexpr int kSkinnyRows = 16;
 
 // The member of a group that owns workgroup tile `unit` (members own
@@ -142,10 +142,21 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
   // compiler's wait before their first use also waited for the weight
   // blocks issued after them, which put the whole prologue behind the
   // weights' round trip.
-  static_assert(AQ != 3 || !RBLK, "one row");
-  uint32_t gm3 = 0;   // AQ == 3: the larger of the lane's two group maxima (G <= 128)
-  if constexpr (AQ == 3)
+  // AQ 3 / 4: A quantized in registers, MQ = 1 / 2 rows
+  constexpr bool kRegA = AQ == 3 || AQ == 4;
+  constexpr int MQ = AQ == 4 ? 2 : 1;
+  static_assert(!kRegA || !RBLK, "one row block");
+  // the larger of the lane's group maxima (G <= 128): one row over the wave
+  // (two per lane), or row lane / 32 over each half-wave (four per lane)
+  uint32_t gm3 = 0;
+  if constexpr (AQ == 3) {
     gm3 = max(__float_as_uint(gmax[min(lane, G - 1)]), __float_as_uint(gmax[min(lane + 64, G - 1)]));
+  } else if constexpr (AQ == 4) {
+    const float* gr = gmax + (lane >> 5) * G;
+    const int l32 = lane & 31;
+    gm3 = max(max(__float_as_uint(gr[min(l32, G - 1)]), __float_as_uint(gr[min(l32 + 32, G - 1)])),
+              max(__float_as_uint(gr[min(l32 + 64, G - 1)]), __float_as_uint(gr[min(l32 + 96, G - 1)])));
+  }
   if constexpr (AQ == 1 || AQ == 2) {
 #pragma unroll
     for (int q = 0; q < kPreMax; ++q) gm[q] = gmax[min(static_cast<int>(threadIdx.x) + q * nthr, M * G - 1)];
@@ -172,22 +183,26 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
   // One batch of U groups per wave; batch 0 (which holds the prologue) is
   // peeled off the loop, so the common single-batch case has no back edge
   // (the compiler otherwise waits for earlier loads before reusing registers).
-  constexpr int QR = (U + 1) / 2;   // AQ == 3: quantizer rounds per batch (two groups each)
-  float am3 = 0.0f, inv3 = 0.0f;
-  // AQ == 3: lane l quantizes codes 4 (l & 31) .. + 3 of batch it's group
-  // 2 r + (l >> 5), from 8 bytes of the fp16 row (clamped, unconditional).
-  // The first kPreB batches' bytes are requested at once, ahead of the
-  // first weights; later batches request theirs ahead of their own weights.
-  constexpr int kPreB = AQ == 3 ? 4 : 1;
+  // Register A: a batch's (group u, row m) slots s = u * MQ + m go two to a
+  // quantizer round, round r taking slots 2 r (lanes 0-31) and 2 r + 1 (lanes
+  // 32-63); lane l quantizes codes 4 (l & 31) .. + 3 of its slot from 8 bytes
+  // of the fp16 row (clamped, unconditional).  The first kPreB batches' bytes
+  // are requested at once, ahead of the first weights; later batches request
+  // theirs ahead of their own weights.
+  constexpr int QR = (U * MQ + 1) / 2;
+  float am3 = 0.0f, inv3 = 0.0f, am3b = 0.0f, inv3b = 0.0f;   // rows 0 and 1
+  constexpr int kPreB = kRegA ? 4 : 1;
   auto load_ah = [&](const int it, uint2 (&ah)[QR]) {
 #pragma unroll
     for (int r = 0; r < QR; ++r) {
-      const int g = min(wave + it * W * U + W * min(2 * r + (lane >> 5), U - 1), G - 1);
-      ah[r] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(xr) + g * 128 + 4 * (lane & 31));
+      const int sl = 2 * r + (lane >> 5);
+      const int g = min(wave + it * W * U + W * min(sl / MQ, U - 1), G - 1);
+      ah[r] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(xr) + (sl % MQ) * K + g * 128 +
+                                              4 * (lane & 31));
     }
   };
   uint2 ahp[kPreB][QR];
-  if constexpr (AQ == 3) {
+  if constexpr (kRegA) {
 #pragma unroll
     for (int b = 0; b < kPreB; ++b) load_ah(b, ahp[b]);
   }
@@ -199,7 +214,7 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
     uint32_t wm[U][NT];
     v4i a0[U], a1[U];
     uint2 ah[QR];
-    if constexpr (AQ == 3) {
+    if constexpr (kRegA) {
       if constexpr (PB >= 0) {
 #pragma unroll
         for (int r = 0; r < QR; ++r) ah[r] = ahp[PB][r];
@@ -232,22 +247,40 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
       }
     }
     uint32_t qd[QR];
-    if constexpr (AQ == 3) {
-      if (it == 0) {   // the token scale, the same in every wave (maxima >= 0: unsigned order)
-        am3 = __uint_as_float(pq_wave_umax(gm3));
+    if constexpr (kRegA) {
+      if (it == 0) {   // the token scales, the same in every wave (maxima >= 0: unsigned order)
+        if constexpr (MQ == 1) {
+          am3 = __uint_as_float(pq_wave_umax(gm3));
+        } else {
+          // the first five steps of the wave maximum leave lanes 0-31's in lane 31, 32-63's in lane 63
+          uint32_t u5 = pq_dpp_umax<0xb1, 0xf>(gm3);
+          u5 = pq_dpp_umax<0x4e, 0xf>(u5);
+          u5 = pq_dpp_umax<0x141, 0xf>(u5);
+          u5 = pq_dpp_umax<0x140, 0xf>(u5);
+          u5 = pq_dpp_umax<0x142, 0xa>(u5);
+          am3 = __uint_as_float(__builtin_amdgcn_readlane(static_cast<int>(u5), 31));
+          am3b = __uint_as_float(__builtin_amdgcn_readlane(static_cast<int>(u5), 63));
+          inv3b = inv_scale(am3b);
+        }
         inv3 = inv_scale(am3);
       }
+      // a lane's slots all lie in row (lane / 32) % MQ
+      const float inv_l = MQ == 2 && (lane >> 5) ? inv3b : inv3;
 #pragma unroll
-      for (int r = 0; r < QR; ++r) qd[r] = quant4_f16(ah[r].x, ah[r].y, inv3);
+      for (int r = 0; r < QR; ++r) qd[r] = quant4_f16(ah[r].x, ah[r].y, inv_l);
       if constexpr (PARTIALS) {
-        // Parity form: the member's first workgroup writes the codes and the token scale it multiplies.
+        // Parity form: the member's first workgroup writes the codes and the token scales it multiplies.
         if (blockIdx.x == static_cast<unsigned>(grp.first[mi])) {
 #pragma unroll
           for (int r = 0; r < QR; ++r) {
-            const int uu = 2 * r + (lane >> 5), g = g0 + W * uu;
-            if (uu < U && g < G) *reinterpret_cast<uint32_t*>(mb.a_out + g * 128 + 4 * (lane & 31)) = qd[r];
+            const int sl = 2 * r + (lane >> 5), uu = sl / MQ, g = g0 + W * uu;
+            if (uu < U && g < G)
+              *reinterpret_cast<uint32_t*>(mb.a_out + (sl % MQ) * K + g * 128 + 4 * (lane & 31)) = qd[r];
           }
-          if (it == 0 && threadIdx.x == 0) mb.as_out[0] = am3 / 127.0f;
+          if (it == 0 && threadIdx.x == 0) {
+            mb.as_out[0] = am3 / 127.0f;
+            if (MQ == 2) mb.as_out[1] = am3b / 127.0f;
+          }
         }
       }
     }
@@ -323,18 +356,20 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int g = g0 + W * u;
-      // AQ == 3 multiplies a group past G too (its clamped operands, scaled
-      // by 0): behind this branch the compiler moved the batch's weight loads
-      // down to their use, after the quantization
-      if (AQ == 3 || g < G) {
+      // register A multiplies a group past G too (its clamped operands,
+      // scaled by 0): behind this branch the compiler moved the batch's
+      // weight loads down to their use, after the quantization
+      if (kRegA || g < G) {
         if constexpr (AQ == 1 || AQ == 2) {   // A from the LDS image, next to its use
           a0[u] = *reinterpret_cast<const v4i*>(al + g * 128);
           a1[u] = *reinterpret_cast<const v4i*>(al + g * 128 + 16);
-        } else if constexpr (AQ == 3) {
-          // codes j*32 .. j*32+31 of group u: dwords 8j .. 8j+7 of the lanes that quantized it
-          // (g is wave-uniform here, so every lane takes part)
-          const int src = ((u & 1) * 32 + 8 * j) * 4;
-          const int v = static_cast<int>(qd[u >> 1]);
+        } else if constexpr (kRegA) {
+          // codes j*32 .. j*32+31 of group u, row c (rows past MQ repeat the last): dwords 8j .. 8j+7 of
+          // the lanes that quantized slot u * MQ + row, all in round (u * MQ) / 2 (g is wave-uniform
+          // here, so every lane takes part)
+          const int sl = u * MQ + min(c, MQ - 1);
+          const int src = ((sl & 1) * 32 + 8 * j) * 4;
+          const int v = static_cast<int>(qd[(u * MQ) >> 1]);
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             a0[u][q] = __builtin_amdgcn_ds_bpermute(src + 4 * q, v);
@@ -367,7 +402,7 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
               if (m < M && g < G) partials[(static_cast<int64_t>(m) * G + g) * N + (tile0 + nt) * 16 + c] = p[v];
             }
           } else {
-            const float sc = AQ != 3 || g < G ? meta_scale(meta) : 0.0f;
+            const float sc = !kRegA || g < G ? meta_scale(meta) : 0.0f;
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[nt][v] = fmaf(static_cast<float>(p[v]), sc, acc[nt][v]);
           }
@@ -378,7 +413,7 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
   using First = std::integral_constant<int, 0>;
   using Later = std::integral_constant<int, -1>;
   run_batch(0, First{});
-  if constexpr (AQ == 3) {
+  if constexpr (kRegA) {
     if (batches > 1) run_batch(1, std::integral_constant<int, 1>{});
     if (batches > 2) run_batch(2, std::integral_constant<int, 2>{});
     if (batches > 3) run_batch(3, std::integral_constant<int, 3>{});
@@ -403,7 +438,7 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
 #pragma unroll
     for (int w = 0; w < W; ++w) sum += red[w][nt][rv][rl];
     const int n = (tile0 + nt) * 16 + (rl & 15);
-    const float xsm = AQ == 3 ? am3 / 127.0f : AQ != 0 ? s_amax[m] / 127.0f : xs[m];
+    const float xsm = kRegA ? (m == 0 ? am3 : am3b) / 127.0f : AQ != 0 ? s_amax[m] / 127.0f : xs[m];
     pq_store_dyn(y, y_dtype, static_cast<int64_t>(m) * N + n, epilogue(sum, xsm, bias, bias_dtype, n));
   }
 }
@@ -999,6 +1034,7 @@ void launch_gemm_group(GemmGroup grp, int aq, int bias_dtype, int y_dtype, int m
     return;
   }
   if (aq == 1 && m == 1) launch_skinny<false, 3>(cfg, grp, bias_dtype, y_dtype, m, k, stream);
+  else if (aq == 1 && m == 2) launch_skinny<false, 4>(cfg, grp, bias_dtype, y_dtype, m, k, stream);
   else if (aq == 1) launch_skinny<false, 1>(cfg, grp, bias_dtype, y_dtype, m, k, stream);
   else launch_skinny<false, 2>(cfg, grp, bias_dtype, y_dtype, m, k, stream);
 }
@@ -1012,6 +1048,7 @@ void launch_gemm_group_partials(GemmGroup grp, int aq, int m, int k, hipStream_t
   const SkinnyCfg cfg = choose_skinny_group(grp, m, k, aq != 0);
   if (aq == 0) launch_skinny<true, 0>(cfg, grp, 0, 0, m, k, stream);
   else if (aq == 1 && m == 1) launch_skinny<true, 3>(cfg, grp, 0, 0, m, k, stream);
+  else if (aq == 1 && m == 2) launch_skinny<true, 4>(cfg, grp, 0, 0, m, k, stream);
   else if (aq == 1) launch_skinny<true, 1>(cfg, grp, 0, 0, m, k, stream);
   else launch_skinny<true, 2>(cfg, grp, 0, 0, m, k, stream);
 }
