@@ -914,11 +914,11 @@ struct SkinnyCfg {
 //   tile per workgroup at every token count (two from 5 tokens up measured
 //   slower there: the M = 8 layer 58.3 against 55.8 us, the verify block
 //   2.45 against 2.41 ms).  Not when a member of a group has an odd tile
-//   count, nor with 16 waves behind the LDS A-quantizing prologue (2-16
-//   rows: that combination spills).  At one row, whose A is quantized in
-//   registers, two tiles on 16 waves stay (the q/k/v group: 192 workgroups,
-//   one batch; GEMM launches 6.64 -> 6.60 us, the decode chain 1.493 ->
-//   1.484 ms).
+//   count, nor with 16 waves behind the LDS A-quantizing prologue (3-16
+//   rows: that combination spills).  At one and two rows, whose A is
+//   quantized in registers, two tiles on 16 waves stay (the q/k/v group: 192
+//   workgroups, one batch; M = 1: GEMM launches 6.64 -> 6.60 us, the decode
+//   chain 1.493 -> 1.484 ms; the M = 2 layer 42.8 / 42.9 -> 42.3 / 42.2 us).
 // - Behind that prologue, where every workgroup first quantizes the whole
 //   activation row into LDS, 16 waves per workgroup only up to 4 per SIMD
 //   over the grid (the q/k/v group, 384 workgroups, on 8 waves: the M = 1
@@ -937,7 +937,7 @@ SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k, bool two_tiles_ok = tru
   int nt = (two_tiles_ok && tiles % 2 == 0 && (tiles >= 768 || (tiles > 256 && tiles < 512))) ? 2 : 1;
   const int rblk = aq ? 1 : static_cast<int>((m + kSkinnyRows - 1) / kSkinnyRows);   // int8 A: row blocks of 16
   int w = waves_for(static_cast<int64_t>(tiles / nt) * rblk);
-  if (aq && m > 1 && nt == 2 && w == 16) {
+  if (aq && m > 2 && nt == 2 && w == 16) {
     nt = 1;
     w = waves_for(tiles);
   }
