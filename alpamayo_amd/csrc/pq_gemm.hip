@@ -137,11 +137,6 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
   float gm[kPreMax];
   uint4 pre[kPre][AQ == 2 ? 2 : 1];
   bool preloaded = false;
-  // All of these loads are unconditional, with clamped indices (their values
-  // are used only where the index is in range): behind a branch, the
-  // compiler's wait before their first use also waited for the weight
-  // blocks issued after them, which put the whole prologue behind the
-  // weights' round trip.
   // AQ 3 / 4: A quantized in registers, MQ = 1 / 2 rows
   constexpr bool kRegA = AQ == 3 || AQ == 4;
   constexpr int MQ = AQ == 4 ? 2 : 1;
@@ -157,6 +152,11 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
     gm3 = max(max(__float_as_uint(gr[min(l32, G - 1)]), __float_as_uint(gr[min(l32 + 32, G - 1)])),
               max(__float_as_uint(gr[min(l32 + 64, G - 1)]), __float_as_uint(gr[min(l32 + 96, G - 1)])));
   }
+  // All of these loads are unconditional, with clamped indices (their values
+  // are used only where the index is in range): behind a branch, the
+  // compiler's wait before their first use also waited for the weight
+  // blocks issued after them, which put the whole prologue behind the
+  // weights' round trip.
   if constexpr (AQ == 1 || AQ == 2) {
 #pragma unroll
     for (int q = 0; q < kPreMax; ++q) gm[q] = gmax[min(static_cast<int>(threadIdx.x) + q * nthr, M * G - 1)];
