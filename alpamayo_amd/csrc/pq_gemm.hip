@@ -87,28 +87,23 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
   extern __shared__ __attribute__((aligned(16))) int8_t aq[];
   const int mi = group_member(grp, blockIdx.x);
   const pq::GemmMember& mb = grp.mem[mi];
-  // RBLK (int8 A, 17-32 rows): grid.y cuts the rows into blocks of 16
-  // (block b takes rows 16b .. 16b+15; every pointer below moves to the
-  // block's first row).  A separate instance, so that launches of up to 16
-  // rows keep their own code (the row-block arithmetic ahead of the first
-  // loads measured 1-3 % slower on their decode layers).
+  // RBLK (int8 A, 17-32 rows): the workgroup carries both row blocks of 16
+  // (rows 0-15 and 16 .. M-1) as two MFMA chains on every weight fragment,
+  // so the weights stream once.  A separate instance, so that launches of up
+  // to 16 rows keep their own code.
   static_assert(!RBLK || AQ == 0, "row blocks on int8 A only");
-  const int rb = RBLK ? static_cast<int>(blockIdx.y) : 0;
-  if constexpr (RBLK) M = min(M - rb * kSkinnyRows, kSkinnyRows);
-  const int8_t* __restrict__ xq = RBLK ? mb.xq + static_cast<int64_t>(rb) * kSkinnyRows * K : mb.xq;
-  const float* __restrict__ xs = RBLK ? mb.xs + rb * kSkinnyRows : mb.xs;
+  constexpr int RB = RBLK ? 2 : 1;
+  const int8_t* __restrict__ xq = mb.xq;
+  const float* __restrict__ xs = mb.xs;
   const void* __restrict__ xr = mb.xr;
   const float* __restrict__ gmax = mb.gmax;
   const uint8_t* __restrict__ wpack = mb.wpack;
   const uint32_t* __restrict__ wmeta = mb.wmeta;
   const void* __restrict__ bias = mb.bias;
   const int N = mb.n;
-  void* __restrict__ y = RBLK ? static_cast<void*>(static_cast<char*>(mb.y) + static_cast<int64_t>(rb) * kSkinnyRows *
-                                                                                N * (y_dtype == PQ_F32 ? 4 : 2))
-                              : mb.y;
+  void* __restrict__ y = mb.y;
   const int G = K >> 7;
   int32_t* __restrict__ partials = mb.partials;
-  if constexpr (PARTIALS && RBLK) partials += static_cast<int64_t>(rb) * kSkinnyRows * G * N;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar branches
   const int lane = threadIdx.x & 63;
   const int c = lane & 15;
@@ -117,13 +112,18 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
   const int astride = K + 16;
   const int tile0 = (blockIdx.x - grp.first[mi]) * NT;
 
-  float acc[NT][4];
+  float acc[RB][NT][4];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt)
+  for (int b = 0; b < RB; ++b)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) acc[nt][v] = 0.0f;
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[b][nt][v] = 0.0f;
 
   const int8_t* ap = xq + static_cast<int64_t>(arow ? c : 0) * K + j * 32;
+  // the second row block's rows (RBLK: M >= 17, so row 16 exists)
+  const int8_t* ap1 = xq + static_cast<int64_t>(RBLK && kSkinnyRows + c < M ? kSkinnyRows + c : kSkinnyRows) * K +
+                      j * 32;
   const int8_t* al = aq + (arow ? c : 0) * astride + j * 32;
   const int nthr = W * 64;
   const int k8 = K >> 3;
@@ -213,6 +213,7 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
     v4i wb[U][NT];
     uint32_t wm[U][NT];
     v4i a0[U], a1[U];
+    v4i a0b[RBLK ? U : 1], a1b[RBLK ? U : 1];   // RBLK: the second row block's fragments
     uint2 ah[QR];
     if constexpr (kRegA) {
       if constexpr (PB >= 0) {
@@ -243,6 +244,10 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
           // branch around the loads would make the compiler wait early.
           a0[u] = *reinterpret_cast<const v4i*>(ap + static_cast<int64_t>(g) * 128);
           a1[u] = *reinterpret_cast<const v4i*>(ap + static_cast<int64_t>(g) * 128 + 16);
+          if constexpr (RBLK) {
+            a0b[u] = *reinterpret_cast<const v4i*>(ap1 + static_cast<int64_t>(g) * 128);
+            a1b[u] = *reinterpret_cast<const v4i*>(ap1 + static_cast<int64_t>(g) * 128 + 16);
+          }
         }
       }
     }
@@ -390,21 +395,31 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
           const v4i b1 = nibbles16(static_cast<uint32_t>(w.z), static_cast<uint32_t>(w.w));
           const int nz = static_cast<int>(meta_neg_zero4(meta));
           const v4i bz = {nz, nz, nz, nz};
-          v4i p = {0, 0, 0, 0};
-          p = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, b0, p, 0, 0, 0);
-          p = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, b1, p, 0, 0, 0);
-          p = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, bz, p, 0, 0, 0);
-          p = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, bz, p, 0, 0, 0);
+          v4i p[RB];
+#pragma unroll
+          for (int b = 0; b < RB; ++b) {   // the row blocks share the weight fragment
+            const v4i x0 = b == 0 ? av0 : a0b[RBLK ? u : 0], x1 = b == 0 ? av1 : a1b[RBLK ? u : 0];
+            p[b] = v4i{0, 0, 0, 0};
+            p[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, b0, p[b], 0, 0, 0);
+            p[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, b1, p[b], 0, 0, 0);
+            p[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, bz, p[b], 0, 0, 0);
+            p[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, bz, p[b], 0, 0, 0);
+          }
           if constexpr (PARTIALS) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              const int m = 4 * j + v;
-              if (m < M && g < G) partials[(static_cast<int64_t>(m) * G + g) * N + (tile0 + nt) * 16 + c] = p[v];
-            }
+            for (int b = 0; b < RB; ++b)
+#pragma unroll
+              for (int v = 0; v < 4; ++v) {
+                const int m = b * kSkinnyRows + 4 * j + v;
+                if (m < M && g < G)
+                  partials[(static_cast<int64_t>(m) * G + g) * N + (tile0 + nt) * 16 + c] = p[b][v];
+              }
           } else {
             const float sc = !kRegA || g < G ? meta_scale(meta) : 0.0f;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) acc[nt][v] = fmaf(static_cast<float>(p[v]), sc, acc[nt][v]);
+            for (int b = 0; b < RB; ++b)
+#pragma unroll
+              for (int v = 0; v < 4; ++v) acc[b][nt][v] = fmaf(static_cast<float>(p[b][v]), sc, acc[b][nt][v]);
           }
         }
       }
@@ -423,23 +438,28 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
   }
   if constexpr (PARTIALS) return;
 
+  // the row blocks one after the other through the same LDS
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt)
+  for (int b = 0; b < RB; ++b) {
+    if (b > 0) __syncthreads();   // the previous block's sums are read
 #pragma unroll
-    for (int v = 0; v < 4; ++v) red[wave][nt][v][lane] = acc[nt][v];
-  __syncthreads();
-  for (int t = threadIdx.x; t < NT * 256; t += W * 64) {
-    const int nt = t >> 8;
-    const int rv = (t >> 6) & 3;
-    const int rl = t & 63;
-    const int m = 4 * (rl >> 4) + rv;
-    if (m >= M) continue;
-    float sum = 0.0f;
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-    for (int w = 0; w < W; ++w) sum += red[w][nt][rv][rl];
-    const int n = (tile0 + nt) * 16 + (rl & 15);
-    const float xsm = kRegA ? (m == 0 ? am3 : am3b) / 127.0f : AQ != 0 ? s_amax[m] / 127.0f : xs[m];
-    pq_store_dyn(y, y_dtype, static_cast<int64_t>(m) * N + n, epilogue(sum, xsm, bias, bias_dtype, n));
+      for (int v = 0; v < 4; ++v) red[wave][nt][v][lane] = acc[b][nt][v];
+    __syncthreads();
+    for (int t = threadIdx.x; t < NT * 256; t += W * 64) {
+      const int nt = t >> 8;
+      const int rv = (t >> 6) & 3;
+      const int rl = t & 63;
+      const int m = b * kSkinnyRows + 4 * (rl >> 4) + rv;
+      if (m >= M) continue;
+      float sum = 0.0f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) sum += red[w][nt][rv][rl];
+      const int n = (tile0 + nt) * 16 + (rl & 15);
+      const float xsm = kRegA ? (m == 0 ? am3 : am3b) / 127.0f : AQ != 0 ? s_amax[m] / 127.0f : xs[m];
+      pq_store_dyn(y, y_dtype, static_cast<int64_t>(m) * N + n, epilogue(sum, xsm, bias, bias_dtype, n));
+    }
   }
 }
 
@@ -935,8 +955,7 @@ SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k, bool two_tiles_ok = tru
   const int tiles = static_cast<int>(n / 16);
   auto waves_for = [](int64_t wgs) { return wgs * 16 <= 6144 ? 16 : wgs * 8 <= 6144 ? 8 : 4; };
   int nt = (two_tiles_ok && tiles % 2 == 0 && (tiles >= 768 || (tiles > 256 && tiles < 512))) ? 2 : 1;
-  const int rblk = aq ? 1 : static_cast<int>((m + kSkinnyRows - 1) / kSkinnyRows);   // int8 A: row blocks of 16
-  int w = waves_for(static_cast<int64_t>(tiles / nt) * rblk);
+  int w = waves_for(static_cast<int64_t>(tiles / nt));
   if (aq && m > 2 && nt == 2 && w == 16) {
     nt = 1;
     w = waves_for(tiles);
@@ -959,9 +978,8 @@ void launch_skinny_nwu(pq::GemmGroup grp, int bias_dtype, int y_dtype, int M, in
   const unsigned tiles = static_cast<unsigned>(grp.first[grp.count]);
   const size_t lds = (AQ == 1 || AQ == 2) ? static_cast<size_t>(M) * (K + 16) : 0;
   if constexpr (AQ == 0) {
-    if (M > kSkinnyRows) {   // int8 A, 17-32 rows: one grid row per block of 16
-      const dim3 grid(tiles, static_cast<unsigned>((M + kSkinnyRows - 1) / kSkinnyRows));
-      gemm_skinny<NT, W, U, PARTIALS, AQ, true><<<grid, W * 64, 0, stream>>>(grp, bias_dtype, y_dtype, M, K);
+    if (M > kSkinnyRows) {   // int8 A, 17-32 rows: both row blocks of 16 in every workgroup
+      gemm_skinny<NT, W, U, PARTIALS, AQ, true><<<tiles, W * 64, 0, stream>>>(grp, bias_dtype, y_dtype, M, K);
       return;
     }
   }
