@@ -79,7 +79,7 @@ __device__ __forceinline__ int group_member(const pq::GemmGroup& grp, int unit) 
   return mi;
 }
 
-template <int NT, int W, int U, bool PARTIALS, int AQ, bool RBLK = false>
+template <int NT, int W, int U, bool PARTIALS, int AQ, int RB = 1>
 __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) void gemm_skinny(
     const pq::GemmGroup grp, int bias_dtype, int y_dtype, int M, int K) {
   __shared__ float red[W][NT][4][64];
@@ -87,12 +87,12 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
   extern __shared__ __attribute__((aligned(16))) int8_t aq[];
   const int mi = group_member(grp, blockIdx.x);
   const pq::GemmMember& mb = grp.mem[mi];
-  // RBLK (int8 A, 17-32 rows): the workgroup carries both row blocks of 16
-  // (rows 0-15 and 16 .. M-1) as two MFMA chains on every weight fragment,
-  // so the weights stream once.  A separate instance, so that launches of up
-  // to 16 rows keep their own code.
-  static_assert(!RBLK || AQ == 0, "row blocks on int8 A only");
-  constexpr int RB = RBLK ? 2 : 1;
+  // RB > 1 (int8 A, 17-64 rows): the workgroup carries RB row blocks of 16
+  // (block b: rows 16b .. 16b + 15, rows past M repeating row M - 1) as RB
+  // MFMA chains on every weight fragment, so the weights stream once.
+  // Separate instances, so that launches of up to 16 rows keep their code.
+  static_assert(RB == 1 || AQ == 0, "row blocks on int8 A only");
+  static_assert(RB >= 1 && RB <= 4, "up to 64 rows");
   const int8_t* __restrict__ xq = mb.xq;
   const float* __restrict__ xs = mb.xs;
   const void* __restrict__ xr = mb.xr;
@@ -121,9 +121,10 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
       for (int v = 0; v < 4; ++v) acc[b][nt][v] = 0.0f;
 
   const int8_t* ap = xq + static_cast<int64_t>(arow ? c : 0) * K + j * 32;
-  // the second row block's rows (RBLK: M >= 17, so row 16 exists)
-  const int8_t* ap1 = xq + static_cast<int64_t>(RBLK && kSkinnyRows + c < M ? kSkinnyRows + c : kSkinnyRows) * K +
-                      j * 32;
+  // the further row blocks' rows
+  const int8_t* apb[RB > 1 ? RB - 1 : 1];
+#pragma unroll
+  for (int b = 1; b < RB; ++b) apb[b - 1] = xq + static_cast<int64_t>(min(b * kSkinnyRows + c, M - 1)) * K + j * 32;
   const int8_t* al = aq + (arow ? c : 0) * astride + j * 32;
   const int nthr = W * 64;
   const int k8 = K >> 3;
@@ -140,7 +141,7 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
   // AQ 3 / 4: A quantized in registers, MQ = 1 / 2 rows
   constexpr bool kRegA = AQ == 3 || AQ == 4;
   constexpr int MQ = AQ == 4 ? 2 : 1;
-  static_assert(!kRegA || !RBLK, "one row block");
+  static_assert(!kRegA || RB == 1, "one row block");
   // the larger of the lane's group maxima (G <= 128): one row over the wave
   // (two per lane), or row lane / 32 over each half-wave (four per lane)
   uint32_t gm3 = 0;
@@ -213,7 +214,7 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
     v4i wb[U][NT];
     uint32_t wm[U][NT];
     v4i a0[U], a1[U];
-    v4i a0b[RBLK ? U : 1], a1b[RBLK ? U : 1];   // RBLK: the second row block's fragments
+    v4i a0b[RB > 1 ? RB - 1 : 1][U], a1b[RB > 1 ? RB - 1 : 1][U];   // the further row blocks' fragments
     uint2 ah[QR];
     if constexpr (kRegA) {
       if constexpr (PB >= 0) {
@@ -244,9 +245,10 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
           // branch around the loads would make the compiler wait early.
           a0[u] = *reinterpret_cast<const v4i*>(ap + static_cast<int64_t>(g) * 128);
           a1[u] = *reinterpret_cast<const v4i*>(ap + static_cast<int64_t>(g) * 128 + 16);
-          if constexpr (RBLK) {
-            a0b[u] = *reinterpret_cast<const v4i*>(ap1 + static_cast<int64_t>(g) * 128);
-            a1b[u] = *reinterpret_cast<const v4i*>(ap1 + static_cast<int64_t>(g) * 128 + 16);
+#pragma unroll
+          for (int b = 1; b < RB; ++b) {
+            a0b[b - 1][u] = *reinterpret_cast<const v4i*>(apb[b - 1] + static_cast<int64_t>(g) * 128);
+            a1b[b - 1][u] = *reinterpret_cast<const v4i*>(apb[b - 1] + static_cast<int64_t>(g) * 128 + 16);
           }
         }
       }
@@ -398,7 +400,7 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
           v4i p[RB];
 #pragma unroll
           for (int b = 0; b < RB; ++b) {   // the row blocks share the weight fragment
-            const v4i x0 = b == 0 ? av0 : a0b[RBLK ? u : 0], x1 = b == 0 ? av1 : a1b[RBLK ? u : 0];
+            const v4i x0 = b == 0 ? av0 : a0b[b > 0 ? b - 1 : 0][u], x1 = b == 0 ? av1 : a1b[b > 0 ? b - 1 : 0][u];
             p[b] = v4i{0, 0, 0, 0};
             p[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, b0, p[b], 0, 0, 0);
             p[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, b1, p[b], 0, 0, 0);
@@ -911,10 +913,11 @@ void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int M
 // ---------------------------------------------------------------------------
 // Host-side configuration
 // ---------------------------------------------------------------------------
-// The decode GEMM on int8 A takes up to 32 rows, in row blocks of 16 (one
-// grid row per block; the weights are read once per block): M = 17-32 at N = K = 4096 7-9 us against 24.5 us on the prefill
-// kernel's 64 x 128 tiles, M = 32 at K = 12288 17.5 against 65 us.
-constexpr int kSkinnyMaxM = 32;
+// The decode GEMM on int8 A takes up to 64 rows, all its row blocks of 16
+// in every workgroup (the weights are read once): the grouped decode layer at
+// M = 33-64 on it against the row rotate+quant kernel and the prefill GEMM's
+// tiles is recorded in the design notes.
+constexpr int kSkinnyMaxM = 64;
 
 struct SkinnyCfg {
   int nt;  // 16-column tiles per workgroup
@@ -963,7 +966,7 @@ SkinnyCfg choose_skinny(int64_t m, int64_t n, int64_t k, bool two_tiles_ok = tru
   if (aq && w == 16 && static_cast<int64_t>(tiles / nt) * 16 > 4096) w = 8;
   while (w > 4 && w > G) w >>= 1;
   int u = 2;
-  if (G <= w || (!aq && m > 8 && m <= kSkinnyRows)) u = 1;
+  if (G <= w || (!aq && m > 8 && m <= kSkinnyRows) || m > 2 * kSkinnyRows) u = 1;
   else if (G % (w * 2) == 0) u = 2;
   else if (G % (w * 3) == 0) u = 3;
   else if (G % (w * 4) == 0) u = 4;
@@ -978,8 +981,20 @@ void launch_skinny_nwu(pq::GemmGroup grp, int bias_dtype, int y_dtype, int M, in
   const unsigned tiles = static_cast<unsigned>(grp.first[grp.count]);
   const size_t lds = (AQ == 1 || AQ == 2) ? static_cast<size_t>(M) * (K + 16) : 0;
   if constexpr (AQ == 0) {
-    if (M > kSkinnyRows) {   // int8 A, 17-32 rows: both row blocks of 16 in every workgroup
-      gemm_skinny<NT, W, U, PARTIALS, AQ, true><<<tiles, W * 64, 0, stream>>>(grp, bias_dtype, y_dtype, M, K);
+    // int8 A, 17-64 rows: every workgroup carries the ceil(M / 16) row blocks;
+    // from 33 rows one group per batch (their A fragments fill the registers)
+    if (M > 2 * kSkinnyRows) {
+      if constexpr (U != 1) {
+        launch_skinny_nwu<NT, W, 1, PARTIALS, AQ>(grp, bias_dtype, y_dtype, M, K, stream);
+      } else if (M > 3 * kSkinnyRows) {
+        gemm_skinny<NT, W, U, PARTIALS, AQ, 4><<<tiles, W * 64, 0, stream>>>(grp, bias_dtype, y_dtype, M, K);
+      } else {
+        gemm_skinny<NT, W, U, PARTIALS, AQ, 3><<<tiles, W * 64, 0, stream>>>(grp, bias_dtype, y_dtype, M, K);
+      }
+      return;
+    }
+    if (M > kSkinnyRows) {
+      gemm_skinny<NT, W, U, PARTIALS, AQ, 2><<<tiles, W * 64, 0, stream>>>(grp, bias_dtype, y_dtype, M, K);
       return;
     }
   }

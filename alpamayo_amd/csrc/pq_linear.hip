@@ -9,7 +9,7 @@
 //     row's absmax per group; the decode GEMM derives the token scales and
 //     quantizes A into LDS in its prologue, while its first weight blocks
 //     are already in flight.
-//   split3 (k >= 4096 beyond that, up to 32 tokens): the split rotation
+//   split3 (k >= 4096 beyond that, up to 64 tokens): the split rotation
 //     with the rows spread over waves, a token-scale + int8 kernel, then
 //     the decode GEMM on int8 A (three launches).
 //   rows (otherwise): pq_rotate_quant_i8 (rotation + absmax + int8 quant of
@@ -48,7 +48,7 @@ bool use_split(int64_t m, int64_t k) {
   return (m * k <= 8192 || (k >= 8192 && m <= 2)) && pq::gemm_rotated_supported(m, k);
 }
 
-// Rows of 4096 channels or more past the split pair, up to 32 tokens: the
+// Rows of 4096 channels or more past the split pair, up to 64 tokens: the
 // split rotation with its rows spread over waves (kSplitRowsPerWave rows
 // each), a small kernel for the token scales and int8 codes, then the decode
 // GEMM on int8 A.  The row kernel runs each row on one CU, whose VALU needs
@@ -61,11 +61,13 @@ bool use_split(int64_t m, int64_t k) {
 // rotation).  One row per wave: the verify block at 16 tokens 2.40 -> 2.34 ms
 // against four rows per wave (2.36 ms with two, 2.50 ms with eight).
 constexpr int kSplitRowsPerWave = 1;
-// Up to 32 tokens: with one row per wave the split rotation takes any row
-// count, and the decode GEMM on int8 A takes 32 rows (two row blocks).  At
-// 17-32 tokens the row kernel would run each 12288-channel row on one CU
-// (the decode layer at M = 17: 80.1 us with down on the row kernel).
-constexpr int kSplit3MaxRows = 32;
+// Up to 64 tokens: with one row per wave the split rotation takes any row
+// count, and the decode GEMM on int8 A takes 64 rows (up to four row blocks
+// per workgroup).  At 17-64 tokens the row kernel would run each
+// 12288-channel row on one CU (the decode layer at M = 17: 80.1 us with down
+// on the row kernel), and from 33 tokens the prefill GEMM's tiles re-read
+// the weights per row tile.
+constexpr int kSplit3MaxRows = 64;
 bool use_split3(int64_t m, int64_t k) {
   return !use_split(m, k) && m >= 1 && m <= kSplit3MaxRows && k >= 4096 && k <= 16384 && k % 128 == 0;
 }

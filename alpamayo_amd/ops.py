@@ -760,11 +760,11 @@ def split_path(m, k) -> bool:
     pq_w4a8_linear_split_path, restated in Python so that torch.compile can guard on it when m is a symbolic
     size (tests check the two agree).  Split pair: m * k <= 8192, or k >= 8192 and m <= 2, as long as the
     GEMM's LDS image of A fits (m <= 16, m * (k + 16) <= 80 KiB); three-launch rows: otherwise
-    k in [4096, 16384] and m <= 32."""
+    k in [4096, 16384] and m <= 64."""
     if m < 1 or k % 128 or k > 16384:
         return False
     split = (m * k <= 8192 or (k >= 8192 and m <= 2)) and m <= 16 and m * (k + 16) <= 80 * 1024
-    return bool(split or (m <= 32 and k >= 4096))
+    return bool(split or (m <= 64 and k >= 4096))
 
 
 def linear_group_workspace_bytes(m: int, k: int, count: int) -> int:

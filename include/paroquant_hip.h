@@ -267,9 +267,9 @@ typedef struct pq_linear_member {
 
 /* 1 when pq_w4a8_linear (and the group entry points) run m tokens of k
  * features through the split rotation (waves per 128-channel group, spread
- * over the chip): with a GEMM that quantizes A in its prologue (m*k <= 8192,
+ * over the chip): with a GEMM that quantizes A itself (m*k <= 8192,
  * or k >= 8192 and m <= 2), or for rows of 4096 channels or more (k a
- * multiple of 128 in [4096, 16384], up to 32 tokens) with a token-scale +
+ * multiple of 128 in [4096, 16384], up to 64 tokens) with a token-scale +
  * int8 kernel and the
  * GEMM on int8 A.  0 when they run the row rotate+quant kernel plus the
  * GEMM.  Callers use it to decide whether an elementwise step is cheaper

@@ -21,11 +21,11 @@ int main(void) {
   /* decode sizes: rotated fp32 rows (256-byte aligned) + per-group maxima */
   CHECK(pq_w4a8_linear_workspace_size(1, 4096, 4096, 8) == 4096 * 4 + 32 * 4);
   /* row path: int8 codes + token scales */
-  CHECK(pq_w4a8_linear_workspace_size(64, 4096, 4096, 8) == 64 * 4096 + 64 * 4);
-  CHECK(pq_w4a8_linear_group_workspace_size(64, 4096, 3) == 3 * (64 * 4096 + 64 * 4));
+  CHECK(pq_w4a8_linear_workspace_size(65, 4096, 4096, 8) == 65 * 4096 + 65 * 4);
+  CHECK(pq_w4a8_linear_group_workspace_size(65, 4096, 3) == 3 * (65 * 4096 + 65 * 4));
   CHECK(pq_w4a16_linear_workspace_size(64, 4096) == 64 * 4096 * 2);
   CHECK(pq_w4a8_linear_split_path(1, 4096) == 1 && pq_w4a8_linear_split_path(16, 4096) == 1 &&
-        pq_w4a8_linear_split_path(33, 4096) == 0);
+        pq_w4a8_linear_split_path(64, 4096) == 1 && pq_w4a8_linear_split_path(65, 4096) == 0);
 
   /* a bad group size is refused on the host, with a message */
   void* p = (void*)(size_t)256;

@@ -77,12 +77,12 @@ def test_linear_argument_checks():
     assert lib.pq_w4a8_linear(*args(1, 4096, 8, 4, None, 0)) == 1
     assert lib.pq_w4a8_linear(*args(1, 32768, 8, 3, None, 0)) == 1
     assert lib.pq_w4a8_linear(*args(0, 4096, 8, 3, None, 0)) == 0
-    need = lib.pq_w4a8_linear_workspace_size(64, 4096, 4096, 8)
-    assert need == 64 * 4096 + 64 * 4
-    assert lib.pq_w4a8_linear(*args(64, 4096, 8, 3, None, 0)) == 4
+    need = lib.pq_w4a8_linear_workspace_size(65, 4096, 4096, 8)
+    assert need == 65 * 4096 + 65 * 4
+    assert lib.pq_w4a8_linear(*args(65, 4096, 8, 3, None, 0)) == 4
     assert "workspace" in _err(lib)
-    assert lib.pq_w4a8_linear(*args(64, 4096, 8, 3, p, need - 1)) == 4
-    assert lib.pq_w4a8_linear(*args(64, 4096, 8, 3, ctypes.c_void_p(272), need)) == 4   # not 256-aligned
+    assert lib.pq_w4a8_linear(*args(65, 4096, 8, 3, p, need - 1)) == 4
+    assert lib.pq_w4a8_linear(*args(65, 4096, 8, 3, ctypes.c_void_p(272), need)) == 4   # not 256-aligned
 
 
 def test_linear_group_argument_checks():
@@ -124,7 +124,7 @@ def test_workspace_size_rules():
     assert lib.pq_w4a8_linear_workspace_size(1, 4096, 12288, 16) == split(1, 12288)
     assert lib.pq_w4a8_linear_workspace_size(2, 4096, 4096, 8) == split(2, 4096)
     assert lib.pq_w4a8_linear_workspace_size(2, 4096, 12288, 8) == split(2, 12288)
-    # rows of k >= 4096 past that, up to 32 tokens: rotated rows and int8 codes, then group maxima
+    # rows of k >= 4096 past that, up to 64 tokens: rotated rows and int8 codes, then group maxima
     # and token scales
     def split3(m, k):
         return (m * k * 4 + 255) // 256 * 256 + (m * k + 255) // 256 * 256 + m * (k // 128) * 4 + m * 4
@@ -137,9 +137,11 @@ def test_workspace_size_rules():
     assert lib.pq_w4a8_linear_workspace_size(3, 4096, 4096, 8) == split3(3, 4096)
     assert lib.pq_w4a8_linear_workspace_size(17, 4096, 12288, 8) == split3(17, 12288)
     assert lib.pq_w4a8_linear_workspace_size(32, 4096, 4096, 8) == split3(32, 4096)
+    assert lib.pq_w4a8_linear_workspace_size(33, 4096, 12288, 8) == split3(33, 12288)
+    assert lib.pq_w4a8_linear_workspace_size(64, 4096, 4096, 8) == split3(64, 4096)
     # otherwise the row path holds xq and xscale
-    assert lib.pq_w4a8_linear_workspace_size(33, 4096, 12288, 8) == 33 * 12288 + 132
-    assert lib.pq_w4a8_linear_workspace_size(33, 4096, 4096, 8) == 33 * 4096 + 132
+    assert lib.pq_w4a8_linear_workspace_size(65, 4096, 12288, 8) == 65 * 12288 + 260
+    assert lib.pq_w4a8_linear_workspace_size(65, 4096, 4096, 8) == 65 * 4096 + 260
     assert lib.pq_w4a8_linear_workspace_size(5, 4096, 2048, 8) == 5 * 2048 + 20
     assert lib.pq_w4a8_linear_workspace_size(3, 64, 100, 8) == 0       # invalid shape -> 0
 
@@ -276,9 +278,12 @@ def test_split_path_rule():
     assert lib.pq_w4a8_linear_split_path(16, 8192) == 1
     assert lib.pq_w4a8_linear_split_path(17, 12288) == 1
     assert lib.pq_w4a8_linear_split_path(32, 16384) == 1
-    assert lib.pq_w4a8_linear_split_path(33, 12288) == 0
+    assert lib.pq_w4a8_linear_split_path(33, 12288) == 1
+    assert lib.pq_w4a8_linear_split_path(64, 16384) == 1
+    assert lib.pq_w4a8_linear_split_path(65, 12288) == 0
     assert lib.pq_w4a8_linear_split_path(16, 4096) == 1
-    assert lib.pq_w4a8_linear_split_path(33, 4096) == 0
+    assert lib.pq_w4a8_linear_split_path(64, 4096) == 1
+    assert lib.pq_w4a8_linear_split_path(65, 4096) == 0
     assert lib.pq_w4a8_linear_split_path(2, 4096) == 1
     assert lib.pq_w4a8_linear_split_path(4, 6144) == 1
     assert lib.pq_w4a8_linear_split_path(3, 3968) == 0
@@ -352,7 +357,7 @@ def test_split_path_python_rule_matches_library():
 
     lib = _lib.load()
     for k in range(128, 16384 + 1, 128):
-        for m in list(range(0, 40)) + [63, 64, 96, 1000, 3072]:
+        for m in list(range(0, 40)) + [47, 48, 63, 64, 65, 96, 1000, 3072]:
             assert ops.split_path(m, k) == bool(lib.pq_w4a8_linear_split_path(m, k)), (m, k)
     assert ops.split_path(1, 16384 + 128) == bool(lib.pq_w4a8_linear_split_path(1, 16384 + 128))
     # depths that are not a multiple of 128 take neither split path, in either form

@@ -44,8 +44,8 @@ SHAPES = [(1, 16, 128), (3, 64, 256), (16, 1024, 4096), (4, 4096, 4096), (1, 102
           (33, 48, 256), (130, 256, 512), (257, 384, 1024), (64, 1024, 12288), (200, 1552, 384),
           # decode GEMM with two column tiles per workgroup: 384 tiles (between one and two rounds of one)
           (8, 6144, 1024),
-          # decode GEMM on two row blocks of 16 (17-32 rows), one and two column tiles per workgroup
-          (32, 4096, 1024), (24, 6144, 512)]
+          # decode GEMM on two to four row blocks of 16 (17-64 rows), one and two column tiles per workgroup
+          (32, 4096, 1024), (24, 6144, 512), (40, 6144, 1024), (64, 4096, 4096), (49, 1024, 12288)]
 # prefill tiling: 192 x 256 workgroup tiles once there are >= 256 of them, else 128 x 256 when 128-256 of
 # those, else 128 x 128 or 64 x 128.
 # These reach the big tiles with an odd group count, ragged M and a partial last column tile.

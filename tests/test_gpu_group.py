@@ -86,11 +86,11 @@ def test_group_matches_oracle_and_single_calls(M, K, ns, krot, flags):
         assert_bf16_close(to_np(y), _oracle(mb, x_np, flags))
         single = torch.ops.paroquant.w4a8_linear(xc, mb["rot_idx"], mb["rot_cs"], mb["scales"], krot, mb["wp"],
                                                  mb["wm"], mb["bias"], flags[0], flags[1], torch.bfloat16)
-        if M > 32:
+        if M > 64:
             # same rotate+quant rows, and the prefill tiles accumulate every output element in the same order
             assert torch.equal(y, single)
         else:
-            # the decode GEMM (up to 32 rows on int8 A) may split K over a different number of waves for the
+            # the decode GEMM (up to 64 rows on int8 A) may split K over a different number of waves for the
             # group
             torch.testing.assert_close(y.float(), single.float(), rtol=2 ** -7, atol=1e-3)
 

@@ -1,13 +1,14 @@
 """Parity of what the production W4A8 linear paths multiply (pq_w4a8_linear_group_intermediates).
 
 The linear entry points pick one of three launch sequences by token count and row length: the split pair
-(split rotation, then a decode GEMM that derives the token scales and int8 codes in its prologue, into LDS),
+(split rotation, then a decode GEMM that derives the token scales and int8 codes itself: in registers at one
+and two tokens, into LDS otherwise),
 the three-launch long-row path (split rotation, quant_split_kernel, decode GEMM on int8 A) and the row
-rotate+quant kernel followed by the decode GEMM (up to 32 rows) or the prefill GEMM (tile-pair form on its big
+rotate+quant kernel followed by the decode GEMM (up to 64 rows) or the prefill GEMM (tile-pair form on its big
 tiles).  The intermediates entry point runs the same launches with the GEMM in its partials form and returns the
 int8 codes and token scales that GEMM used and its int32 per-group partials.  Checked here, against the oracle,
 for every path, every prologue (none, RMSNorm, residual add, SwiGLU), single linears and groups, on the
-Qwen3-8B decoder-layer shapes at 1-32 tokens and at prefill sizes:
+Qwen3-8B decoder-layer shapes at 1-64 tokens and at prefill sizes:
 
   - int8 codes: >= 99.9 % identical to the oracle's per-token quantization (vLLM scaled_int8_quant semantics,
     as invoked before the Marlin GEMM at paroquant_marlin_w4a8.py:319-333) of the oracle's rotation of the
@@ -70,7 +71,7 @@ def _run(mbs, x, krot, flags, **kw):
         [m["wp"] for m in mbs], [m["wm"] for m in mbs], flags[0], flags[1], **kw)
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 16, 17, 32])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 16, 17, 32, 33, 48, 64])
 @pytest.mark.parametrize("layout", list(LAYOUTS))
 def test_plain_group_intermediates(M, layout):
     K, ns = LAYOUTS[layout]
