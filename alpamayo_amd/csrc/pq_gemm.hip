@@ -23,13 +23,14 @@
 // two more MFMAs against bytes of -z, which adds -z * sum_k a exactly.
 //
 // Two kernels:
-//   gemm_skinny  M <= 32: each wave streams 1 KB weight blocks (one 16-column
+//   gemm_skinny  M <= 64: each wave streams 1 KB weight blocks (one 16-column
 //                tile x one 128-group) with 16-byte loads, four
 //                v_mfma_i32_16x16x64_i8 per block (activation rows padded to
-//                16; 17-32 rows on int8 A run as two row blocks of 16); the
+//                16; 17-64 rows on int8 A run as two to four row blocks of 16
+//                in every workgroup, so the weights stream once); the
 //                waves of a workgroup split K and add their partial sums in
 //                LDS in a fixed order.
-//   gemm_prefill M > 32: 192x256, 128x256, 128x128, 64x128 or 32x128 output
+//   gemm_prefill M > 64: 192x256, 128x256, 128x128, 64x128 or 32x128 output
 //                tiles (by the measured cost of rounds of 256 workgroups), 8 (or 4) waves
 //                side by side along n, operands copied from global memory
 //                straight into a 3-stage LDS ring, v_mfma_i32_32x32x32_i8
