@@ -47,7 +47,7 @@ using namespace pqd;
 namespace {
 
 // ---------------------------------------------------------------------------
-// Decode-size GEMM (M <= 16 per launch row block; int8 A up to 32 rows)
+// Decode-size GEMM (M <= 16 per launch row block; int8 A up to 64 rows)
 //
 // Workgroup = W waves over NT 16-column tiles; wave w takes the groups
 // w, w+W, w+2W, ... of K and issues the 16-byte loads of U groups at once.

@@ -100,7 +100,7 @@ def test_unrounded_rows_intermediates(M, K, ns):
     _check(mbs, to_np(x), codes, xscale, parts, flags)
 
 
-@pytest.mark.parametrize("M", [1, 2, 4, 16, 32])
+@pytest.mark.parametrize("M", [1, 2, 4, 16, 32, 48, 64])
 @pytest.mark.parametrize("layout", ["qkv", "gateup"])
 def test_rmsnorm_prologue_intermediates(M, layout):
     K, ns = LAYOUTS[layout]
@@ -117,7 +117,8 @@ def test_rmsnorm_prologue_intermediates(M, layout):
     _check(mbs, to_np(h), codes, xscale, parts, flags)
 
 
-@pytest.mark.parametrize("M,K,ns", [(4, 8192, (1024,)), (17, 12288, (4096,)), (13, 8192, (1024, 64))])
+@pytest.mark.parametrize("M,K,ns", [(4, 8192, (1024,)), (17, 12288, (4096,)), (13, 8192, (1024, 64)),
+                                   (40, 12288, (4096,)), (64, 8192, (1024, 64))])
 def test_rmsnorm_prologue_long_rows(M, K, ns):
     """The RMSNorm prologue on the three-launch long-row path."""
     print(f"intermediates rmsnorm long rows M={M} K={K} ns={ns}", flush=True)
@@ -132,7 +133,7 @@ def test_rmsnorm_prologue_long_rows(M, K, ns):
     _check(mbs, to_np(h), codes, xscale, parts, flags)
 
 
-@pytest.mark.parametrize("M", [1, 2, 4, 16, 32])
+@pytest.mark.parametrize("M", [1, 2, 4, 16, 32, 48, 64])
 def test_add_prologue_intermediates(M):
     K, ns = LAYOUTS["qkv"]
     print(f"intermediates add qkv M={M}", flush=True)
@@ -147,9 +148,10 @@ def test_add_prologue_intermediates(M):
 
 
 @pytest.mark.parametrize("M,K", [(1, 12288), (2, 12288), (3, 12288), (16, 12288), (17, 12288), (24, 12288),
-                                 (32, 12288), (32, 16384), (2, 4096), (16, 4096), (1, 16384), (1, 8320)])
+                                 (32, 12288), (32, 16384), (2, 4096), (16, 4096), (1, 16384), (1, 8320),
+                                 (48, 12288), (64, 12288)])
 def test_swiglu_prologue_intermediates(M, K):
-    """down_proj's input silu(gate) * up: the split pair, the long-row path up to 32 tokens, the row path.
+    """down_proj's input silu(gate) * up: the split pair, the long-row path up to 64 tokens, the row path.
     At one token the GEMM quantizes A in registers: K = 16384 takes all 128 group maxima, K = 8320 (65
     groups) leaves the last batch part past K."""
     ns = (4096,)

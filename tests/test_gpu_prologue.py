@@ -22,8 +22,8 @@ pytestmark = pytest.mark.gpu
 
 CASES = [
     # (M, K, member Ns): the split pair (M*K <= 8192, or M <= 2 for K >= 8192), the three-launch
-    # path (K >= 4096 up to 32 tokens), the row rotate+quant path (short rows at a few tokens, and
-    # from 33 tokens), ragged row counts
+    # path (K >= 4096 up to 64 tokens), the row rotate+quant path (short rows at a few tokens, and
+    # from 65 tokens), ragged row counts
     (1, 4096, (4096, 1024, 1024)),
     (1, 12288, (4096,)),
     (3, 12288, (4096,)),
@@ -33,6 +33,9 @@ CASES = [
     (17, 12288, (4096,)),
     (24, 12288, (1024, 48)),
     (32, 16384, (4096,)),
+    (48, 4096, (4096, 1024, 1024)),
+    (64, 12288, (4096,)),
+    (65, 4096, (1024, 64)),
     (300, 4096, (4096, 1024)),
     (1029, 2048, (1040, 16)),
     (6, 2048, (1024, 64)),
