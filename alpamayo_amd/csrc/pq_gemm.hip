@@ -467,7 +467,7 @@ __global__ __launch_bounds__(W * 64, (W == 4 && NT == 1 && !PARTIALS) ? 3 : 1) v
 }
 
 // ---------------------------------------------------------------------------
-// Prefill-size GEMM (M > 16)
+// Prefill-size GEMM (M > 64)
 //
 // Workgroup tile BM x BN; WM x WN waves, each a (BM/WM) x (BN/WN) block of
 // TM x TN 32 x 32 tiles (v_mfma_i32_32x32x32_i8).  The operands of one K
@@ -902,8 +902,8 @@ void launch_prefill(const pq::GemmGroup& grp, int bias_dtype, int y_dtype, int M
   } else if (static_cast<int64_t>((M + 127) / 128) * bn128 >= 256)
     launch_prefill_t<128, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, M, K, stream);
   else if (static_cast<int64_t>((M + 31) / 32) * bn128 <= 256)
-    // at most one round of 32-row tiles (33-256 tokens at N = 4096; up to
-    // 32 the decode kernel runs them): each workgroup walks all of K, so its
+    // at most one round of 32-row tiles (65-256 tokens at N = 4096; up to
+    // 64 the decode kernel runs them): each workgroup walks all of K, so its
     // time follows its rows (25 -> 19 us at K = 4096, 65 -> 49.5 us at
     // K = 12288 against 64 x 128)
     launch_prefill_t<32, 128, 1, 4, PARTIALS>(grp, bias_dtype, y_dtype, M, K, stream);
